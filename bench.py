@@ -1,0 +1,227 @@
+"""Benchmark: minidist's grad-bucket pipeline on one MI355X (BASELINE cfg1).
+
+One step = the per-rank gradient-communication path over GPT-2-124M's fp32
+gradients with W = 8 data-parallel replicas resident in HBM (rank 0 live,
+peers' packed contributions staged before timing), 25 MB buckets in reverse
+parameter order, loss scale 2^16:
+
+    DistributedDataParallel.finish_gradient_sync()
+        pack + 1/W       -> mdx_pack             (every bucket, one dispatch per 48 spans)
+        W-way SUM        -> mdx_allreduce_sum    (every bucket, one dispatch)
+        unpack + unscale + found-inf -> mdx_unpack (fused scaler epilogue)
+    DistributedGradScaler.unscale_(opt) -> flag.item()  (the path's one host sync)
+    DistributedGradScaler.update()
+
+value = algorithmic bytes of the staged pipeline, 52*N (pack 8N, W-way 36N,
+unpack 8N for fp32, W = 8), divided by the measured step time.  The roofline
+object is for the dominant kernel, the W-way reduction: (W+1)*N*4 bytes per
+dispatch over its HIP-event time measured on its own stream inside the timed
+steps.  The CPU baseline (reference op chain on torch CPU + gloo, W processes)
+runs first, before anything touches the GPU.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "distributed-training-framework_amd"))
+
+METRIC = "grad-bucket pipeline HBM GB/s (% of 8 TB/s) GPT-2-124M W=8; ms/step"
+HBM_PEAK_GBS = 8000.0
+W = 8
+CAP_MB = 25.0
+LOSS_SCALE = 2.0**16
+
+
+def cpu_baseline(steps: int, threads: int) -> dict | None:
+    """Time the reference's CPU path (oracle/gloo_path.py) in a child process."""
+    cmd = [sys.executable, "-m", "oracle.gloo_path", "--world", str(W), "--steps", str(steps),
+           "--warmup", "1", "--threads", str(threads)]
+    res = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+    if res.returncode != 0:
+        print(res.stderr[-2000:], file=sys.stderr, flush=True)
+        return None
+    line = [ln for ln in res.stdout.splitlines() if ln.startswith("{")][-1]
+    return json.loads(line)
+
+
+def host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: this build emulates the W={W} data-parallel replicas on a single "
+            f"MI355X (no inter-GPU collectives), so --gpus {args.gpus} is not supported",
+            file=sys.stderr,
+        )
+        return 2
+
+    # ---- CPU baseline first: nothing has touched the GPU yet ------------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        cores = max(W, min(16, host_cores()))
+        threads = max(1, cores // W)
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(args.cpu_steps, threads)
+        print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
+
+    import torch
+    from torch import nn
+
+    from minidist import DDP, DistributedGradScaler, ResidentGroup
+    from minidist import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    specs = wl.gpt_specs(**wl.GPT2_SMALL)
+    N = wl.total_numel(specs)
+
+    class Params(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ps = nn.ParameterList([nn.Parameter(torch.zeros(s.shape, device=dev)) for s in specs])
+
+    model = Params()
+    scaler = DistributedGradScaler(init_scale=LOSS_SCALE)
+    group = ResidentGroup(W, 0, dev)
+    ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+    ddp.allocate_buckets()
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    for p in model.parameters():
+        p.grad = torch.randn(p.shape, device=dev, generator=gen) * (1e-3 * LOSS_SCALE)
+    for b in range(len(ddp._buckets)):
+        rows = ddp.bucket_replicas(b)
+        for r in range(1, W):
+            rows[r].copy_(torch.randn(rows[r].shape, device=dev, generator=gen) * (1e-3 * LOSS_SCALE / W))
+
+    class _Opt:  # the scaler only reads param_groups
+        param_groups = [{"params": list(model.parameters())}]
+
+    opt = _Opt()
+
+    # Dominant kernel timing: HIP events around the W-way reduction dispatch,
+    # recorded on the stream it is launched on.
+    red_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+    timing = {"on": False}
+    orig = ResidentGroup.all_reduce_sum
+
+    def timed_all_reduce(self, tensors, async_op=False):
+        if not timing["on"]:
+            return orig(self, tensors, async_op)
+        s = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        work = orig(self, tensors, async_op)
+        e1.record(s)
+        red_events.append((e0, e1))
+        return work
+
+    ResidentGroup.all_reduce_sum = timed_all_reduce
+
+    def step() -> bool:
+        ddp.finish_gradient_sync()
+        found = scaler.unscale_(opt)
+        scaler.update()
+        return found
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timing["on"] = True
+    t0 = time.perf_counter()
+    found_any = False
+    for _ in range(args.steps):
+        found_any |= step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timing["on"] = False
+    ResidentGroup.all_reduce_sum = orig
+
+    ms_per_step = elapsed / args.steps * 1e3
+    alg_bytes = 52 * N  # pack 8N + W-way (W+1)*4N + unpack 8N, fp32, W = 8
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
+    red_avg_ms = sum(red_ms) / len(red_ms)
+    red_bytes = (W + 1) * N * 4
+    red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
+
+    traffic = None
+    tfile = ROOT / "profiles" / "allreduce_sum_gpt2_124m_w8_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded randn grads x 2^16 loss scale; peers' contributions staged in HBM)",
+        "config": {
+            "workload": "cfg1: GPT-2-124M fp32 grads (148 tensors, N=124,439,808), W=8 replicas on one GPU, "
+                        "25 MB buckets in reverse parameter order (18 buckets), loss scale 2^16",
+            "world": W,
+            "numel": N,
+            "buckets": len(ddp._buckets),
+            "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "found_inf": bool(found_any),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mdx reduce_kernel<float,float,float,8> (mdx_allreduce_sum, all 18 buckets per dispatch)",
+            "achieved": round(red_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(red_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": red_bytes,
+            "avg_launch_ms": round(red_avg_ms, 4),
+        },
+        "cpu_baseline": None,
+    }
+    if cpu is not None:
+        cpu_gbs = alg_bytes / (cpu["median_ms"] * 1e-3) / 1e9
+        out["cpu_baseline"] = {
+            "value": round(cpu_gbs, 3),
+            "unit": "GB/s",
+            "cores": cpu["cores"],
+            "kind": "port",
+            "sample": f"{cpu['steps']} timed steps (+1 warmup) of the full cfg1 pipeline, reference op chain on "
+                      f"torch CPU + gloo, {W} processes x {cpu['threads_per_rank']} threads; "
+                      f"median {cpu['median_ms']:.1f} ms/step",
+            "ms_per_step": round(cpu["median_ms"], 2),
+            "speedup": round(cpu["median_ms"] / ms_per_step, 1),
+        }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

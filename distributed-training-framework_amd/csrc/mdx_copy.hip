@@ -1,0 +1,127 @@
+// Multi-tensor copy / convert / scale kernel: the pack, unpack (+ fused
+// unscale and found-inf), in-place unscale and fp32->bf16 cast entry points
+// all run this one kernel with different dtype pairs and flags.
+//
+// Per element:  v = cvt_dst(src);  if (scale) v = rnd_dst(f32(v) * scale)
+//                                  (or / scale for the FSDP pre-division);
+//               dst = v;           if (check) bad |= !isfinite(v)
+// which is `dst.copy_(src)` followed by `dst.mul_(scale)` in ATen's op order.
+//
+// Layout of the work: each span is cut into chunks of kBlock * U fragments
+// (a fragment = E elements = one or two 16-byte vectors).  Lane t of chunk c
+// handles fragments c*VPB + u*kBlock + t, so every vector instruction of a
+// wave touches 64 consecutive 16-byte vectors.  A span whose src and dst
+// cannot both be brought to 16-byte alignment by the same element offset is
+// processed with coalesced scalar accesses instead.
+#include "mdx_internal.h"
+
+namespace mdx {
+namespace {
+
+template <typename S, typename D>
+struct CopyOp {
+  float scale;
+  int32_t flags;
+  __device__ __forceinline__ D operator()(S x, bool& bad) const {
+    D v = Cvt<S, D>::run(x);
+    if (flags & kCopyScale) v = from_f32<D>(to_f32(v) * scale);
+    if (flags & kCopyDivide) v = from_f32<D>(to_f32(v) / scale);
+    if (flags & kCopyCheck) bad |= !is_finite(v);
+    return v;
+  }
+};
+
+template <typename S, typename D>
+__global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p) {
+  constexpr int E = frag_elems(int(sizeof(S)), int(sizeof(D)));
+  constexpr int U = kCopyElemsPerThread / E;
+  constexpr int VPB = kBlock * U;
+  constexpr int EPB = kBlock * kCopyElemsPerThread;
+
+  const int blk = int(blockIdx.x);
+  const int s = find_run(b.first_block, b.count, blk);
+  const int c = blk - b.first_block[s];
+  const int nblk = b.first_block[s + 1] - b.first_block[s];
+  const S* src = static_cast<const S*>(b.src[s]);
+  D* dst = static_cast<D*>(b.dst[s]);
+  const int64_t n = b.numel[s];
+  const int32_t h = b.head[s];
+  const int t = int(threadIdx.x);
+  const bool zero_src = (src == nullptr);
+  const CopyOp<S, D> op{p.scale, p.flags};
+  bool bad = false;
+
+  if (h >= 0) {
+    const int64_t nvec = (n - h) / E;
+    const S* vs = src + h;
+    D* vd = dst + h;
+    S in[U][E];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if (v < nvec) {
+        if (zero_src) {
+#pragma unroll
+          for (int k = 0; k < E; ++k) in[u][k] = zero_of<S>();
+        } else {
+          vload<S, E, true>(in[u], vs + v * E);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if (v < nvec) {
+        D out[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) out[k] = op(in[u][k], bad);
+        vstore<D, E, false>(vd + v * E, out);
+      }
+    }
+    // Ragged edges: the head before the aligned body (first chunk) and the
+    // tail after it (last chunk), one element per lane.
+    if (c == 0 && t < h && t < n) {
+      const S x = zero_src ? zero_of<S>() : src[t];
+      dst[t] = op(x, bad);
+    }
+    const int64_t tail0 = h + nvec * E;
+    if (c == nblk - 1 && tail0 + t < n) {
+      const int64_t i = tail0 + t;
+      const S x = zero_src ? zero_of<S>() : src[i];
+      dst[i] = op(x, bad);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kCopyElemsPerThread; ++k) {
+      const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
+      if (i < n) {
+        const S x = zero_src ? zero_of<S>() : src[i];
+        dst[i] = op(x, bad);
+      }
+    }
+  }
+  if (p.flags & kCopyCheck) flag_nonfinite(bad, p.found_inf);
+}
+
+template <typename S, typename D>
+hipError_t launch_typed(const SpanBatch& b, const CopyParams& p, hipStream_t stream) {
+  const int blocks = b.first_block[b.count];
+  hipLaunchKernelGGL((copy_kernel<S, D>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int copy_frag_elems(int src_dtype, int dst_dtype) {
+  return frag_elems(dtype_size(src_dtype), dtype_size(dst_dtype));
+}
+
+hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
+                       hipStream_t stream) {
+  if (src_dtype == MDX_F32 && dst_dtype == MDX_F32) return launch_typed<float, float>(b, p, stream);
+  if (src_dtype == MDX_F32 && dst_dtype == MDX_BF16) return launch_typed<float, bf16>(b, p, stream);
+  if (src_dtype == MDX_BF16 && dst_dtype == MDX_F32) return launch_typed<bf16, float>(b, p, stream);
+  return launch_typed<bf16, bf16>(b, p, stream);
+}
+
+}  // namespace mdx

@@ -1,0 +1,213 @@
+// Internal declarations shared by the libmdx translation units.
+//
+// Work tables travel in the kernel-argument segment of each dispatch: the
+// host packs up to kRunsPerLaunch runs (spans or pieces) into one struct
+// passed by value; a workgroup finds its run by a binary search over
+// `first_block`, which the compiler reads with scalar loads because the index
+// is wave-uniform.  Runs are split on the host so that no run needs more than
+// kMaxRunElems elements, which keeps every grid far below 2^32 work-items.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mdx.h"
+
+#pragma clang fp contract(off)
+
+namespace mdx {
+
+constexpr int kBlock = 256;               // 4 wave64 per workgroup
+constexpr int kRunsPerLaunch = 48;        // runs per dispatch (kernarg budget)
+constexpr int64_t kMaxRunElems = int64_t(1) << 26;
+
+// bf16 storage type: raw bits, so that conversions are exact and explicit.
+struct bf16 {
+  uint16_t u;
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ----------------------------------------------------------------------------
+// Element conversions (IEEE, round to nearest even, NaN -> 0xFFFF for bf16)
+// ----------------------------------------------------------------------------
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return __uint_as_float(uint32_t(x.u) << 16); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) {
+  return x;
+}
+
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) {
+  uint32_t u = __float_as_uint(x);
+  bf16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.u = 0xffffu;
+  } else {
+    r.u = uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+  return r;
+}
+
+// `dst.copy_(src)` for one element: identity within a dtype (NaN payloads
+// untouched), one rounding across dtypes.
+template <typename S, typename D>
+struct Cvt {
+  __device__ __forceinline__ static D run(S x) { return from_f32<D>(to_f32(x)); }
+};
+template <typename T>
+struct Cvt<T, T> {
+  __device__ __forceinline__ static T run(T x) { return x; }
+};
+
+__device__ __forceinline__ bool is_finite(float x) { return __builtin_isfinite(x); }
+__device__ __forceinline__ bool is_finite(bf16 x) { return (x.u & 0x7f80u) != 0x7f80u; }
+
+template <typename T>
+__device__ __forceinline__ T zero_of() {
+  T z;
+  __builtin_memset(&z, 0, sizeof(T));
+  return z;
+}
+
+// ----------------------------------------------------------------------------
+// 16-byte vector loads and stores of E elements
+// ----------------------------------------------------------------------------
+
+template <typename T, int E, bool NT>
+__device__ __forceinline__ void vload(T (&dst)[E], const T* p) {
+  static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
+  constexpr int NV = int(E * sizeof(T) / 16);
+  constexpr int PER = int(16 / sizeof(T));
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    u32x4 w;
+    if constexpr (NT) {
+      w = __builtin_nontemporal_load(q + k);
+    } else {
+      w = q[k];
+    }
+    __builtin_memcpy(&dst[k * PER], &w, 16);
+  }
+}
+
+template <typename T, int E, bool NT>
+__device__ __forceinline__ void vstore(T* p, const T (&src)[E]) {
+  static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
+  constexpr int NV = int(E * sizeof(T) / 16);
+  constexpr int PER = int(16 / sizeof(T));
+  u32x4* q = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    u32x4 w;
+    __builtin_memcpy(&w, &src[k * PER], 16);
+    if constexpr (NT) {
+      __builtin_nontemporal_store(w, q + k);
+    } else {
+      q[k] = w;
+    }
+  }
+}
+
+// Workgroup -> run lookup: largest s with first_block[s] <= blk.
+__device__ __forceinline__ int find_run(const int32_t* first_block, int count, int blk) {
+  int lo = 0, hi = count;
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (first_block[mid] <= blk) {
+      lo = mid;
+    } else {
+      hi = mid;
+    }
+  }
+  return lo;
+}
+
+// One wave stores 1 into *flag if any of its lanes saw a non-finite value.
+// Must be reached by every lane of the wave.
+__device__ __forceinline__ void flag_nonfinite(bool bad, int32_t* flag) {
+  if (__ballot(bad) != 0ull && (threadIdx.x & 63u) == 0u) {
+    *flag = 1;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Copy / convert / scale (pack, unpack, unscale, cast)
+// ----------------------------------------------------------------------------
+
+struct SpanBatch {
+  const void* src[kRunsPerLaunch];
+  void* dst[kRunsPerLaunch];
+  int64_t numel[kRunsPerLaunch];
+  int32_t head[kRunsPerLaunch];  // scalar elements before the 16B-aligned body; -1 = no body
+  int32_t first_block[kRunsPerLaunch + 1];
+  int32_t count;
+};
+
+enum : int32_t { kCopyScale = 1, kCopyCheck = 2, kCopyDivide = 4 };
+
+struct CopyParams {
+  float scale;
+  int32_t flags;
+  int32_t* found_inf;
+};
+
+// Elements per 16-byte-aligned fragment and per thread for a dtype pair.
+constexpr int frag_elems(int src_size, int dst_size) {
+  return 16 / (src_size < dst_size ? src_size : dst_size);
+}
+constexpr int kCopyElemsPerThread = 16;
+
+hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
+                       hipStream_t stream);
+int copy_frag_elems(int src_dtype, int dst_dtype);
+
+// ----------------------------------------------------------------------------
+// W-way reduction (all-reduce sum, reduce-scatter share)
+// ----------------------------------------------------------------------------
+
+struct PieceBatch {
+  const void* own[kRunsPerLaunch];
+  int64_t pos[kRunsPerLaunch];
+  int64_t numel[kRunsPerLaunch];
+  int32_t head[kRunsPerLaunch];
+  int32_t first_block[kRunsPerLaunch + 1];
+  int32_t count;
+};
+
+enum : int32_t {
+  kRedPreMul = 1,      // every contribution * pre, rounded to the reduce dtype
+  kRedPreDiv = 2,      // every contribution / pre, rounded to the reduce dtype
+  kRedAccumulate = 4,  // out = out + result (rounded to the out dtype)
+  kRedUnscale = 8,     // out value * inv_scale, rounded to the out dtype
+  kRedCheck = 16,      // found-inf on the stored value
+};
+
+struct ReduceParams {
+  const void* peer[MDX_MAX_WORLD];
+  void* out;
+  int32_t rank;
+  int32_t flags;
+  float pre;
+  float inv_scale;
+  int32_t* found_inf;
+};
+
+// Fragments kept in flight per lane and contribution: W * U 16-byte loads per
+// lane before the first add (16 for W = 8).
+constexpr int reduce_unroll(int world) { return world <= 4 ? 4 : (world <= 8 ? 2 : 1); }
+
+hipError_t launch_reduce(int in_dtype, int acc_dtype, int out_dtype, int world, const PieceBatch& b,
+                         const ReduceParams& p, hipStream_t stream);
+int reduce_frag_elems(int in_dtype, int out_dtype);
+
+inline int dtype_size(int dt) { return dt == MDX_BF16 ? 2 : 4; }
+
+}  // namespace mdx

@@ -1,0 +1,88 @@
+"""Build libmdx.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+
+Usage: ``python -m minidist._build`` or ``minidist._build.build_native()``.
+The library lands next to this file, where :mod:`minidist._native` loads it.
+Cross-compiles for gfx950 on a machine without a GPU.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+PROJECT_DIR = PKG_DIR.parent
+CSRC = PROJECT_DIR / "csrc"
+INCLUDE = PROJECT_DIR.parent / "include"
+BUILD_DIR = PROJECT_DIR / "_build"
+LIB_PATH = PKG_DIR / "libmdx.so"
+
+SOURCES = [
+    "mdx_api.hip",
+    "mdx_copy.hip",
+    "mdx_reduce.hip",
+    "mdx_reduce_f32.hip",
+    "mdx_reduce_bf16.hip",
+    "mdx_reduce_bf16_f32.hip",
+    "mdx_reduce_mixed.hip",
+]
+HEADERS = ["mdx_internal.h", "mdx_reduce_impl.h"]
+
+ARCH = "gfx950"
+
+# -ffp-contract=off: x*s + y must stay two roundings, as in the ATen chains.
+# -packed-fp32-ops off: no v_pk_* fp32 forms anywhere in this library.
+CXXFLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found: install ROCm or put hipcc on PATH")
+    return exe
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *CXXFLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build_native(jobs: int | None = None) -> Path:
+    """Compile every translation unit for gfx950 and link ``libmdx.so``."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of libmdx.so failed:\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_native())

@@ -1,0 +1,199 @@
+"""ctypes binding of libmdx.so (the C ABI in include/mdx.h).
+
+This is the only module that touches the native library.  Every kernel call
+goes through :func:`lib`, which raises when ``libmdx.so`` has not been built:
+there is no Python or CPU fallback for any kernel, so a missing library is a
+loud error, never a silently slower path.
+
+Span / piece tables are built as numpy structured arrays whose memory layout
+is the C structs ``mdx_span`` / ``mdx_piece``; the library copies them into
+each dispatch's kernel arguments, so they only have to live for the call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import numpy as np
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmdx.so"
+
+MDX_F32 = 0
+MDX_BF16 = 1
+MDX_MAX_WORLD = 16
+ABI_VERSION = 1
+
+# Every function declared in include/mdx.h, with (restype, argtypes).
+_vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+SIGNATURES: dict[str, tuple] = {
+    "mdx_pack": (_i32, [_vp, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "mdx_unpack": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _vp]),
+    "mdx_unscale_found_inf": (_i32, [_vp, _i32, _i32, _f32, _vp, _vp]),
+    "mdx_allreduce_sum": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "mdx_reduce_scatter_share": (
+        _i32,
+        [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
+    ),
+    "mdx_cast_f32_bf16": (_i32, [_vp, _vp, _i64, _vp]),
+    "mdx_strerror": (ctypes.c_char_p, [_i32]),
+    "mdx_abi_version": (_i32, []),
+}
+
+SPAN_DTYPE = np.dtype([("src", "<u8"), ("dst", "<u8"), ("numel", "<i8")])
+PIECE_DTYPE = np.dtype([("own", "<u8"), ("pos", "<i8"), ("numel", "<i8")])
+
+_lib: ctypes.CDLL | None = None
+_lock = threading.Lock()
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} is missing: build the gfx950 kernels with "
+                    "`python -m minidist._build` (there is no fallback path)"
+                )
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            if handle.mdx_abi_version() != ABI_VERSION:
+                raise NativeLibraryMissing(
+                    f"{LIB_PATH} has ABI {handle.mdx_abi_version()}, expected {ABI_VERSION}: rebuild it"
+                )
+            _lib = handle
+    return _lib
+
+
+def available() -> bool:
+    return LIB_PATH.exists()
+
+
+def strerror(code: int) -> str:
+    return lib().mdx_strerror(code).decode()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {strerror(rc)} (status {rc})")
+
+
+# ---------------------------------------------------------------------------
+# torch <-> ABI plumbing
+# ---------------------------------------------------------------------------
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return MDX_F32
+    if dtype == torch.bfloat16:
+        return MDX_BF16
+    raise TypeError(f"minidist kernels handle float32 and bfloat16, not {dtype}")
+
+
+def require_device_tensor(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"{what} lives on {t.device}; minidist's gradient path runs only as HIP kernels "
+            "on a GPU (there is no CPU implementation)"
+        )
+
+
+def require_dense(t: torch.Tensor, what: str) -> None:
+    if not t.is_contiguous():
+        raise RuntimeError(f"{what} must be contiguous for the flat-span kernels")
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def spans_array(rows: list[tuple[int, int, int]]) -> np.ndarray:
+    return np.array(rows, dtype=SPAN_DTYPE)
+
+
+def pieces_array(rows: list[tuple[int, int, int]]) -> np.ndarray:
+    return np.array(rows, dtype=PIECE_DTYPE)
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    return None if a is None or a.size == 0 else a.ctypes.data
+
+
+def _ptrs(values: list[int]) -> ctypes.Array:
+    return (ctypes.c_void_p * len(values))(*values)
+
+
+# ---------------------------------------------------------------------------
+# Entry points (thin: argument marshalling + status check)
+# ---------------------------------------------------------------------------
+
+
+def pack(spans: np.ndarray, src_dtype: int, dst_dtype: int, scale: float, divide: bool, stream: int) -> None:
+    rc = lib().mdx_pack(_ptr(spans), len(spans), src_dtype, dst_dtype, scale, int(divide), stream)
+    check(rc, "mdx_pack")
+
+
+def unpack(
+    spans: np.ndarray, src_dtype: int, dst_dtype: int, inv_scale: float, found_inf: int | None, stream: int
+) -> None:
+    rc = lib().mdx_unpack(_ptr(spans), len(spans), src_dtype, dst_dtype, inv_scale, found_inf, stream)
+    check(rc, "mdx_unpack")
+
+
+def unscale_found_inf(spans: np.ndarray, dtype: int, inv_scale: float, found_inf: int | None, stream: int) -> None:
+    rc = lib().mdx_unscale_found_inf(_ptr(spans), len(spans), dtype, inv_scale, found_inf, stream)
+    check(rc, "mdx_unscale_found_inf")
+
+
+def allreduce_sum(
+    replicas: list[int], dtype: int, offsets: list[int], numels: list[int], out: int, stream: int
+) -> None:
+    n = len(offsets)
+    offs = (ctypes.c_int64 * n)(*offsets)
+    nums = (ctypes.c_int64 * n)(*numels)
+    rc = lib().mdx_allreduce_sum(_ptrs(replicas), len(replicas), dtype, offs, nums, n, out, stream)
+    check(rc, "mdx_allreduce_sum")
+
+
+def reduce_scatter_share(
+    own: np.ndarray,
+    peers: list[int],
+    rank: int,
+    in_dtype: int,
+    reduce_dtype: int,
+    divide: bool,
+    shard: int,
+    shard_dtype: int,
+    accumulate: bool,
+    inv_scale: float,
+    found_inf: int | None,
+    stream: int,
+) -> None:
+    rc = lib().mdx_reduce_scatter_share(
+        _ptr(own), len(own), _ptrs(peers), len(peers), rank, in_dtype, reduce_dtype, int(divide),
+        shard, shard_dtype, int(accumulate), inv_scale, found_inf, stream,
+    )
+    check(rc, "mdx_reduce_scatter_share")
+
+
+def cast_f32_bf16(src: int, dst: int, numel: int, stream: int) -> None:
+    check(lib().mdx_cast_f32_bf16(src, dst, numel, stream), "mdx_cast_f32_bf16")
+
+
+def f32(x: float) -> float:
+    """The fp32 value a Python float becomes when ATen uses it as a scalar."""
+    return float(np.float32(x))

@@ -1,0 +1,254 @@
+"""Mixed precision and the collective grad scaler.
+
+Same surface and arithmetic as the reference's minidist/amp.py
+(``PrecisionConfig`` :61-81, ``resolve_precision`` :84-111,
+``DistributedGradScaler`` :114-267).  ``unscale_`` is where the data path
+changes: instead of ~6 ATen launches per gradient tensor (``mul_``,
+``isfinite``, ``~``, ``any``, ``to``, ``+=``, amp.py:208-213) it issues one
+multi-tensor ``mdx_unscale_found_inf`` dispatch per dtype, whose waves store
+a 1 into a device flag when they produce a non-finite value.  Gradients that
+a DDP wrapper already unscaled in its unpack epilogue (``grad_scaler=``) are
+skipped.  The flag is then all-reduced with MAX across a real process group
+and read back with one ``.item()`` -- the path's only host synchronisation,
+as in the reference (amp.py:216-219).
+"""
+
+from __future__ import annotations
+
+from contextlib import nullcontext
+from dataclasses import dataclass
+
+import torch
+import torch.distributed as dist
+
+from . import _native, comm
+
+__all__ = ["PrecisionConfig", "DistributedGradScaler", "resolve_precision"]
+
+
+@dataclass
+class PrecisionConfig:
+    """The precision decisions for one training run."""
+
+    dtype: torch.dtype
+    device_type: str
+    enabled: bool
+
+    @property
+    def needs_grad_scaler(self) -> bool:
+        return self.enabled and self.dtype == torch.float16
+
+    def autocast(self):
+        if not self.enabled:
+            return nullcontext()
+        return torch.autocast(device_type=self.device_type, dtype=self.dtype)
+
+    def __repr__(self) -> str:
+        if not self.enabled:
+            return "PrecisionConfig(fp32)"
+        return f"PrecisionConfig({str(self.dtype).replace('torch.', '')} autocast)"
+
+
+def resolve_precision(name: str, device: torch.device | None = None) -> PrecisionConfig:
+    """``'fp32' | 'fp16' | 'bf16' | 'auto'`` -> configuration (amp.py:84-111).
+
+    ``auto`` picks bf16 wherever the device supports it natively (every
+    MI355X does), which avoids loss scaling altogether.
+    """
+    device = device or comm.current_device()
+    device_type = device.type
+    if name == "auto":
+        if device_type == "cuda":
+            name = "bf16" if torch.cuda.is_bf16_supported() else "fp16"
+        else:
+            name = "bf16"
+    if name == "fp32":
+        return PrecisionConfig(torch.float32, device_type, enabled=False)
+    if name == "bf16":
+        return PrecisionConfig(torch.bfloat16, device_type, enabled=True)
+    if name == "fp16":
+        if device_type == "cpu":
+            raise ValueError("fp16 autocast is not useful on CPU; use bf16 or fp32")
+        return PrecisionConfig(torch.float16, device_type, enabled=True)
+    raise ValueError(f"unknown precision {name!r}")
+
+
+class DistributedGradScaler:
+    """Adaptive loss scaling whose skip/scale decisions are agreed across ranks.
+
+    Parameters and state follow the reference (amp.py:114-176).
+    ``process_group`` spans every rank holding a piece of the gradient; a
+    :class:`~minidist.comm.ResidentGroup` needs no flag exchange (this rank's
+    kernels saw every value that exists in this process).
+    """
+
+    def __init__(
+        self,
+        init_scale: float = 2.0**16,
+        growth_factor: float = 2.0,
+        backoff_factor: float = 0.5,
+        growth_interval: int = 2000,
+        enabled: bool = True,
+        process_group=None,
+        min_scale: float = 1.0,
+    ):
+        self.enabled = enabled
+        self.process_group = process_group
+        self._scale = float(init_scale)
+        self._growth_factor = growth_factor
+        self._backoff_factor = backoff_factor
+        self._growth_interval = growth_interval
+        self._min_scale = min_scale
+        self._good_steps = 0
+        self._found_inf_this_step = False
+        self._unscaled = False
+        self.num_skipped = 0
+        self.num_steps = 0
+        # Device-side found-inf flags (int32 [1] per device) and the flag's
+        # "zeroed for this step" marker; ids of params whose grads a fused
+        # producer (DDP unpack) already unscaled this step.
+        self._flags: dict[torch.device, torch.Tensor] = {}
+        self._flag_armed: set[torch.device] = set()
+        self._prescaled: set[int] = set()
+
+    # -- state --------------------------------------------------------------
+
+    @property
+    def scale(self) -> float:
+        return self._scale if self.enabled else 1.0
+
+    def state_dict(self) -> dict:
+        return {
+            "scale": self._scale,
+            "good_steps": self._good_steps,
+            "num_skipped": self.num_skipped,
+            "num_steps": self.num_steps,
+        }
+
+    def load_state_dict(self, state: dict) -> None:
+        self._scale = state["scale"]
+        self._good_steps = state["good_steps"]
+        self.num_skipped = state.get("num_skipped", 0)
+        self.num_steps = state.get("num_steps", 0)
+
+    # -- device flag ----------------------------------------------------------
+
+    def _flag(self, device: torch.device) -> torch.Tensor:
+        """This step's found-inf flag on ``device``, zeroed on first use in a step.
+
+        Cleared with a fill kernel (not a memset) so that the step can be
+        captured into a HIP graph."""
+        flag = self._flags.get(device)
+        if flag is None:
+            flag = torch.zeros(1, dtype=torch.int32, device=device)
+            self._flags[device] = flag
+            self._flag_armed.add(device)
+        elif device not in self._flag_armed:
+            flag.zero_()
+            self._flag_armed.add(device)
+        return flag
+
+    def _begin_fused_unscale(self, device: torch.device, params) -> tuple[float, torch.Tensor]:
+        """Hand a producer (DDP's unpack) the inverse scale and the device flag.
+
+        The producer writes these params' grads already multiplied by
+        ``1/scale`` and flags non-finite results; ``unscale_`` then skips them.
+        Gradients must not be accumulated on top of unscaled values, so a
+        second synchronised backward before ``step``/``update`` is an error."""
+        if self._unscaled:
+            raise RuntimeError("gradients were already unscaled this step; call update() first")
+        ids = {id(p) for p in params}
+        if ids & self._prescaled:
+            raise RuntimeError(
+                "a second synchronised backward ran before scaler.step()/update(): its gradients "
+                "would accumulate onto already-unscaled ones"
+            )
+        self._prescaled |= ids
+        return 1.0 / self._scale, self._flag(device)
+
+    # -- the training-loop surface -----------------------------------------
+
+    def scale_loss(self, loss: torch.Tensor) -> torch.Tensor:
+        if not self.enabled:
+            return loss
+        return loss * self._scale
+
+    scale_tensor = scale_loss
+
+    def unscale_(self, optimizer: torch.optim.Optimizer) -> bool:
+        """Divide gradients by the scale and detect overflow (amp.py:188-221).
+
+        Idempotent within a step.  Returns whether any rank found an inf/NaN.
+        """
+        if not self.enabled:
+            return False
+        if self._unscaled:
+            return self._found_inf_this_step
+
+        inv_scale = _native.f32(1.0 / self._scale)
+        device = comm.current_device()
+        flag = self._flag(device)
+
+        groups: dict[torch.dtype, list[tuple[int, int, int]]] = {}
+        for group in optimizer.param_groups:
+            for p in group["params"]:
+                g = p.grad
+                if g is None or id(p) in self._prescaled:
+                    continue
+                _native.require_device_tensor(g, "gradient")
+                if not g.is_contiguous():
+                    raise RuntimeError("unscale_: gradient is not contiguous")
+                groups.setdefault(g.dtype, []).append((g.data_ptr(), g.data_ptr(), g.numel()))
+        stream = _native.stream_of(flag.device)
+        for dtype, rows in groups.items():
+            _native.unscale_found_inf(
+                _native.spans_array(rows), _native.dtype_code(dtype), inv_scale, flag.data_ptr(), stream
+            )
+
+        # The collective that makes the decision unanimous under FSDP / TP.
+        if (
+            not isinstance(self.process_group, comm.ResidentGroup)
+            and comm.is_distributed()
+            and comm.get_world_size(self.process_group) > 1
+        ):
+            dist.all_reduce(flag, op=dist.ReduceOp.MAX, group=self.process_group)
+
+        self._found_inf_this_step = bool(flag.item() > 0)
+        self._unscaled = True
+        return self._found_inf_this_step
+
+    def step(self, optimizer: torch.optim.Optimizer) -> bool:
+        """Run ``optimizer.step()`` unless the group agreed an overflow occurred."""
+        self.num_steps += 1
+        if not self.enabled:
+            optimizer.step()
+            return True
+        found_inf = self.unscale_(optimizer)
+        if found_inf:
+            self.num_skipped += 1
+            return False
+        optimizer.step()
+        return True
+
+    def update(self) -> None:
+        """Adapt the scale, then reset per-step state (amp.py:240-258)."""
+        if not self.enabled:
+            return
+        if self._found_inf_this_step:
+            self._scale = max(self._min_scale, self._scale * self._backoff_factor)
+            self._good_steps = 0
+        else:
+            self._good_steps += 1
+            if self._good_steps >= self._growth_interval:
+                self._scale *= self._growth_factor
+                self._good_steps = 0
+        self._found_inf_this_step = False
+        self._unscaled = False
+        self._flag_armed.clear()
+        self._prescaled.clear()
+
+    def summary(self) -> str:
+        if not self.enabled:
+            return "grad scaler disabled (bf16 or fp32)"
+        pct = 100.0 * self.num_skipped / max(1, self.num_steps)
+        return f"scale={self._scale:g}  skipped={self.num_skipped}/{self.num_steps} ({pct:.1f}%)"

@@ -1,0 +1,467 @@
+"""Process-group bootstrap, instrumented collectives, and the resident replica group.
+
+Public surface and byte accounting follow minidist/comm.py of the reference
+(``CommStats`` :50-99, ``record_comm`` :105-113, bootstrap :121-202, the
+collective wrappers :223-277), so callers and the accounting formulas are
+unchanged.  What changes is what sits under the collective hook:
+
+* With a real ``torch.distributed`` group the wrappers forward to
+  ``dist.*`` exactly as the reference does (RCCL on ROCm devices).
+* With a :class:`ResidentGroup` -- W data-parallel replicas emulated on ONE
+  GPU -- the peers' contributions are already resident in this GPU's HBM
+  (symmetric buffers, one row per replica) and the reduction arithmetic runs
+  as a gfx950 kernel over them, in the fixed rank order 0..W-1.  The call
+  returns a Work whose ``wait()`` orders the caller's stream after the kernel;
+  nothing synchronises the host.
+"""
+
+from __future__ import annotations
+
+import os
+from collections.abc import Iterator, Sequence
+from contextlib import contextmanager
+from dataclasses import dataclass, field
+from datetime import timedelta
+
+import torch
+import torch.distributed as dist
+
+from . import _native
+
+__all__ = [
+    "CommStats",
+    "comm_stats",
+    "record_comm",
+    "init_distributed",
+    "shutdown_distributed",
+    "current_device",
+    "is_distributed",
+    "get_rank",
+    "get_world_size",
+    "is_primary",
+    "barrier",
+    "all_reduce",
+    "all_reduce_coalesced",
+    "all_gather_into_tensor",
+    "reduce_scatter_tensor",
+    "broadcast",
+    "print_rank0",
+    "ResidentGroup",
+    "zeros_for_collective",
+]
+
+
+# --------------------------------------------------------------------------
+# Byte accounting (reference comm.py:50-113, same formulas)
+# --------------------------------------------------------------------------
+
+
+@dataclass
+class _OpStat:
+    count: int = 0
+    payload_bytes: int = 0
+    bus_bytes: int = 0
+
+
+@dataclass
+class CommStats:
+    """Per-collective counters: ``payload_bytes`` (caller's tensor) and
+    ``bus_bytes`` (ring-algorithm interconnect volume): all-reduce
+    ``2(W-1)/W*N``, all-gather ``(W-1)/W*N_out``, reduce-scatter
+    ``(W-1)/W*N_in``, broadcast ``N``."""
+
+    enabled: bool = False
+    ops: dict[str, _OpStat] = field(default_factory=dict)
+
+    def add(self, op: str, payload_bytes: int, bus_bytes: int) -> None:
+        if not self.enabled:
+            return
+        stat = self.ops.setdefault(op, _OpStat())
+        stat.count += 1
+        stat.payload_bytes += payload_bytes
+        stat.bus_bytes += bus_bytes
+
+    def reset(self) -> None:
+        self.ops.clear()
+
+    def total_bus_bytes(self) -> int:
+        return sum(s.bus_bytes for s in self.ops.values())
+
+    def as_rows(self) -> list[tuple[str, int, int, int]]:
+        return sorted((name, s.count, s.payload_bytes, s.bus_bytes) for name, s in self.ops.items())
+
+
+comm_stats = CommStats()
+
+
+@contextmanager
+def record_comm() -> Iterator[CommStats]:
+    """Enable byte accounting for the duration of the block."""
+    previous, comm_stats.enabled = comm_stats.enabled, True
+    comm_stats.reset()
+    try:
+        yield comm_stats
+    finally:
+        comm_stats.enabled = previous
+
+
+# --------------------------------------------------------------------------
+# Bootstrap (reference comm.py:121-202)
+# --------------------------------------------------------------------------
+
+
+def _default_backend() -> str:
+    if torch.cuda.is_available() and dist.is_nccl_available():
+        return "nccl"  # RCCL on ROCm
+    return "gloo"
+
+
+def init_distributed(backend: str | None = None, timeout_seconds: int = 1800) -> tuple[int, int, torch.device]:
+    """Initialise the default process group from torchrun's environment.
+
+    Falls back to a single-rank world without torchrun.  Binds the device
+    before RCCL initialises (the communicator derives its topology from it).
+    """
+    if dist.is_initialized():
+        return get_rank(), get_world_size(), current_device()
+    rank = int(os.environ.get("RANK", 0))
+    world_size = int(os.environ.get("WORLD_SIZE", 1))
+    local_rank = int(os.environ.get("LOCAL_RANK", 0))
+    backend = backend or _default_backend()
+    if backend == "nccl":
+        if not torch.cuda.is_available():
+            raise RuntimeError("backend='nccl' requested but no GPU is available")
+        torch.cuda.set_device(local_rank)
+    os.environ.setdefault("MASTER_ADDR", "127.0.0.1")
+    os.environ.setdefault("MASTER_PORT", "29500")
+    dist.init_process_group(
+        backend=backend, rank=rank, world_size=world_size, timeout=timedelta(seconds=timeout_seconds)
+    )
+    return rank, world_size, current_device()
+
+
+def shutdown_distributed() -> None:
+    if dist.is_initialized():
+        dist.barrier()
+        dist.destroy_process_group()
+
+
+def current_device() -> torch.device:
+    if torch.cuda.is_available():
+        return torch.device("cuda", torch.cuda.current_device())
+    return torch.device("cpu")
+
+
+def is_distributed() -> bool:
+    return dist.is_available() and dist.is_initialized()
+
+
+def get_rank(group=None) -> int:
+    if isinstance(group, ResidentGroup):
+        return group.rank()
+    return dist.get_rank(group) if is_distributed() else 0
+
+
+def get_world_size(group=None) -> int:
+    if isinstance(group, ResidentGroup):
+        return group.size()
+    return dist.get_world_size(group) if is_distributed() else 1
+
+
+def is_primary() -> bool:
+    return get_rank() == 0
+
+
+def barrier(group=None) -> None:
+    if isinstance(group, ResidentGroup):
+        return
+    if is_distributed():
+        dist.barrier(group)
+
+
+def print_rank0(*args, **kwargs) -> None:
+    if is_primary():
+        print(*args, **kwargs, flush=True)
+
+
+# --------------------------------------------------------------------------
+# Resident replica group: W data-parallel replicas on one GPU
+# --------------------------------------------------------------------------
+
+
+class _EventWork:
+    """Completion handle of a collective launched on a stream.
+
+    ``wait()`` has NCCL-Work semantics on a GPU: it makes the *current* stream
+    wait for the collective; the host does not block.
+    """
+
+    def __init__(self, stream: torch.cuda.Stream):
+        self._event = torch.cuda.Event()
+        self._event.record(stream)
+
+    def wait(self, timeout=None) -> bool:  # noqa: ARG002 - mirrors dist.Work.wait
+        torch.cuda.current_stream().wait_event(self._event)
+        return True
+
+    def is_completed(self) -> bool:
+        return self._event.query()
+
+    def synchronize(self) -> None:
+        self._event.synchronize()
+
+
+_ROW_ALIGN_BYTES = 256
+
+
+class _Arena:
+    """W equally laid-out rows (one per replica) of one symmetric allocation."""
+
+    __slots__ = ("data", "numel", "row_elems", "dtype", "own_base", "esize")
+
+    def __init__(self, world: int, rank: int, numel: int, dtype: torch.dtype, device: torch.device):
+        esize = torch.empty((), dtype=dtype).element_size()
+        align = _ROW_ALIGN_BYTES // esize
+        self.row_elems = max(align, (numel + align - 1) // align * align)
+        self.data = torch.zeros((world, self.row_elems), dtype=dtype, device=device)
+        self.numel = numel
+        self.dtype = dtype
+        self.esize = esize
+        self.own_base = self.data[rank].data_ptr()
+
+    def row(self, r: int) -> torch.Tensor:
+        return self.data[r, : self.numel]
+
+    def offset_of(self, t: torch.Tensor) -> int | None:
+        p = t.data_ptr()
+        off, rem = divmod(p - self.own_base, self.esize)
+        if rem or off < 0 or off + t.numel() > self.numel or t.dtype != self.dtype:
+            return None
+        return off
+
+
+class ResidentGroup:
+    """A data-parallel group of ``world_size`` replicas emulated on one GPU.
+
+    Rank ``rank`` is the live replica driven by this process.  Its peers exist
+    as their *contributions* -- what would arrive over xGMI from the other
+    GPUs -- held in symmetric buffers: :meth:`zeros` allocates one row per
+    replica and hands back this rank's row; :meth:`replicas` returns the W
+    rows for any view of such a buffer (this rank's view at index ``rank``).
+    Whoever stages an emulated step writes the peers' rows; the collectives
+    then reduce over all W rows with the gfx950 kernels, in rank order.
+
+    The group plays the role of a process group everywhere minidist takes one
+    (``comm.get_world_size(group)`` is ``world_size``).  There is no
+    inter-GPU traffic and no second process.
+    """
+
+    def __init__(self, world_size: int, rank: int = 0, device: torch.device | str | None = None):
+        if not 1 <= world_size <= _native.MDX_MAX_WORLD:
+            raise ValueError(f"world_size must be in [1, {_native.MDX_MAX_WORLD}], got {world_size}")
+        if not 0 <= rank < world_size:
+            raise ValueError(f"rank {rank} outside [0, {world_size})")
+        self._world = world_size
+        self._rank = rank
+        self.device = torch.device(device) if device is not None else current_device()
+        self._arenas: list[_Arena] = []
+
+    def size(self) -> int:
+        return self._world
+
+    def rank(self) -> int:
+        return self._rank
+
+    def __repr__(self) -> str:
+        return f"ResidentGroup(world_size={self._world}, rank={self._rank}, device={self.device})"
+
+    # -- symmetric memory ---------------------------------------------------
+
+    def zeros(self, numel: int, dtype: torch.dtype) -> torch.Tensor:
+        """This rank's row of a new zero-filled symmetric buffer of ``numel`` elements."""
+        arena = _Arena(self._world, self._rank, numel, dtype, self.device)
+        self._arenas.append(arena)
+        return arena.row(self._rank)
+
+    def _locate(self, t: torch.Tensor) -> tuple[_Arena, int]:
+        for arena in self._arenas:
+            off = arena.offset_of(t)
+            if off is not None:
+                return arena, off
+        raise RuntimeError(
+            "tensor is not part of a symmetric buffer of this ResidentGroup "
+            "(allocate collective buffers with ResidentGroup.zeros)"
+        )
+
+    def replicas(self, t: torch.Tensor) -> list[torch.Tensor]:
+        """The W replicas' copies of ``t`` (index ``rank`` is ``t``'s own memory)."""
+        arena, off = self._locate(t)
+        n = t.numel()
+        return [arena.data[r, off : off + n].view(t.shape) for r in range(self._world)]
+
+    def release(self) -> None:
+        """Drop every symmetric buffer (views handed out keep their memory alive)."""
+        self._arenas.clear()
+
+    # -- collectives ----------------------------------------------------------
+
+    def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
+        """In-place SUM over the W replicas of each tensor, rank order 0..W-1.
+
+        Tensors living in the same symmetric buffer are reduced by one
+        dispatch (the runs must be in increasing offset order, as DDP's
+        buckets are)."""
+        if not tensors:
+            return None
+        device = tensors[0].device
+        stream = torch.cuda.current_stream(device)
+        groups: dict[int, tuple[_Arena, list[int], list[int]]] = {}
+        for t in tensors:
+            _native.require_device_tensor(t, "all_reduce input")
+            arena, off = self._locate(t)
+            entry = groups.setdefault(id(arena), (arena, [], []))
+            entry[1].append(off)
+            entry[2].append(t.numel())
+        for arena, offs, nums in groups.values():
+            order = sorted(range(len(offs)), key=offs.__getitem__)
+            bases = [arena.data[r].data_ptr() for r in range(self._world)]
+            _native.allreduce_sum(
+                bases,
+                _native.dtype_code(arena.dtype),
+                [offs[i] for i in order],
+                [nums[i] for i in order],
+                arena.own_base,
+                stream.cuda_stream,
+            )
+        return _EventWork(stream) if async_op else None
+
+    def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
+        """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
+        _native.require_device_tensor(input_, "reduce_scatter input")
+        reps = self.replicas(input_)
+        S = output.numel()
+        if input_.numel() != S * self._world:
+            raise ValueError(f"reduce_scatter: input has {input_.numel()} elements, expected {S * self._world}")
+        if output.dtype != input_.dtype:
+            raise TypeError("reduce_scatter: output and input dtypes differ")
+        _native.require_dense(output, "reduce_scatter output")
+        lo = self._rank * S
+        flat = [r.reshape(-1) for r in reps]
+        own = _native.pieces_array([(flat[self._rank][lo:].data_ptr(), 0, S)])
+        peers = [f[lo:].data_ptr() for f in flat]
+        code = _native.dtype_code(input_.dtype)
+        stream = torch.cuda.current_stream(input_.device)
+        _native.reduce_scatter_share(
+            own, peers, self._rank, code, code, False, output.data_ptr(), code, False, 1.0, None,
+            stream.cuda_stream,
+        )
+        return _EventWork(stream) if async_op else None
+
+    def all_gather_into(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
+        """``output[r*S:(r+1)*S] = replicas(input_)[r]`` for every rank r."""
+        _native.require_device_tensor(input_, "all_gather input")
+        _native.require_dense(output, "all_gather output")
+        reps = self.replicas(input_)
+        S = input_.numel()
+        if output.numel() != S * self._world or output.dtype != input_.dtype:
+            raise ValueError("all_gather: output must hold world_size inputs of the same dtype")
+        out = output.view(-1)
+        rows = [(reps[r].data_ptr(), out[r * S :].data_ptr(), S) for r in range(self._world)]
+        code = _native.dtype_code(input_.dtype)
+        stream = torch.cuda.current_stream(input_.device)
+        _native.pack(_native.spans_array(rows), code, code, 1.0, False, stream.cuda_stream)
+        return _EventWork(stream) if async_op else None
+
+
+def zeros_for_collective(numel: int, dtype: torch.dtype, device: torch.device, group=None) -> torch.Tensor:
+    """A zero-filled flat buffer that ``group``'s collectives can operate on.
+
+    For a :class:`ResidentGroup` this is this rank's row of a symmetric
+    buffer; otherwise a plain ``torch.zeros`` (reference ddp.py:83-84)."""
+    if isinstance(group, ResidentGroup):
+        return group.zeros(numel, dtype)
+    return torch.zeros(numel, dtype=dtype, device=device)
+
+
+# --------------------------------------------------------------------------
+# Instrumented collectives (reference comm.py:210-277)
+# --------------------------------------------------------------------------
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+_all_gather_single = getattr(dist, "all_gather_single", None) or dist.all_gather_into_tensor
+_reduce_scatter_single = getattr(dist, "reduce_scatter_single", None) or dist.reduce_scatter_tensor
+
+
+def all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op: bool = False):
+    world = get_world_size(group)
+    if world == 1:
+        return None
+    payload = _nbytes(tensor)
+    comm_stats.add("all_reduce", payload, int(2 * (world - 1) / world * payload))
+    if isinstance(group, ResidentGroup):
+        if op != dist.ReduceOp.SUM:
+            raise NotImplementedError("ResidentGroup all_reduce implements SUM")
+        return group.all_reduce_sum([tensor], async_op=async_op)
+    return dist.all_reduce(tensor, op=op, group=group, async_op=async_op)
+
+
+def all_reduce_coalesced(tensors: Sequence[torch.Tensor], group=None, async_op: bool = False):
+    """SUM all-reduce of several tensors issued as one collective call.
+
+    Same accounting as one :func:`all_reduce` per tensor.  A ResidentGroup
+    reduces every tensor of one symmetric buffer in a single dispatch; a real
+    group issues the per-tensor collectives back to back and returns the last
+    Work (collectives on one communicator complete in order)."""
+    world = get_world_size(group)
+    if world == 1 or not tensors:
+        return None
+    for t in tensors:
+        payload = _nbytes(t)
+        comm_stats.add("all_reduce", payload, int(2 * (world - 1) / world * payload))
+    if isinstance(group, ResidentGroup):
+        return group.all_reduce_sum(list(tensors), async_op=async_op)
+    work = None
+    for t in tensors:
+        work = dist.all_reduce(t, group=group, async_op=async_op)
+    return work
+
+
+def all_gather_into_tensor(output: torch.Tensor, input_: torch.Tensor, group=None, async_op: bool = False):
+    world = get_world_size(group)
+    if world == 1:
+        output.copy_(input_)
+        return None
+    payload = _nbytes(output)
+    comm_stats.add("all_gather", payload, int((world - 1) / world * payload))
+    if isinstance(group, ResidentGroup):
+        return group.all_gather_into(output, input_, async_op=async_op)
+    return _all_gather_single(output, input_, group=group, async_op=async_op)
+
+
+def reduce_scatter_tensor(
+    output: torch.Tensor, input_: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op: bool = False
+):
+    world = get_world_size(group)
+    if world == 1:
+        output.copy_(input_)
+        return None
+    payload = _nbytes(input_)
+    comm_stats.add("reduce_scatter", payload, int((world - 1) / world * payload))
+    if isinstance(group, ResidentGroup):
+        if op != dist.ReduceOp.SUM:
+            raise NotImplementedError("ResidentGroup reduce_scatter implements SUM")
+        return group.reduce_scatter_sum(output, input_, async_op=async_op)
+    return _reduce_scatter_single(output, input_, op=op, group=group, async_op=async_op)
+
+
+def broadcast(tensor: torch.Tensor, src: int, group=None, async_op: bool = False):
+    if get_world_size(group) == 1:
+        return None
+    comm_stats.add("broadcast", _nbytes(tensor), _nbytes(tensor))
+    if isinstance(group, ResidentGroup):
+        return None  # peers are staged by the caller; nothing to send
+    return dist.broadcast(tensor, src=src, group=group, async_op=async_op)

@@ -1,0 +1,157 @@
+/*
+ * mdx.h -- C ABI of libmdx.so, the MI355X (gfx950) kernels behind minidist's
+ * per-rank gradient-communication path.
+ *
+ * The reference (minidist, pure Python on torch.distributed) has no native
+ * layer: its "operator API" for this path is a handful of Python methods that
+ * chain ATen ops.  Each entry point below replaces one of them; the comment
+ * above it cites the reference lines (paths relative to the reference repo).
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (HBM) unless stated; the span / piece
+ *     tables themselves are HOST arrays that the library copies into the
+ *     kernel-argument segment of each dispatch (no device table to manage).
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Every call is
+ *     asynchronous and stream-ordered; no call synchronises the host, and no
+ *     call allocates memory.
+ *   - Return 0 on success, a negative MDX_E* code for a rejected argument
+ *     (checked before anything is launched), or a positive hipError_t value.
+ *     mdx_strerror() names both kinds.
+ *   - Arithmetic is IEEE fp32 with round-to-nearest-even, denormals kept and
+ *     no contraction, in the same op order as the ATen chain it replaces, so
+ *     results are bit-identical to the reference for a fixed summation order.
+ *     bf16 results are rounded to nearest even; every NaN becomes 0xFFFF.
+ *   - found_inf, when not NULL, points to one int32 on the device that the
+ *     caller zeroes; a kernel stores 1 into it if it produced any inf or NaN,
+ *     and never stores 0.
+ *   - No global mutable state: calls are thread-safe; calls that write the
+ *     same memory must be ordered by the caller (same stream or events).
+ */
+#ifndef MDX_H_
+#define MDX_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MDX_ABI_VERSION 1
+
+/* Only the entry points below are exported (the library builds with hidden
+ * visibility by default). */
+#if defined(__GNUC__) || defined(__clang__)
+#define MDX_API __attribute__((visibility("default")))
+#else
+#define MDX_API
+#endif
+
+/* Element types (torch.float32, torch.bfloat16). */
+enum { MDX_F32 = 0, MDX_BF16 = 1 };
+
+/* Status codes (negative; positive values are hipError_t). */
+enum {
+  MDX_OK = 0,
+  MDX_EINVAL = -1,    /* NULL pointer, negative count or size            */
+  MDX_EDTYPE = -2,    /* dtype code not in {MDX_F32, MDX_BF16}            */
+  MDX_EWORLD = -3,    /* world outside [1, MDX_MAX_WORLD] or rank >= world */
+  MDX_EALIAS = -4,    /* an output overlaps an input it must not overlap  */
+};
+
+#define MDX_MAX_WORLD 16
+
+/* One contiguous run copied from `src` to `dst` (both device pointers).
+ * `src == NULL` reads as zeros (a parameter whose .grad is None). */
+typedef struct mdx_span {
+  const void* src;
+  void* dst;
+  int64_t numel;
+} mdx_span;
+
+/* One run of this rank's own contribution to a W-way reduction: elements
+ * [pos, pos + numel) of the reduced vector come, for this rank, from `own`
+ * (a device pointer, NULL = zeros) and, for every peer r, from
+ * peers[r] + pos. */
+typedef struct mdx_piece {
+  const void* own;
+  int64_t pos;
+  int64_t numel;
+} mdx_piece;
+
+/* Pack: flatten gradients into a bucket, then pre-scale.
+ * Replaces _Bucket.gather_into_buffer (minidist/ddp.py:75-92): per span
+ * `flat.copy_(p.grad.reshape(-1))` / `flat.zero_()` (ddp.py:85-90), then
+ * `buffer.mul_(scale)` (ddp.py:91) with scale = 1/W rounded to fp32 and
+ * divide = 0.  Also the FSDP flatten + pre-division of reduce_scatter_grads,
+ * `buf[off:off+n].copy_(p.grad.reshape(-1))` then `buf.div_(W)`
+ * (minidist/fsdp.py:218-227), with scale = W and divide = 1.
+ * dst[i] = rnd_dst(rnd_dst(src[i]) * scale), or ... / scale when divide != 0;
+ * the scaling is skipped when scale == 1.  All spans of one call share dtypes. */
+MDX_API int mdx_pack(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, float scale,
+             int divide, void* stream);
+
+/* Unpack, with the loss-scaler's unscale + found-inf fused as an epilogue.
+ * Replaces _Bucket.scatter_from_buffer (minidist/ddp.py:94-102):
+ * `p.grad.copy_(bucket_slice)` -- and, when inv_scale != 1 or found_inf is
+ * given, the per-gradient body of DistributedGradScaler.unscale_
+ * (minidist/amp.py:212-213): `p.grad.mul_(inv_scale)` then
+ * `found_inf += (~isfinite(p.grad)).any()`.
+ * dst[i] = v = rnd_dst(src[i]); if inv_scale != 1: v = rnd_dst(v * inv_scale);
+ * flag if !isfinite(v).  Spans must not have src == NULL. */
+MDX_API int mdx_unpack(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, float inv_scale,
+               int32_t* found_inf, void* stream);
+
+/* Multi-tensor unscale + found-inf, in place on each span's `dst`
+ * (`src` is ignored).  Replaces the loop of DistributedGradScaler.unscale_
+ * (minidist/amp.py:208-213) for gradients that no fused unpack has unscaled:
+ * g = rnd(g * inv_scale); flag if !isfinite(g). */
+MDX_API int mdx_unscale_found_inf(const mdx_span* spans, int n_spans, int dtype, float inv_scale,
+                          int32_t* found_inf, void* stream);
+
+/* W-way SUM all-reduce arithmetic over W replica buffers resident in HBM,
+ * in the fixed rank order ((in[0] + in[1]) + in[2]) + ..., one rounding per
+ * add in `dtype`.  The W `replicas` share one layout; the call reduces the
+ * n_runs element ranges [offsets[k], offsets[k] + numels[k]) (increasing,
+ * non-overlapping) of all of them into the same ranges of `out`, which may
+ * be one of the replica bases (the in-place all-reduce of a bucket) and must
+ * otherwise not overlap them.  One bucket is one run; a run of ready buckets
+ * laid out in one buffer is reduced by a single dispatch.
+ * Replaces the reduction done by comm.all_reduce -> dist.all_reduce(SUM)
+ * (minidist/comm.py:223-234) on DDP buckets (minidist/ddp.py:243-247). */
+MDX_API int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,
+                      const int64_t* numels, int n_runs, void* out, void* stream);
+
+/* This rank's share of a SUM reduce-scatter, with FSDP's pre-division,
+ * dtype changes and optional accumulation fused.
+ * Replaces _FSDPUnit.reduce_scatter_grads (minidist/fsdp.py:215-237): widen
+ * each contribution to reduce_dtype (fsdp.py:218-222), `buf.div_(W)` when
+ * divide != 0 (fsdp.py:227), rank-ordered SUM of the rank's slice
+ * (comm.reduce_scatter_tensor, minidist/comm.py:252-265), `out.to(shard
+ * dtype)` (fsdp.py:233), then set or `flat_shard.grad.add_(out)`
+ * (fsdp.py:234-237) when accumulate != 0.  Optional unscale + found-inf
+ * epilogue on the final shard value as in mdx_unpack.
+ * Element j of the shard: contribution of rank r = peers[r][j] for r != rank,
+ * and own data from the piece covering position j for r == rank (`peers` are
+ * already offset to this rank's slice; peers[rank] is ignored). */
+MDX_API int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const* peers, int world,
+                             int rank, int in_dtype, int reduce_dtype, int divide, void* shard,
+                             int shard_dtype, int accumulate, float inv_scale, int32_t* found_inf,
+                             void* stream);
+
+/* fp32 -> bf16 round-to-nearest-even cast (NaN -> 0xFFFF), written straight
+ * into this rank's slot of the FSDP gather buffer.
+ * Replaces `src = flat_shard.to(param_dtype)` in _FSDPUnit.unshard
+ * (minidist/fsdp.py:178-180). */
+MDX_API int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stream);
+
+/* Static description of a status code. */
+MDX_API const char* mdx_strerror(int code);
+
+/* MDX_ABI_VERSION of the loaded library. */
+MDX_API int mdx_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDX_H_ */

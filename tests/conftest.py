@@ -1,0 +1,71 @@
+"""Test configuration: import paths, the ``gpu`` marker, shared helpers.
+
+``-m "not gpu"`` runs here without a GPU: the oracle against the golden
+fixtures and the mathematics, host logic, and the C ABI's exports and
+argument checks.  ``-m gpu`` runs on an MI355X: every kernel through the C
+ABI against the oracle, and the Python API end to end.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+PKG_PARENT = ROOT / "distributed-training-framework_amd"
+for p in (str(ROOT), str(PKG_PARENT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+
+
+def load_golden(name: str) -> dict:
+    with np.load(GOLDEN / name, allow_pickle=False) as d:
+        return {k: d[k] for k in d.files}
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    """Bitwise equality, except that any NaN equals any NaN (payloads are not compared)."""
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    if a.dtype == np.float32:
+        na, nb = np.isnan(a), np.isnan(b)
+        if not np.array_equal(na, nb):
+            return False
+        return np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb])
+    if a.dtype == np.uint16:  # bf16 bits
+        na = (a & 0x7FFF) > 0x7F80
+        nb = (b & 0x7FFF) > 0x7F80
+        if not np.array_equal(na, nb):
+            return False
+        return np.array_equal(a[~na], b[~nb])
+    return np.array_equal(a, b)
+
+
+def first_mismatch(a: np.ndarray, b: np.ndarray) -> str:
+    a = np.asarray(a).reshape(-1)
+    b = np.asarray(b).reshape(-1)
+    if a.shape != b.shape:
+        return f"shape {a.shape} vs {b.shape}"
+    ua = a.view(np.uint32) if a.dtype == np.float32 else a
+    ub = b.view(np.uint32) if b.dtype == np.float32 else b
+    idx = np.nonzero(ua != ub)[0]
+    if idx.size == 0:
+        return "no mismatch"
+    i = int(idx[0])
+    return f"{idx.size} mismatches; first at {i}: {a[i]!r} ({int(ua[i]):#x}) vs {b[i]!r} ({int(ub[i]):#x})"
+
+
+@pytest.fixture(scope="session")
+def rng():
+    return np.random.default_rng(1234)

@@ -1,0 +1,302 @@
+"""DDP and the grad scaler through the Python API, on the GPU, vs the oracle.
+
+W data-parallel replicas are emulated on one GPU with a ResidentGroup: the
+peers' packed, pre-scaled bucket contributions (what would arrive over the
+wire) are staged with the oracle's pack, this rank's gradients go through the
+real DDP hooks / finish_gradient_sync, and the results are compared bit for
+bit with oracle.ddp_pipeline, and within the reference's 2e-5 tolerance with
+the single-process full-batch gradient (reference tests/test_ddp.py:32-146).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import tiny_gpt
+from conftest import first_mismatch, same_bits
+from minidist import DDP, DistributedGradScaler, ResidentGroup
+from oracle import gradpath as o
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def host_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().reshape(-1)
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().astype(np.uint16)
+    return t.numpy().copy()
+
+
+def dev_from(a: np.ndarray, shape) -> torch.Tensor:
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).to(DEV).view(shape)
+    return torch.from_numpy(a.copy()).to(DEV).view(shape)
+
+
+def odt(dtype: torch.dtype) -> str:
+    return o.BF16 if dtype == torch.bfloat16 else o.F32
+
+
+class Flat(nn.Module):
+    """Parameters of given shapes, registered in order (no forward needed)."""
+
+    def __init__(self, shapes, dtype=torch.float32):
+        super().__init__()
+        self.ps = nn.ParameterList([nn.Parameter(torch.zeros(s, dtype=dtype, device=DEV)) for s in shapes])
+
+
+def stage_peers(ddp: DDP, replica_grads, dtypes, rank: int, W: int) -> None:
+    """Write every peer's packed, 1/W-scaled bucket into its resident row."""
+    params = [p for p in ddp.module.parameters() if p.requires_grad]
+    index = {id(p): i for i, p in enumerate(params)}
+    for b, bucket in enumerate(ddp._buckets):
+        idxs = [index[id(p)] for p in bucket.params]
+        rows = ddp.bucket_replicas(b)
+        bdt = dtypes[idxs[0]]
+        for r in range(W):
+            if r == rank:
+                continue
+            packed = o.pack([replica_grads[r][i] for i in idxs], [dtypes[i] for i in idxs],
+                            [params[i].numel() for i in idxs], bdt, 1.0 / W)
+            rows[r].copy_(dev_from(packed, rows[r].shape))
+
+
+def synthetic_grads(rng, shapes, W, dtype, scale, none_at=()):
+    out = []
+    for r in range(W):
+        row = []
+        for i, s in enumerate(shapes):
+            n = int(np.prod(s))
+            g = (rng.standard_normal(n) * 1e-3 * scale).astype(np.float32)
+            row.append(o.from_f32(g, odt(dtype)))
+        out.append(row)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("W,rank", [(2, 1), (4, 0), (8, 5), (3, 2)])
+@pytest.mark.parametrize("cap", [1e-6, 0.01, 25.0, 1e6])
+def test_finish_gradient_sync_bitwise(rng, dtype, W, rank, cap):
+    shapes = [(33,), (64, 8), (5,), (130,), (1,), (7, 9), (256, 4), (3,)]
+    model = Flat(shapes, dtype)
+    grp = ResidentGroup(W, rank, DEV)
+    ddp = DDP(model, process_group=grp, bucket_cap_mb=cap)
+    grads = synthetic_grads(rng, shapes, W, dtype, 2.0**10)
+    grads[rank][2] = None  # a parameter that received no gradient on this rank
+    dts = [odt(dtype)] * len(shapes)
+    stage_peers(ddp, grads, dts, rank, W)
+    for p, g in zip(model.parameters(), grads[rank], strict=True):
+        p.grad = None if g is None else dev_from(g, p.shape)
+    ddp.finish_gradient_sync()
+    want = o.ddp_pipeline(grads, dts, [int(np.prod(s)) for s in shapes], cap, rank, None)
+    for i, p in enumerate(model.parameters()):
+        got = host_bits(p.grad)
+        assert same_bits(got, want["grads"][i]), f"param {i}: " + first_mismatch(got, want["grads"][i])
+    for b, bucket in enumerate(ddp._buckets):
+        assert same_bits(host_bits(bucket.buffer), want["reduced"][b])
+
+
+def test_bucket_caps_give_identical_grads(rng):
+    """cfg2's property at small scale: 1 B, 25 MB and one giant bucket agree exactly."""
+    shapes = [(300, 7), (11,), (1024,), (5, 5), (2048, 3), (9,)]
+    W, rank = 4, 3
+    grads = synthetic_grads(rng, shapes, W, torch.float32, 1.0)
+    results = []
+    for cap in (1e-6, 25.0, 1e6):
+        model = Flat(shapes)
+        ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap)
+        stage_peers(ddp, grads, [o.F32] * len(shapes), rank, W)
+        for p, g in zip(model.parameters(), grads[rank], strict=True):
+            p.grad = dev_from(g, p.shape)
+        ddp.finish_gradient_sync()
+        results.append([host_bits(p.grad) for p in model.parameters()])
+    for other in results[1:]:
+        for a, b in zip(results[0], other, strict=True):
+            assert np.array_equal(a, b)
+
+
+def _capture_hook(store):
+    def hook(p):
+        store[id(p)] = p.grad.detach().clone()
+
+    return hook
+
+
+@pytest.mark.parametrize("W", [2, 4])
+@pytest.mark.parametrize("cap,overlap", [(25.0, True), (1e-6, True), (1e6, True), (25.0, False)])
+def test_backward_matches_full_batch_and_oracle(W, cap, overlap):
+    """Reference tests/test_ddp.py:32-77 on one GPU: rank r's DDP grads == full-batch grads."""
+    c = tiny_gpt.Config()
+    ids, tgt = tiny_gpt.batch(c, 8)
+    full = tiny_gpt.GPT(c).to(DEV)
+    _, loss = full(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    expected = [p.grad.detach().clone() for p in full.parameters()]
+
+    # Each replica's local gradient on its chunk of the batch.
+    replica = []
+    for r in range(W):
+        m = tiny_gpt.GPT(c).to(DEV)
+        _, l_r = m(ids.chunk(W)[r].to(DEV), tgt.chunk(W)[r].to(DEV))
+        l_r.backward()
+        replica.append([host_bits(p.grad) for p in m.parameters()])
+
+    rank = W - 1
+    model = tiny_gpt.GPT(c).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture_hook(captured))  # runs before DDP's hook
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap)
+    dts = [o.F32] * len(expected)
+    stage_peers(ddp, replica, dts, rank, W)
+    _, l = ddp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
+    l.backward()
+
+    own = [host_bits(captured[id(p)]) for p in model.parameters()]
+    grads_in = [own if r == rank else replica[r] for r in range(W)]
+    want = o.ddp_pipeline(grads_in, dts, [p.numel() for p in model.parameters()], cap, rank, None)
+    for i, (p, e) in enumerate(zip(model.parameters(), expected, strict=True)):
+        assert same_bits(host_bits(p.grad), want["grads"][i]), f"param {i}"
+        diff = (p.grad - e).abs().max().item()
+        denom = max(e.abs().max().item(), 1.0)
+        assert diff / denom <= 2e-5, f"param {i}: relative error {diff / denom:.3e}"
+
+
+def test_no_sync_accumulation_then_sync():
+    """Reference tests/test_ddp.py:80-100: two half-batches under no_sync + synced == full step."""
+    c = tiny_gpt.Config()
+    W, rank = 2, 0
+    ids, tgt = tiny_gpt.batch(c, 8)
+    full = tiny_gpt.GPT(c).to(DEV)
+    _, loss = full(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    expected = [p.grad.detach().clone() for p in full.parameters()]
+    replica = []
+    for r in range(W):
+        m = tiny_gpt.GPT(c).to(DEV)
+        for half in zip(ids.chunk(W)[r].chunk(2), tgt.chunk(W)[r].chunk(2), strict=True):
+            _, l_r = m(half[0].to(DEV), half[1].to(DEV))
+            (l_r / 2).backward()
+        replica.append([host_bits(p.grad) for p in m.parameters()])
+    model = tiny_gpt.GPT(c).to(DEV)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV))
+    stage_peers(ddp, replica, [o.F32] * len(expected), rank, W)
+    halves = list(zip(ids.chunk(W)[rank].chunk(2), tgt.chunk(W)[rank].chunk(2), strict=True))
+    with ddp.no_sync():
+        _, l = ddp(halves[0][0].to(DEV), halves[0][1].to(DEV))
+        (l / 2).backward()
+    _, l = ddp(halves[1][0].to(DEV), halves[1][1].to(DEV))
+    (l / 2).backward()
+    for p, e in zip(model.parameters(), expected, strict=True):
+        rel = (p.grad - e).abs().max().item() / max(e.abs().max().item(), 1.0)
+        assert rel <= 2e-5
+
+
+def test_bucket_layout_matches_reference_invariants():
+    c = tiny_gpt.Config()
+    ddp = DDP(tiny_gpt.GPT(c).to(DEV), process_group=ResidentGroup(2, 0, DEV), bucket_cap_mb=0.05)
+    summary = ddp.bucket_summary()
+    assert len(summary) > 1
+    assert [b[0] for b in summary] == list(range(len(summary)))
+    for _, n, mb in summary:
+        assert mb <= 0.05 or n == 1
+    params = list(ddp.module.parameters())
+    assert ddp._buckets[0].params[0] is params[-1]
+    nbytes = [p.numel() * p.element_size() for p in params]
+    layout = o.build_buckets(nbytes, 0.05)
+    index = {id(p): i for i, p in enumerate(params)}
+    assert [[index[id(p)] for p in b.params] for b in ddp._buckets] == layout
+
+
+# ---------------------------------------------------------------------------
+# Grad scaler (reference tests/test_amp.py) on the GPU
+# ---------------------------------------------------------------------------
+
+
+def _linear():
+    torch.manual_seed(0)
+    m = torch.nn.Linear(4, 4).to(DEV)
+    return m, torch.optim.SGD(m.parameters(), lr=0.1)
+
+
+def test_overflow_skips_and_backs_off():
+    m, opt = _linear()
+    scaler = DistributedGradScaler(init_scale=1024.0)
+    for p in m.parameters():
+        p.grad = torch.ones_like(p)
+    next(iter(m.parameters())).grad[0, 0] = float("inf")
+    before = [p.detach().clone() for p in m.parameters()]
+    assert not scaler.step(opt)
+    scaler.update()
+    for p, b in zip(m.parameters(), before, strict=True):
+        assert torch.equal(p.detach(), b)
+    assert scaler.scale == 512.0 and scaler.num_skipped == 1
+
+
+def test_clean_steps_grow_the_scale():
+    m, opt = _linear()
+    scaler = DistributedGradScaler(init_scale=1024.0, growth_interval=2)
+    for _ in range(2):
+        for p in m.parameters():
+            p.grad = torch.full_like(p, 2.0) * scaler.scale
+        assert scaler.step(opt)
+        scaler.update()
+    assert scaler.scale == 2048.0 and scaler.num_skipped == 0
+
+
+def test_unscale_is_idempotent():
+    m, opt = _linear()
+    scaler = DistributedGradScaler(init_scale=256.0)
+    for p in m.parameters():
+        p.grad = torch.full_like(p, 3.0) * scaler.scale
+    assert not scaler.unscale_(opt)
+    scaler.unscale_(opt)
+    for p in m.parameters():
+        assert torch.equal(p.grad, torch.full_like(p.grad, 3.0))
+
+
+def test_mixed_overflow_history_final_scale():
+    m, opt = _linear()
+    scaler = DistributedGradScaler(init_scale=4096.0, growth_interval=2)
+    for bad in [True, False, False, True, True]:
+        for p in m.parameters():
+            p.grad = torch.ones_like(p)
+        if bad:
+            next(iter(m.parameters())).grad[0, 0] = float("nan")
+        scaler.step(opt)
+        scaler.update()
+    assert scaler.scale == 1024.0
+
+
+@pytest.mark.parametrize("inject", [False, True])
+def test_fused_unscale_in_ddp_unpack(rng, inject):
+    """DDP(grad_scaler=...) unscales in its unpack; the scaler then skips those grads."""
+    shapes = [(100, 3), (17,), (4096,), (2,)]
+    W, rank, S = 4, 1, 2.0**16
+    model = Flat(shapes)
+    extra = nn.Parameter(torch.full((5,), 3.0 * S, device=DEV))  # optimizer param outside DDP
+    scaler = DistributedGradScaler(init_scale=S)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=0.01, grad_scaler=scaler)
+    grads = synthetic_grads(rng, shapes, W, torch.float32, S)
+    if inject:
+        grads[(rank + 1) % W][2][123] = np.float32(np.inf)
+    stage_peers(ddp, grads, [o.F32] * 4, rank, W)
+    for p, g in zip(model.parameters(), grads[rank], strict=True):
+        p.grad = dev_from(g, p.shape)
+    extra.grad = torch.full((5,), 3.0 * S, device=DEV)
+    opt = torch.optim.SGD(list(model.parameters()) + [extra], lr=0.0)
+    ddp.finish_gradient_sync()
+    found = scaler.unscale_(opt)
+    want = o.ddp_pipeline(grads, [o.F32] * 4, [int(np.prod(s)) for s in shapes], 0.01, rank, 1.0 / S)
+    for i, p in enumerate(model.parameters()):
+        assert same_bits(host_bits(p.grad), want["grads"][i])
+    assert torch.equal(extra.grad, torch.full((5,), 3.0, device=DEV))
+    assert found == want["found_inf"] == inject
+    with pytest.raises(RuntimeError):
+        ddp.finish_gradient_sync()  # second sync before update(): refused
+    scaler.update()
+

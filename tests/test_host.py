@@ -1,0 +1,232 @@
+"""Host-side logic and the C ABI surface, on the CPU (no kernel is launched).
+
+* libmdx.so loads and exports every function include/mdx.h declares, and the
+  ctypes table binds exactly those;
+* argument checks return their MDX_E* codes before anything is launched;
+* byte accounting, precision resolution, the scaler's state machine, the DDP
+  bucket layout (on meta tensors, at the real GPT-2 shapes) and the loud
+  failure on CPU tensors.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from conftest import ROOT
+from minidist import _native as nat
+from minidist import comm
+from minidist.amp import DistributedGradScaler, resolve_precision
+from minidist.ddp import DistributedDataParallel
+from minidist import workloads as w
+from oracle import gradpath as o
+
+HEADER = ROOT / "include" / "mdx.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^MDX_API\s+(?:int|const char\*)\s+(mdx_\w+)\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert names == set(nat.SIGNATURES), "ctypes table and header disagree"
+    lib = nat.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.mdx_abi_version() == nat.ABI_VERSION
+
+
+def test_exported_symbols_are_only_the_abi():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(nat.LIB_PATH)], capture_output=True, text=True)
+    if out.returncode != 0:
+        pytest.skip("nm unavailable")
+    text_syms = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    assert text_syms == declared_functions()
+
+
+def test_strerror_names_every_mdx_code():
+    for code_, frag in [(0, "success"), (-1, "invalid"), (-2, "dtype"), (-3, "world"), (-4, "overlap")]:
+        assert frag in nat.strerror(code_)
+    assert "unknown" in nat.strerror(-99)
+
+
+def _span(src, dst, n):
+    return nat.spans_array([(src, dst, n)])
+
+
+def test_argument_checks_happen_before_any_launch():
+    L = nat.lib()
+    P = ctypes.c_void_p
+    # dtype
+    assert L.mdx_pack(None, 0, 9, 0, 1.0, 0, None) == -2
+    assert L.mdx_unpack(None, 0, 0, 5, 1.0, None, None) == -2
+    assert L.mdx_unscale_found_inf(None, 0, 3, 1.0, None, None) == -2
+    # counts and NULLs
+    assert L.mdx_pack(None, -1, 0, 0, 1.0, 0, None) == -1
+    assert L.mdx_pack(None, 3, 0, 0, 1.0, 0, None) == -1
+    s = _span(0, 0, 10)  # dst NULL with numel > 0
+    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None) == -1
+    s = _span(0, 4096, 10)  # unpack needs a source
+    assert L.mdx_unpack(s.ctypes.data, 1, 0, 0, 1.0, None, None) == -1
+    s = _span(0, 4096, -1)
+    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None) == -1
+    assert L.mdx_cast_f32_bf16(None, None, -1, None) == -1
+    assert L.mdx_cast_f32_bf16(P(4096), P(4096 + 8), 16, None) == -4  # overlapping cast
+    # zero-length work is a no-op that succeeds without a device
+    assert L.mdx_pack(None, 0, 0, 0, 1.0, 0, None) == 0
+    assert L.mdx_cast_f32_bf16(None, None, 0, None) == 0
+    # world / rank
+    reps = (ctypes.c_void_p * 2)(4096, 8192)
+    offs = (ctypes.c_int64 * 1)(0)
+    nums = (ctypes.c_int64 * 1)(8)
+    assert L.mdx_allreduce_sum(reps, 0, 0, offs, nums, 1, P(4096), None) == -3
+    assert L.mdx_allreduce_sum(reps, 17, 0, offs, nums, 1, P(4096), None) == -3
+    bad_offs = (ctypes.c_int64 * 2)(8, 0)  # runs must increase
+    bad_nums = (ctypes.c_int64 * 2)(4, 4)
+    assert L.mdx_allreduce_sum(reps, 2, 0, bad_offs, bad_nums, 2, P(4096), None) == -1
+    assert L.mdx_allreduce_sum(reps, 2, 0, offs, nums, 1, P(4096 + 4), None) == -4  # partial overlap
+    pc = nat.pieces_array([(4096, 0, 8)])
+    peers = (ctypes.c_void_p * 2)(0, 8192)
+    assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 2, 0, 0, 1, P(1 << 20), 0, 0, 1.0, None, None) == -3
+    assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 0, 0, 7, 1, P(1 << 20), 0, 0, 1.0, None, None) == -2
+    assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 0, 0, 0, 1, P(8192), 0, 0, 1.0, None, None) == -4
+
+
+# ---------------------------------------------------------------------------
+# comm
+# ---------------------------------------------------------------------------
+
+
+def test_comm_stats_formulas_match_reference():
+    """minidist/comm.py:65-72: all-reduce 2(W-1)/W N, all-gather / reduce-scatter (W-1)/W N."""
+    grp = comm.ResidentGroup(4, 1, "cpu")
+    with comm.record_comm() as stats:
+        comm.comm_stats.add("all_reduce", 1000, int(2 * 3 / 4 * 1000))
+    assert stats.as_rows() == [("all_reduce", 1, 1000, 1500)]
+    assert stats.total_bus_bytes() == 1500
+    assert not comm.comm_stats.enabled
+    assert comm.get_world_size(grp) == 4 and comm.get_rank(grp) == 1
+    assert comm.get_world_size(None) == 1 and comm.get_rank(None) == 0
+    assert comm.all_reduce(torch.zeros(3), group=None) is None  # world 1 short-circuit
+
+
+def test_resident_group_validates_its_shape():
+    with pytest.raises(ValueError):
+        comm.ResidentGroup(0)
+    with pytest.raises(ValueError):
+        comm.ResidentGroup(17, device="cpu")
+    with pytest.raises(ValueError):
+        comm.ResidentGroup(4, 4, "cpu")
+
+
+def test_resident_group_symmetric_rows_cpu_layout():
+    grp = comm.ResidentGroup(3, 2, "cpu")
+    own = grp.zeros(10, torch.float32)
+    reps = grp.replicas(own[3:7])
+    assert len(reps) == 3 and reps[2].data_ptr() == own[3:7].data_ptr()
+    assert all(r.numel() == 4 for r in reps)
+    assert len({r.data_ptr() for r in reps}) == 3
+    with pytest.raises(RuntimeError):
+        grp.replicas(torch.zeros(4))
+
+
+# ---------------------------------------------------------------------------
+# amp (host logic; kernels are exercised on the GPU)
+# ---------------------------------------------------------------------------
+
+
+def test_resolve_precision():
+    """Reference tests/test_amp.py:123-134."""
+    assert not resolve_precision("fp32", torch.device("cpu")).enabled
+    bf16 = resolve_precision("bf16", torch.device("cpu"))
+    assert bf16.dtype == torch.bfloat16 and not bf16.needs_grad_scaler
+    assert resolve_precision("auto", torch.device("cpu")).dtype == torch.bfloat16
+    with pytest.raises(ValueError):
+        resolve_precision("fp16", torch.device("cpu"))
+    with pytest.raises(ValueError):
+        resolve_precision("int4", torch.device("cpu"))
+
+
+def test_disabled_scaler_is_transparent():
+    """Reference tests/test_amp.py:137-143."""
+    model = nn.Linear(4, 4)
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    scaler = DistributedGradScaler(enabled=False)
+    loss = torch.tensor(2.0)
+    assert scaler.scale_loss(loss) is loss
+    assert scaler.scale == 1.0
+    for p in model.parameters():
+        p.grad = torch.ones_like(p)
+    assert scaler.step(opt)
+
+
+@pytest.mark.parametrize(
+    "init,interval,found,final",
+    [(1024.0, 2000, [True], 512.0), (1024.0, 2, [False, False], 2048.0), (4096.0, 2, [True, False, False, True, True], 1024.0)],
+)
+def test_scaler_state_machine_matches_oracle(init, interval, found, final):
+    s = DistributedGradScaler(init_scale=init, growth_interval=interval)
+    ref = o.ScalerState(scale=init, growth_interval=interval)
+    for f in found:
+        s._found_inf_this_step, s._unscaled = f, True  # what unscale_ would have decided
+        s.update()
+        ref.update(f)
+        assert s.scale == ref.scale
+        assert not s._unscaled
+    assert s.scale == final
+    assert set(s.state_dict()) == {"scale", "good_steps", "num_skipped", "num_steps"}
+
+
+# ---------------------------------------------------------------------------
+# DDP layout (meta tensors: real GPT-2 shapes without allocating them)
+# ---------------------------------------------------------------------------
+
+
+class MetaParams(nn.Module):
+    def __init__(self, specs):
+        super().__init__()
+        self.ps = nn.ParameterList([nn.Parameter(torch.empty(s.shape, device="meta", dtype=s.dtype)) for s in specs])
+
+
+@pytest.mark.parametrize("cfg,W,cap", [(w.GPT2_SMALL, 8, 25.0), (w.GPT2_MEDIUM, 4, 1e-6), (w.GPT2_MEDIUM, 4, 1e6), (w.TINY_GPT, 4, 25.0)])
+def test_ddp_layout_matches_oracle_at_real_shapes(cfg, W, cap):
+    specs = w.gpt_specs(**cfg)
+    ddp = DistributedDataParallel(MetaParams(specs), process_group=comm.ResidentGroup(W, 0, "meta"), bucket_cap_mb=cap)
+    layout = o.build_buckets([s.nbytes for s in specs], cap)
+    assert [len(b.params) for b in ddp._buckets] == [len(b) for b in layout]
+    assert [b.numel for b in ddp._buckets] == [sum(specs[i].numel for i in b) for b in layout]
+    assert ddp.world_size == W
+
+
+def test_out_of_scope_names_say_so():
+    import minidist
+
+    with pytest.raises(ImportError, match="does not provide"):
+        minidist.ParallelMesh  # noqa: B018
+    with pytest.raises(AttributeError):
+        minidist.no_such_thing  # noqa: B018
+
+
+def test_cpu_tensors_fail_loudly():
+    model = nn.Linear(3, 3)
+    ddp = DistributedDataParallel(model, process_group=comm.ResidentGroup(2, 0, "cpu"))
+    for p in model.parameters():
+        p.grad = torch.ones_like(p)
+    with pytest.raises(RuntimeError, match="HIP kernels"):
+        ddp.finish_gradient_sync()
+
+
+def test_span_table_layout_is_the_c_struct():
+    a = nat.spans_array([(1, 2, 3)])
+    assert a.itemsize == 24 and a.tobytes() == np.array([1, 2, 3], dtype="<i8").tobytes()
+    b = nat.pieces_array([(5, 6, 7)])
+    assert b.itemsize == 24

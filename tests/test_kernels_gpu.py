@@ -1,0 +1,366 @@
+"""Kernel parity on the GPU: every libmdx entry point vs the oracle, bit for bit.
+
+Each test builds seeded inputs on the host, runs the entry point through the C
+ABI (minidist._native is a ctypes shim over include/mdx.h) on ``cuda:0``,
+copies the result back and compares it with oracle/gradpath.py.  NaN payloads
+are not compared (every NaN equals every NaN); every other bit is.  Buffers
+carry sentinel gaps so that a write outside a span shows up.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import first_mismatch, load_golden, same_bits
+from minidist import _native as nat
+from oracle import gradpath as o
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+SENTINEL_F32 = np.float32(-7.25)
+SENTINEL_BF16 = np.uint16(0x4242)
+
+
+def code(dt: str) -> int:
+    return nat.MDX_BF16 if dt == o.BF16 else nat.MDX_F32
+
+
+def to_dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).to(DEV).view(torch.bfloat16)
+    return torch.from_numpy(a.astype(np.float32)).to(DEV)
+
+
+def to_host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().astype(np.uint16)
+    return t.numpy().copy()
+
+
+def empty_dev(n: int, dt: str) -> torch.Tensor:
+    if dt == o.BF16:
+        return torch.full((n,), int(SENTINEL_BF16.view(np.int16)), dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    return torch.full((n,), float(SENTINEL_F32), dtype=torch.float32, device=DEV)
+
+
+def stream() -> int:
+    return torch.cuda.current_stream(DEV).cuda_stream
+
+
+def values(rng, n: int, dt: str, specials: bool = True, scale: float = 1.0) -> np.ndarray:
+    x = (rng.standard_normal(n) * scale).astype(np.float32)
+    if specials and n:
+        pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-40, 3.4e38, -3.39e38, 1.2e-38], np.float32)
+        idx = rng.integers(0, n, max(1, n // 50))
+        x[idx] = pool[rng.integers(0, len(pool), idx.size)]
+    return o.from_f32(x, dt)
+
+
+def esize(dt: str) -> int:
+    return 2 if dt == o.BF16 else 4
+
+
+# ---------------------------------------------------------------------------
+# pack / unpack / unscale (the copy kernel)
+# ---------------------------------------------------------------------------
+
+SIZES = [0, 1, 2, 3, 7, 8, 15, 16, 17, 63, 64, 65, 255, 256, 1000, 4095, 4096, 4097, 12345, 70001]
+
+
+def _span_case(rng, sdt, ddt, null_every=0, n_spans=None):
+    """Random spans: misaligned sources (sub-views), misaligned packed destinations."""
+    n_spans = n_spans or len(SIZES)
+    sizes = [SIZES[i % len(SIZES)] for i in range(n_spans)]
+    rng.shuffle(sizes)
+    srcs, rows_host = [], []
+    dst_off, offs = 0, []
+    for k, n in enumerate(sizes):
+        shift = int(rng.integers(0, 8))
+        host = values(rng, n + shift, sdt)
+        t = to_dev(host)
+        null = null_every and k % null_every == 0
+        srcs.append((t, shift, host[shift:], null))
+        dst_off += int(rng.integers(0, 4))  # gap keeps a sentinel
+        offs.append(dst_off)
+        dst_off += n
+    dst = empty_dev(dst_off + 5, ddt)
+    rows = []
+    for (t, shift, host, null), off, n in zip(srcs, offs, sizes, strict=True):
+        src_ptr = 0 if null else t.data_ptr() + shift * esize(sdt)
+        rows.append((src_ptr, dst.data_ptr() + off * esize(ddt), n))
+        rows_host.append((None if null else host, off, n))
+    return srcs, dst, rows, rows_host
+
+
+@pytest.mark.parametrize("sdt,ddt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.BF16, o.F32)])
+@pytest.mark.parametrize("scale,divide", [(1.0, False), (1.0 / 8, False), (1.0 / 3, False), (3.0, True), (8.0, True)])
+def test_pack_matches_oracle(rng, sdt, ddt, scale, divide):
+    srcs, dst, rows, rows_host = _span_case(rng, sdt, ddt, null_every=5)
+    nat.pack(nat.spans_array(rows), code(sdt), code(ddt), nat.f32(scale), divide, stream())
+    got = to_host(dst)
+    want = np.full(got.shape, SENTINEL_BF16 if ddt == o.BF16 else SENTINEL_F32, dtype=got.dtype)
+    for host, off, n in rows_host:
+        v = o.zeros(n, ddt) if host is None else o.convert(host, sdt, ddt)
+        if scale != 1.0:
+            v = o.div_scalar(v, ddt, int(scale)) if divide else o.mul_scalar(v, ddt, scale)
+        want[off : off + n] = v
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("bdt,gdt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16)])
+@pytest.mark.parametrize("inv_scale", [1.0, 2.0**-16, 1.0 / 3])
+def test_unpack_unscale_found_inf_matches_oracle(rng, bdt, gdt, inv_scale):
+    n_total = sum(SIZES) + 64
+    bucket_host = values(rng, n_total, bdt, specials=False, scale=1e3)
+    bucket = to_dev(bucket_host)
+    grads, rows, expect = [], [], []
+    off = 0
+    for n in SIZES:
+        off += int(rng.integers(0, 3))
+        g = empty_dev(n + 3, gdt)
+        shift = int(rng.integers(0, 3))
+        grads.append(g)
+        rows.append((bucket.data_ptr() + off * esize(bdt), g.data_ptr() + shift * esize(gdt), n))
+        expect.append((g, shift, bucket_host[off : off + n]))
+        off += n
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.unpack(nat.spans_array(rows), code(bdt), code(gdt), nat.f32(inv_scale), flag.data_ptr(), stream())
+    any_bad = False
+    for g, shift, src in expect:
+        v = o.convert(src, bdt, gdt)
+        if inv_scale != 1.0:
+            v = o.mul_scalar(v, gdt, inv_scale)
+        any_bad |= bool((~o.isfinite(v, gdt)).any())
+        got = to_host(g)
+        assert same_bits(got[shift : shift + len(src)], v), first_mismatch(got[shift : shift + len(src)], v)
+        sent = got[:shift].tolist() + got[shift + len(src) :].tolist()
+        assert all(s == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32) for s in sent)
+    assert bool(flag.item()) == any_bad
+
+
+def test_unpack_flags_only_when_nonfinite(rng):
+    clean = to_dev(values(rng, 5000, o.F32, specials=False))
+    out = empty_dev(5000, o.F32)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.unpack(nat.spans_array([(clean.data_ptr(), out.data_ptr(), 5000)]), 0, 0, 1.0, flag.data_ptr(), stream())
+    assert flag.item() == 0
+    for bad in (np.inf, -np.inf, np.nan):
+        h = values(rng, 5000, o.F32, specials=False)
+        h[4321] = bad
+        t = to_dev(h)
+        nat.unpack(nat.spans_array([(t.data_ptr(), out.data_ptr(), 5000)]), 0, 0, 1.0, flag.data_ptr(), stream())
+        assert flag.item() == 1
+        flag.zero_()
+    # fp32 value finite, bf16 result overflows: counts
+    h = np.full(64, 3.40e38, np.float32)
+    t = to_dev(h)
+    ob = empty_dev(64, o.BF16)
+    nat.unpack(nat.spans_array([(t.data_ptr(), ob.data_ptr(), 64)]), 0, 1, 1.0, flag.data_ptr(), stream())
+    assert flag.item() == 1
+
+
+@pytest.mark.parametrize("dt", [o.F32, o.BF16])
+def test_unscale_in_place_matches_oracle(rng, dt):
+    hosts = [values(rng, n, dt, scale=2.0**16) for n in SIZES]
+    devs = [to_dev(h) for h in hosts]
+    rows = [(t.data_ptr(), t.data_ptr(), t.numel()) for t in devs]
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.unscale_found_inf(nat.spans_array(rows), code(dt), nat.f32(2.0**-16), flag.data_ptr(), stream())
+    want, found = o.unscale_found_inf(hosts, [dt] * len(hosts), 2.0**-16)
+    for t, w in zip(devs, want, strict=True):
+        assert same_bits(to_host(t), w), first_mismatch(to_host(t), w)
+    assert bool(flag.item()) == found
+
+
+# ---------------------------------------------------------------------------
+# W-way all-reduce
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dt", [o.F32, o.BF16])
+@pytest.mark.parametrize("W", [1, 2, 3, 4, 5, 8, 16])
+def test_allreduce_sum_matches_oracle(rng, dt, W):
+    runs = [(3, 1), (17, 4096), (5000, 3), (70000, 12345)]  # (offset, numel), increasing
+    extent = runs[-1][0] + runs[-1][1] + 9
+    reps_host = [values(rng, extent, dt, scale=1e-2) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    out = empty_dev(extent, dt)
+    nat.allreduce_sum(
+        [r.data_ptr() for r in reps], code(dt), [a for a, _ in runs], [n for _, n in runs], out.data_ptr(), stream()
+    )
+    got = to_host(out)
+    want = np.full(extent, SENTINEL_BF16 if dt == o.BF16 else SENTINEL_F32, dtype=got.dtype)
+    for a, n in runs:
+        want[a : a + n] = o.allreduce_sum([h[a : a + n] for h in reps_host], dt)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("W,k", [(8, 0), (8, 5), (4, 3)])
+def test_allreduce_in_place_on_one_replica(rng, W, k):
+    n = 1 << 20
+    reps_host = [values(rng, n, o.F32, specials=False) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    nat.allreduce_sum([r.data_ptr() for r in reps], nat.MDX_F32, [0], [n], reps[k].data_ptr(), stream())
+    want = o.allreduce_sum(reps_host, o.F32)
+    assert same_bits(to_host(reps[k]), want)
+    for r in range(W):
+        if r != k:
+            assert same_bits(to_host(reps[r]), reps_host[r])
+
+
+def test_allreduce_full_bucket_exact_sum_property(rng):
+    """A 25 MiB fp32 bucket, W = 8: short-mantissa inputs make the exact sum the answer."""
+    W, n = 8, 25 * 1024 * 1024 // 4
+    ks = rng.integers(-(2**16), 2**16, (W, n), dtype=np.int64)
+    reps = [to_dev((k * 2.0**-10).astype(np.float32)) for k in ks]
+    out = torch.empty(n, dtype=torch.float32, device=DEV)
+    nat.allreduce_sum([r.data_ptr() for r in reps], nat.MDX_F32, [0], [n], out.data_ptr(), stream())
+    want = (ks.sum(axis=0) * 2.0**-10).astype(np.float32)
+    assert np.array_equal(to_host(out), want)
+
+
+# ---------------------------------------------------------------------------
+# reduce-scatter share
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "idt,rdt,sdt",
+    [(o.BF16, o.F32, o.F32), (o.F32, o.F32, o.F32), (o.BF16, o.BF16, o.F32), (o.BF16, o.F32, o.BF16), (o.F32, o.BF16, o.BF16)],
+)
+@pytest.mark.parametrize("W,rank", [(1, 0), (2, 1), (3, 2), (4, 0), (8, 5)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_reduce_scatter_share_matches_oracle(rng, idt, rdt, sdt, W, rank, accumulate):
+    numels = [7, 12, 5, 33, 640, 3, 4099, 1]
+    total = sum(numels)
+    S = (total + W - 1) // W
+    P = S * W
+    grads = []
+    for r in range(W):
+        grads.append([None if (r + i) % 5 == 3 else values(rng, n, idt, scale=1e-3) for i, n in enumerate(numels)])
+    # own pieces: straight from this rank's per-param tensors (as FSDP does)
+    own_devs = [None if g is None else to_dev(g) for g in grads[rank]]
+    lo, hi = rank * S, rank * S + S
+    pieces, off, cursor = [], 0, lo
+    for t, n in zip(own_devs, numels, strict=True):
+        a, b = max(off, lo), min(off + n, hi)
+        if a < b:
+            ptr = 0 if t is None else t.data_ptr() + (a - off) * esize(idt)
+            pieces.append((ptr, a - lo, b - a))
+            cursor = b
+        off += n
+    if cursor < hi:
+        pieces.append((0, cursor - lo, hi - cursor))
+    flats = [o.fsdp_flatten(g, idt, numels, P, idt) for g in grads]
+    peer_devs = [to_dev(f) for f in flats]
+    peers = [peer_devs[r][lo:].data_ptr() for r in range(W)]
+    prev_host = values(rng, S, sdt, specials=False, scale=1e-3)
+    shard = to_dev(prev_host) if accumulate else empty_dev(S, sdt)
+    nat.reduce_scatter_share(
+        nat.pieces_array(pieces), peers, rank, code(idt), code(rdt), True, shard.data_ptr(), code(sdt),
+        accumulate, 1.0, None, stream(),
+    )
+    want = o.fsdp_reduce_scatter_share(grads, idt, numels, rank, rdt, sdt, existing=prev_host if accumulate else None)
+    got = to_host(shard)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+# ---------------------------------------------------------------------------
+# fp32 -> bf16 cast
+# ---------------------------------------------------------------------------
+
+
+def test_cast_structured_sweep():
+    hi = np.arange(1 << 16, dtype=np.uint32) << np.uint32(16)
+    lows = np.array(
+        [0x0000, 0x0001, 0x3FFF, 0x7FFE, 0x7FFF, 0x8000, 0x8001, 0xBFFF, 0xFFFE, 0xFFFF, 0x1234, 0x9ABC],
+        dtype=np.uint32,
+    )
+    x = (hi[:, None] | lows[None, :]).reshape(-1).view(np.float32)
+    src = to_dev(x)
+    dst = empty_dev(x.size, o.BF16)
+    nat.cast_f32_bf16(src.data_ptr(), dst.data_ptr(), x.size, stream())
+    got = to_host(dst)
+    want = o.bf16_from_f32(x)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_cast_matches_golden_and_ties():
+    d = load_golden("bf16_cast.npz")
+    for x, want in ((d["x_bits"].view(np.float32), d["y_bits"]), o.bf16_tie_cases()):
+        src = to_dev(np.ascontiguousarray(x))
+        dst = empty_dev(x.size, o.BF16)
+        nat.cast_f32_bf16(src.data_ptr(), dst.data_ptr(), x.size, stream())
+        assert np.array_equal(to_host(dst), want), first_mismatch(to_host(dst), want)
+
+
+# ---------------------------------------------------------------------------
+# Golden replays through the raw ABI
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz"])
+def test_golden_ddp_replay(name):
+    d = load_golden(name)
+    W, rank = int(d["W"]), int(d["rank"])
+    numels = [int(n) for n in d["numels"]]
+    dt = o.BF16 if "bfloat16" in str(d["dtype"]) else o.F32
+    layout = json.loads(str(d["layout"]))
+    scale = float(d["scale"])
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for b, idxs in enumerate(layout):
+        bn = sum(numels[i] for i in idxs)
+        reps = [torch.zeros(bn + 8, dtype=torch.float32 if dt == o.F32 else torch.bfloat16, device=DEV) for _ in range(W)]
+        keep = []
+        for r in range(W):
+            rows, off = [], 0
+            for i in idxs:
+                g = d.get(f"grad_r{r}_p{i}")
+                t = None if g is None else to_dev(g)
+                keep.append(t)
+                rows.append((0 if t is None else t.data_ptr(), reps[r].data_ptr() + off * esize(dt), numels[i]))
+                off += numels[i]
+            nat.pack(nat.spans_array(rows), code(dt), code(dt), nat.f32(1.0 / W), False, stream())
+        nat.allreduce_sum([x.data_ptr() for x in reps], code(dt), [0], [bn], reps[rank].data_ptr(), stream())
+        got = to_host(reps[rank])[:bn]
+        assert same_bits(got, d[f"reduced_b{b}"]), f"bucket {b}: " + first_mismatch(got, d[f"reduced_b{b}"])
+        rows, outs, off = [], [], 0
+        for i in idxs:
+            g = empty_dev(numels[i], dt)
+            outs.append((i, g))
+            rows.append((reps[rank].data_ptr() + off * esize(dt), g.data_ptr(), numels[i]))
+            off += numels[i]
+        nat.unpack(nat.spans_array(rows), code(dt), code(dt), nat.f32(1.0 / scale), flag.data_ptr(), stream())
+        for i, g in outs:
+            assert same_bits(to_host(g), d[f"unscaled_p{i}"]), f"param {i}"
+    assert bool(flag.item()) == bool(d["found_inf"])
+
+
+# ---------------------------------------------------------------------------
+# ABI argument checks that need device pointers
+# ---------------------------------------------------------------------------
+
+
+def test_allreduce_rejects_partial_overlap():
+    a = torch.zeros(1024, device=DEV)
+    b = torch.zeros(1024, device=DEV)
+    out = a[8:]
+    with pytest.raises(RuntimeError, match="overlaps"):
+        nat.allreduce_sum([a.data_ptr(), b.data_ptr()], nat.MDX_F32, [0], [1000], out.data_ptr(), stream())
+
+
+def test_reduce_scatter_rejects_shard_overlapping_a_peer():
+    peers = torch.zeros((2, 256), device=DEV)
+    own = torch.zeros(128, device=DEV)
+    with pytest.raises(RuntimeError, match="overlaps"):
+        nat.reduce_scatter_share(
+            nat.pieces_array([(own.data_ptr(), 0, 128)]), [0, peers[1].data_ptr()], 0, 0, 0, True,
+            peers[1, 64:].data_ptr(), 0, False, 1.0, None, stream(),
+        )

@@ -1,0 +1,335 @@
+"""Pin the CPU oracle (oracle/gradpath.py) before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself: the
+golden fixtures (torch CPU replays of the reference's ATen chains), torch CPU
+ops on fresh inputs, hand-built answers, the reference's own known-answer
+tests, and invariants that fix the result uniquely.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, first_mismatch, load_golden, same_bits
+from oracle import gradpath as o
+
+
+def _torch_bits(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().astype(np.uint16)
+    return t.numpy().copy()
+
+
+def _from_bits(a: np.ndarray, dtype: str) -> torch.Tensor:
+    if dtype == o.BF16:
+        return torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16)
+    return torch.from_numpy(np.asarray(a, dtype=np.float32).copy())
+
+
+# ---------------------------------------------------------------------------
+# bf16 conversion
+# ---------------------------------------------------------------------------
+
+
+def test_bf16_hand_built_ties_and_specials():
+    x, want = o.bf16_tie_cases()
+    got = o.bf16_from_f32(x)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_bf16_matches_golden_fixture():
+    d = load_golden("bf16_cast.npz")
+    got = o.bf16_from_f32(d["x_bits"].view(np.float32))
+    assert np.array_equal(got, d["y_bits"]), first_mismatch(got, d["y_bits"])
+
+
+def test_bf16_structured_sweep_matches_torch():
+    """Every (sign, exponent, top-7 mantissa) pattern x the low halves that decide rounding."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << np.uint32(16)
+    lows = np.array([0x0000, 0x0001, 0x3FFF, 0x7FFF, 0x8000, 0x8001, 0xBFFF, 0xFFFF], dtype=np.uint32)
+    u = (hi[:, None] | lows[None, :]).reshape(-1)
+    x = u.view(np.float32)
+    got = o.bf16_from_f32(x)
+    want = _torch_bits(torch.from_numpy(x.copy()).to(torch.bfloat16))
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_bf16_widening_is_exact_roundtrip():
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = o.f32_from_bf16(b)
+    nan = np.isnan(f)
+    assert np.array_equal(o.bf16_from_f32(f)[~nan], b[~nan])
+    assert np.all(o.bf16_from_f32(f)[nan] == 0xFFFF)
+
+
+# ---------------------------------------------------------------------------
+# Scalar ops vs torch CPU (the ATen ops the reference calls)
+# ---------------------------------------------------------------------------
+
+
+def _random_with_specials(rng, n: int) -> np.ndarray:
+    x = (rng.standard_normal(n) * 10.0 ** rng.integers(-40, 38, n)).astype(np.float32)
+    pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-40, 3.4e38, 1.17549435e-38], np.float32)
+    idx = rng.integers(0, n, n // 10)
+    x[idx] = pool[rng.integers(0, len(pool), idx.size)]
+    return x
+
+
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("scale", [1.0 / 8, 1.0 / 3, 1.0 / 7, 2.0**-16, 1e-3])
+def test_mul_scalar_matches_torch(rng, dtype, scale):
+    x = o.from_f32(_random_with_specials(rng, 20000), dtype)
+    got = o.mul_scalar(x, dtype, scale)
+    want = _torch_bits(_from_bits(x, dtype).clone().mul_(scale))
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("w", [2, 3, 5, 8])
+def test_div_scalar_matches_torch(rng, dtype, w):
+    x = o.from_f32(_random_with_specials(rng, 20000), dtype)
+    got = o.div_scalar(x, dtype, w)
+    want = _torch_bits(_from_bits(x, dtype).clone().div_(w))
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("src,dst", [(o.F32, o.BF16), (o.BF16, o.F32), (o.F32, o.F32), (o.BF16, o.BF16)])
+def test_convert_matches_torch_copy(rng, src, dst):
+    x = o.from_f32(_random_with_specials(rng, 20000), src)
+    got = o.convert(x, src, dst)
+    tdt = torch.bfloat16 if dst == o.BF16 else torch.float32
+    want = _torch_bits(torch.empty(x.size, dtype=tdt).copy_(_from_bits(x, src)))
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("W", [2, 3, 8, 16])
+def test_allreduce_sum_matches_torch_sequential_add(rng, dtype, W):
+    contribs = [o.from_f32(_random_with_specials(rng, 5000), dtype) for _ in range(W)]
+    got = o.allreduce_sum(contribs, dtype)
+    acc = _from_bits(contribs[0], dtype).clone()
+    for c in contribs[1:]:
+        acc = acc + _from_bits(c, dtype) if dtype == o.BF16 else acc.add_(_from_bits(c, dtype))
+    assert same_bits(got, _torch_bits(acc)), first_mismatch(got, _torch_bits(acc))
+
+
+@pytest.mark.parametrize("W", [2, 3, 7, 8, 16])
+def test_allreduce_sum_of_short_mantissa_copies_is_exact(rng, W):
+    """Inputs k * 2^-10 with |k| < 2^16 keep every partial sum exact in fp32, so the
+    rank-ordered sum of W distinct contributions equals their exact integer sum."""
+    ks = rng.integers(-(2**16), 2**16, (W, 10000))
+    contribs = [(k * 2.0**-10).astype(np.float32) for k in ks]
+    got = o.allreduce_sum(contribs, o.F32)
+    assert np.array_equal(got, (ks.sum(axis=0) * 2.0**-10).astype(np.float32))
+
+
+def test_unscale_found_inf_matches_torch(rng):
+    grads = [_random_with_specials(rng, n) for n in (17, 1000, 3)]
+    grads.append(np.ones(8, np.float32))
+    dts = [o.F32] * len(grads)
+    got, found = o.unscale_found_inf(grads, dts, 1.0 / 65536)
+    f = torch.zeros(1)
+    for g, want in zip(grads, got, strict=True):
+        t = torch.from_numpy(g.copy()).mul_(1.0 / 65536)
+        f += (~torch.isfinite(t)).any().to(f.dtype)
+        assert same_bits(want, t.numpy())
+    assert found == bool(f.item() > 0)
+    _, found_clean = o.unscale_found_inf([np.ones(4, np.float32)], [o.F32], 0.5)
+    assert not found_clean
+
+
+def test_found_inf_sees_bf16_overflow_of_a_finite_fp32_value():
+    big = np.array([3.40e38], np.float32)  # finite in fp32, above the bf16 rounding threshold 3.396e38
+    b = o.convert(big, o.F32, o.BF16)
+    _, found = o.unscale_found_inf([b], [o.BF16], 1.0)
+    assert found
+
+
+# ---------------------------------------------------------------------------
+# DDP bucketer
+# ---------------------------------------------------------------------------
+
+
+def _check_greedy_partition(nbytes, cap_mb, buckets):
+    """The three properties that define the greedy reverse-order partition uniquely."""
+    cap = int(cap_mb * 1024 * 1024)
+    flat = [i for b in buckets for i in b]
+    assert flat == list(reversed(range(len(nbytes)))), "buckets must tile the reversed parameter list"
+    for b in buckets:
+        assert len(b) >= 1
+        assert sum(nbytes[i] for i in b) <= cap or len(b) == 1, "over cap without being a singleton"
+    for b, nxt in zip(buckets, buckets[1:]):
+        assert sum(nbytes[i] for i in b) + nbytes[nxt[0]] > cap, "a flush happened that the cap did not force"
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_build_buckets_is_the_greedy_partition(seed):
+    r = np.random.default_rng(seed)
+    nbytes = [int(x) for x in r.integers(1, 5000, r.integers(1, 40))]
+    cap_mb = float(r.choice([1e-6, 1e-3, 2e-3, 5e-3, 1e6]))
+    _check_greedy_partition(nbytes, cap_mb, o.build_buckets(nbytes, cap_mb))
+
+
+def test_build_buckets_brute_force_tiny():
+    """Exhaustive: every list of up to 6 sizes in {1,2,3} with caps 0..6 bytes."""
+    import itertools
+
+    for n in range(1, 7):
+        for sizes in itertools.product([1, 2, 3], repeat=n):
+            for cap in range(0, 7):
+                cap_mb = cap / (1024 * 1024)
+                _check_greedy_partition(list(sizes), cap_mb, o.build_buckets(list(sizes), cap_mb))
+
+
+def test_cap_one_byte_gives_one_bucket_per_param_and_huge_cap_one_bucket():
+    nbytes = [4 * n for n in (10, 1, 300, 7)]
+    assert o.build_buckets(nbytes, 1e-6) == [[3], [2], [1], [0]]  # int(1.048576) = 1 byte
+    assert o.build_buckets(nbytes, 1e6) == [[3, 2, 1, 0]]
+
+
+def test_reference_layout_invariants_on_the_test_gpt():
+    """tests/test_ddp.py:103-121 on GPTConfig(vocab=64, block=16, n_layer=2, n_embd=32), cap 0.05 MB."""
+    from minidist import workloads as w
+
+    specs = w.gpt_specs(n_layer=2, n_embd=32, vocab=64, ctx=16, untied_head=True)
+    nbytes = [s.nbytes for s in specs]
+    buckets = o.build_buckets(nbytes, 0.05)
+    assert len(buckets) > 1
+    assert buckets[0][0] == len(specs) - 1  # bucket 0 starts from the last parameter
+    _check_greedy_partition(nbytes, 0.05, buckets)
+
+
+def test_cfg_bucket_counts():
+    from minidist import workloads as w
+
+    s1 = w.gpt_specs(**w.GPT2_SMALL)
+    assert w.total_numel(s1) == 124_439_808
+    lay = o.build_buckets([s.nbytes for s in s1], 25.0)
+    # reverse order ends ..., wte (147.24 MiB, alone), wpe (3 MiB, alone)
+    assert len(lay) == 18 and lay[-2] == [1] and lay[-1] == [0]
+    s2 = w.gpt_specs(**w.GPT2_MEDIUM)
+    assert w.total_numel(s2) == 354_823_168
+    assert [len(o.build_buckets([s.nbytes for s in s2], c)) for c in (1e-6, 25.0, 1e6)] == [292, 74, 1]
+    assert w.total_numel(w.llama_specs()) == 6_738_415_616
+
+
+def _golden_ddp_inputs(d):
+    W, rank = int(d["W"]), int(d["rank"])
+    numels = [int(n) for n in d["numels"]]
+    dt = o.BF16 if "bfloat16" in str(d["dtype"]) else o.F32
+    grads = [[d.get(f"grad_r{r}_p{i}") for i in range(len(numels))] for r in range(W)]
+    return W, rank, numels, dt, grads
+
+
+@pytest.mark.parametrize("name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz"])
+def test_ddp_pipeline_matches_golden(name):
+    d = load_golden(name)
+    W, rank, numels, dt, grads = _golden_ddp_inputs(d)
+    res = o.ddp_pipeline(grads, [dt] * len(numels), numels, float(d["cap_mb"]), rank, 1.0 / float(d["scale"]))
+    assert res["layout"] == json.loads(str(d["layout"]))
+    for b, red in enumerate(res["reduced"]):
+        assert same_bits(red, d[f"reduced_b{b}"]), f"bucket {b}: " + first_mismatch(red, d[f"reduced_b{b}"])
+    for i, g in enumerate(res["grads"]):
+        assert same_bits(g, d[f"unscaled_p{i}"]), f"param {i}: " + first_mismatch(g, d[f"unscaled_p{i}"])
+    assert res["found_inf"] == bool(d["found_inf"])
+
+
+def test_ddp_pipeline_is_cap_invariant(rng):
+    """Elementwise fixed-order arithmetic: bucketing cannot change any value (cfg2's property)."""
+    numels = [int(n) for n in rng.integers(1, 300, 15)]
+    W = 4
+    grads = [[(rng.standard_normal(n) * 1e-3).astype(np.float32) for n in numels] for _ in range(W)]
+    outs = [o.ddp_pipeline(grads, [o.F32] * len(numels), numels, cap, 2, 2.0**-16)["grads"] for cap in (1e-6, 1e-3, 1e6)]
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other, strict=True):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# Loss scaler
+# ---------------------------------------------------------------------------
+
+
+def test_scaler_known_answers():
+    kat = json.loads((GOLDEN / "scaler_kat.json").read_text())
+    s = o.ScalerState(scale=kat["overflow_skips"]["init_scale"])
+    stepped = s.step(True)
+    s.update(True)
+    assert not stepped and s.scale == 512.0 and s.num_skipped == 1
+
+    k = kat["clean_growth"]
+    s = o.ScalerState(scale=k["init_scale"], growth_interval=k["growth_interval"])
+    for f in k["found"]:
+        assert s.step(f)
+        s.update(f)
+    assert s.scale == k["scale_after"] and s.num_skipped == 0
+
+    k = kat["mixed_history"]
+    s = o.ScalerState(scale=k["init_scale"], growth_interval=k["growth_interval"])
+    for f in k["found"]:
+        s.step(f)
+        s.update(f)
+    assert s.scale == k["scale_after"]
+    assert s.history == [2048.0, 2048.0, 4096.0, 2048.0, 1024.0]
+
+
+def test_scaler_min_scale_floor():
+    s = o.ScalerState(scale=2.0, min_scale=1.0)
+    for _ in range(5):
+        s.update(True)
+    assert s.scale == 1.0
+
+
+# ---------------------------------------------------------------------------
+# FSDP unit
+# ---------------------------------------------------------------------------
+
+
+def test_fsdp_layout_closed_form_and_invariants():
+    from minidist import workloads as w
+
+    assert o.fsdp_layout([7, 12, 5], 4) == (24, 6, 24)
+    assert o.fsdp_layout([7, 12, 6], 4) == (25, 7, 28)
+    blk = w.gpt_block_specs(0, 1600)
+    total, S, P = o.fsdp_layout([s.numel for s in blk], 8)
+    assert (total, S, P) == (30_740_800, 3_842_600, 30_740_800)
+    # tests/test_fsdp.py:130-149: one unit per block + root, local <= 1.25 * full / W
+    specs = w.gpt_specs(n_layer=3, n_embd=32, vocab=64, ctx=16, untied_head=True)
+    units = [[s.numel for s in specs if s.name.startswith(f"blocks.{i}.")] for i in range(3)]
+    units.append([s.numel for s in specs if not s.name.startswith("blocks.")])
+    full = sum(s.numel for s in specs)
+    for W in (2, 4):
+        local = sum(o.fsdp_layout(u, W)[1] for u in units)
+        assert local <= full / W * 1.25
+    assert len(units) == 3 + 1
+
+
+@pytest.mark.parametrize(
+    "name", ["fsdp_bf16_w4.npz", "fsdp_bf16_w3.npz", "fsdp_f32_w2.npz", "fsdp_bf16red_w4.npz"]
+)
+def test_fsdp_reduce_scatter_and_cast_match_golden(name):
+    d = load_golden(name)
+    W = int(d["W"])
+    numels = [int(n) for n in d["numels"]]
+    gdt = o.BF16 if "bfloat16" in str(d["grad_dtype"]) else o.F32
+    rdt = o.BF16 if "bfloat16" in str(d["reduce_dtype"]) else o.F32
+    grads = [[d.get(f"grad_r{r}_p{i}") for i in range(len(numels))] for r in range(W)]
+    S = int(d["S"])
+    for rank in range(W):
+        got = o.fsdp_reduce_scatter_share(grads, gdt, numels, rank, rdt, o.F32)
+        assert same_bits(got, d[f"shard_grad_r{rank}"]), first_mismatch(got, d[f"shard_grad_r{rank}"])
+        acc = o.fsdp_reduce_scatter_share(grads, gdt, numels, rank, rdt, o.F32, existing=d[f"prev_r{rank}"])
+        assert same_bits(acc, d[f"shard_grad_acc_r{rank}"])
+        cast = o.fsdp_gather_cast(d["master_flat"][rank * S : (rank + 1) * S], o.BF16)
+        assert np.array_equal(cast, d[f"gather_cast_r{rank}"])
+
+
+def test_fsdp_world1_is_plain_flatten(rng):
+    numels = [3, 4]
+    g = [[rng.standard_normal(n).astype(np.float32) for n in numels]]
+    got = o.fsdp_reduce_scatter_share(g, o.F32, numels, 0)
+    assert np.array_equal(got, np.concatenate(g[0]))
