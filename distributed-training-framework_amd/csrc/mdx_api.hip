@@ -121,49 +121,56 @@ bool any_overlap(const void* a, int64_t na, const void* b, int64_t nb) {
 // reduce family
 // ---------------------------------------------------------------------------
 
-int run_reduce(const mdx_piece* pieces, int n_pieces, int world, int in_dt, int acc_dt, int out_dt,
-               const ReduceParams& params, hipStream_t stream) {
-  const int E = reduce_frag_elems(in_dt, out_dt);
-  const int U = reduce_unroll(world);
+// Lays out pieces into dispatches.  `grad_size` > 0 adds each piece's grad
+// pointer to the alignment requirement (fused unpack).
+template <typename Launch>
+int run_pieces(const mdx_piece* pieces, void* const* grads, int n_pieces, const ReduceParams& params,
+               int in_size, int out_size, int grad_size, int E, int U, Launch&& launch) {
   const int64_t VPB = int64_t(kBlock) * U;
   const int64_t EPB = VPB * E;
-  const int is = dtype_size(in_dt), os = dtype_size(out_dt);
-
   PieceBatch b;
   memset(&b, 0, sizeof(b));
   auto flush = [&]() -> int {
     if (b.count == 0) return MDX_OK;
-    const int rc = status(launch_reduce(in_dt, acc_dt, out_dt, world, b, params, stream));
+    const int rc = status(launch(b));
     memset(&b, 0, sizeof(b));
     return rc;
   };
-
   for (int i = 0; i < n_pieces; ++i) {
     const mdx_piece& pc = pieces[i];
     const char* own = static_cast<const char*>(pc.own);
+    char* grad = grads ? static_cast<char*>(grads[i]) : nullptr;
     for (int64_t done = 0; done < pc.numel; done += kMaxRunElems) {
       const int64_t n = std::min<int64_t>(kMaxRunElems, pc.numel - done);
       const int64_t pos = pc.pos + done;
-      uintptr_t ptrs[MDX_MAX_WORLD + 2];
-      int sizes[MDX_MAX_WORLD + 2];
+      uintptr_t ptrs[MDX_MAX_WORLD + 3];
+      int sizes[MDX_MAX_WORLD + 3];
       int np = 0;
-      const void* ro = own ? own + done * is : nullptr;
+      const void* ro = own ? own + done * in_size : nullptr;
+      void* rg = grad ? grad + done * grad_size : nullptr;
       if (ro) {
         ptrs[np] = addr(ro);
-        sizes[np++] = is;
+        sizes[np++] = in_size;
       }
-      for (int r = 0; r < world; ++r) {
+      for (int r = 0; r < params.world; ++r) {
         if (r == params.rank) continue;
-        ptrs[np] = addr(params.peer[r]) + uintptr_t(pos) * uintptr_t(is);
-        sizes[np++] = is;
+        ptrs[np] = addr(params.peer[r]) + uintptr_t(pos) * uintptr_t(in_size);
+        sizes[np++] = in_size;
       }
-      ptrs[np] = addr(params.out) + uintptr_t(pos) * uintptr_t(os);
-      sizes[np++] = os;
+      if (params.out) {
+        ptrs[np] = addr(params.out) + uintptr_t(pos) * uintptr_t(out_size);
+        sizes[np++] = out_size;
+      }
+      if (rg) {
+        ptrs[np] = addr(rg);
+        sizes[np++] = grad_size;
+      }
       const int head = aligned_head(ptrs, sizes, np, E, n);
       const int k = b.count;
       b.own[k] = ro;
       b.pos[k] = pos;
       b.numel[k] = n;
+      b.grad[k] = rg;
       b.head[k] = head;
       b.first_block[k + 1] = b.first_block[k] + run_blocks(n, head, E, VPB, EPB);
       b.count = k + 1;
@@ -174,6 +181,26 @@ int run_reduce(const mdx_piece* pieces, int n_pieces, int world, int in_dt, int 
     }
   }
   return flush();
+}
+
+// Validates W replica bases and increasing, non-overlapping runs; returns the
+// extent (one past the last element) through `end`.
+int check_runs(const void* const* replicas, int world, const int64_t* offs, const int64_t* nums,
+               int n_runs, int64_t* end, bool* any) {
+  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
+  if (n_runs < 0 || replicas == nullptr) return MDX_EINVAL;
+  *end = 0;
+  *any = false;
+  for (int k = 0; k < n_runs; ++k) {
+    if (offs[k] < 0 || nums[k] < 0 || offs[k] < *end) return MDX_EINVAL;
+    *end = offs[k] + nums[k];
+    *any = *any || nums[k] > 0;
+  }
+  if (!*any) return MDX_OK;
+  for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
+  }
+  return MDX_OK;
 }
 
 bool is_pow2(int w) { return w > 0 && (w & (w - 1)) == 0; }
@@ -242,21 +269,14 @@ int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stre
 int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,
                       const int64_t* numels, int n_runs, void* out, void* stream) {
   if (!valid_dtype(dtype)) return MDX_EDTYPE;
-  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
-  if (n_runs < 0 || replicas == nullptr) return MDX_EINVAL;
   if (n_runs > 0 && (offsets == nullptr || numels == nullptr)) return MDX_EINVAL;
-  const int es = dtype_size(dtype);
   int64_t end = 0;
   bool any = false;
-  for (int k = 0; k < n_runs; ++k) {
-    if (offsets[k] < 0 || numels[k] < 0 || offsets[k] < end) return MDX_EINVAL;
-    end = offsets[k] + numels[k];
-    any = any || numels[k] > 0;
-  }
-  if (!any) return MDX_OK;
+  int rc = check_runs(replicas, world, offsets, numels, n_runs, &end, &any);
+  if (rc != MDX_OK || !any) return rc;
   if (out == nullptr) return MDX_EINVAL;
+  const int es = dtype_size(dtype);
   for (int r = 0; r < world; ++r) {
-    if (replicas[r] == nullptr) return MDX_EINVAL;
     // Same base = the in-place case; any other overlap of the reduced extent is rejected.
     if (replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
   }
@@ -264,24 +284,85 @@ int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const i
   memset(&p, 0, sizeof(p));
   for (int r = 0; r < world; ++r) p.peer[r] = replicas[r];
   p.out = out;
-  p.rank = 0;
-  p.flags = 0;
+  p.world = world;
+  p.rank = 0;  // replica 0 is read through the pieces, the others through peer[r] + pos
   p.pre = 1.0f;
   p.inv_scale = 1.0f;
-  // Rank 0's data is read through the pieces, the others through peer[r] + pos.
   const char* base0 = static_cast<const char*>(replicas[0]);
+  const int E = frag_elems(es, es);
+  const int U = allreduce_unroll(world, E * es);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
   mdx_piece pieces[kRunsPerLaunch];
   int np = 0;
+  auto launch = [&](const PieceBatch& b) { return launch_allreduce(dtype, dtype, false, world, b, p, st); };
   for (int k = 0; k < n_runs; ++k) {
     if (numels[k] == 0) continue;
     pieces[np++] = mdx_piece{base0 + offsets[k] * es, offsets[k], numels[k]};
     if (np == kRunsPerLaunch) {
-      const int rc = run_reduce(pieces, np, world, dtype, dtype, dtype, p, static_cast<hipStream_t>(stream));
+      rc = run_pieces(pieces, nullptr, np, p, es, es, 0, E, U, launch);
       if (rc != MDX_OK) return rc;
       np = 0;
     }
   }
-  return run_reduce(pieces, np, world, dtype, dtype, dtype, p, static_cast<hipStream_t>(stream));
+  return run_pieces(pieces, nullptr, np, p, es, es, 0, E, U, launch);
+}
+
+int mdx_allreduce_unpack(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs,
+                         int n_runs, void* out, int grad_dtype, float inv_scale, int32_t* found_inf,
+                         void* stream) {
+  if (!valid_dtype(dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
+  if (n_runs < 0 || (n_runs > 0 && runs == nullptr) || replicas == nullptr) return MDX_EINVAL;
+  const int es = dtype_size(dtype), gs = dtype_size(grad_dtype);
+  int64_t end = 0;
+  bool any = false;
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].offset < 0 || runs[k].numel < 0 || runs[k].offset < end) return MDX_EINVAL;
+    if (runs[k].numel > 0 && runs[k].grad == nullptr) return MDX_EINVAL;
+    end = runs[k].offset + runs[k].numel;
+    any = any || runs[k].numel > 0;
+  }
+  if (!any) return MDX_OK;
+  for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
+    if (out && replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
+  }
+  for (int k = 0; k < n_runs; ++k) {
+    const int64_t gb = runs[k].numel * gs;
+    for (int r = 0; r < world; ++r) {
+      if (any_overlap(runs[k].grad, gb, replicas[r], end * es)) return MDX_EALIAS;
+    }
+    if (out && any_overlap(runs[k].grad, gb, out, end * es)) return MDX_EALIAS;
+  }
+  ReduceParams p;
+  memset(&p, 0, sizeof(p));
+  for (int r = 0; r < world; ++r) p.peer[r] = replicas[r];
+  p.out = out;
+  p.world = world;
+  p.rank = 0;
+  p.pre = 1.0f;
+  p.inv_scale = inv_scale;
+  p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
+  p.found_inf = found_inf;
+  const char* base0 = static_cast<const char*>(replicas[0]);
+  const int E = frag_elems(es, gs);
+  const int U = allreduce_unroll(world, E * es);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](const PieceBatch& b) { return launch_allreduce(dtype, grad_dtype, true, world, b, p, st); };
+  mdx_piece pieces[kRunsPerLaunch];
+  void* grads[kRunsPerLaunch];
+  int np = 0;
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].numel == 0) continue;
+    pieces[np] = mdx_piece{base0 + runs[k].offset * es, runs[k].offset, runs[k].numel};
+    grads[np++] = runs[k].grad;
+    if (np == kRunsPerLaunch) {
+      const int rc = run_pieces(pieces, grads, np, p, es, es, gs, E, U, launch);
+      if (rc != MDX_OK) return rc;
+      np = 0;
+    }
+  }
+  return run_pieces(pieces, grads, np, p, es, es, gs, E, U, launch);
 }
 
 int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const* peers, int world,
@@ -337,10 +418,17 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   }
   if (accumulate) flags |= kRedAccumulate;
   if (inv_scale != 1.0f) flags |= kRedUnscale;
-  if (found_inf) flags |= kRedCheck;
   p.flags = flags;
-  return run_reduce(own, n_own, world, in_dtype, reduce_dtype, shard_dtype, p,
-                    static_cast<hipStream_t>(stream));
+  p.world = world;
+  const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
+  const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
+  const int E = frag_elems(is, os);
+  const int U = share_unroll(wmax, E * is);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](const PieceBatch& b) {
+    return launch_share(in_dtype, reduce_dtype, shard_dtype, wmax, b, p, st);
+  };
+  return run_pieces(own, nullptr, n_own, p, is, os, 0, E, U, launch);
 }
 
 }  // extern "C"

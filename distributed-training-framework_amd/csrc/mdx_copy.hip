@@ -1,37 +1,40 @@
 // Multi-tensor copy / convert / scale kernel: the pack, unpack (+ fused
 // unscale and found-inf), in-place unscale and fp32->bf16 cast entry points
-// all run this one kernel with different dtype pairs and flags.
+// all run this one kernel with different dtype pairs and modes.
 //
-// Per element:  v = cvt_dst(src);  if (scale) v = rnd_dst(f32(v) * scale)
-//                                  (or / scale for the FSDP pre-division);
-//               dst = v;           if (check) bad |= !isfinite(v)
-// which is `dst.copy_(src)` followed by `dst.mul_(scale)` in ATen's op order.
+// Per element:  v = cvt_dst(src);  SCALE: v = rnd_dst(f32(v) * s)  or  rnd_dst(f32(v) / s)
+//               dst = v;           CHECK: bad |= !isfinite(v)
+// which is `dst.copy_(src)` followed by `dst.mul_(s)` / `dst.div_(s)` in
+// ATen's op order.  The scaling and the check are compile-time modes, so a
+// plain pack or unpack carries no dead arithmetic.
 //
 // Layout of the work: each span is cut into chunks of kBlock * U fragments
 // (a fragment = E elements = one or two 16-byte vectors).  Lane t of chunk c
 // handles fragments c*VPB + u*kBlock + t, so every vector instruction of a
-// wave touches 64 consecutive 16-byte vectors.  A span whose src and dst
-// cannot both be brought to 16-byte alignment by the same element offset is
-// processed with coalesced scalar accesses instead.
+// wave touches 64 consecutive 16-byte vectors; all U fragments are loaded
+// (non-temporal: each byte is read once per step) before the first store.
+// A span whose src and dst cannot both be brought to 16-byte alignment by the
+// same element offset is processed with coalesced scalar accesses instead.
 #include "mdx_internal.h"
 
 namespace mdx {
 namespace {
 
-template <typename S, typename D>
+enum : int { kScaleNone = 0, kScaleMul = 1, kScaleDiv = 2 };
+
+template <typename S, typename D, int SCALE, bool CHECK>
 struct CopyOp {
   float scale;
-  int32_t flags;
   __device__ __forceinline__ D operator()(S x, bool& bad) const {
     D v = Cvt<S, D>::run(x);
-    if (flags & kCopyScale) v = from_f32<D>(to_f32(v) * scale);
-    if (flags & kCopyDivide) v = from_f32<D>(to_f32(v) / scale);
-    if (flags & kCopyCheck) bad |= !is_finite(v);
+    if constexpr (SCALE == kScaleMul) v = from_f32<D>(to_f32(v) * scale);
+    if constexpr (SCALE == kScaleDiv) v = from_f32<D>(to_f32(v) / scale);
+    if constexpr (CHECK) bad |= !is_finite(v);
     return v;
   }
 };
 
-template <typename S, typename D>
+template <typename S, typename D, int SCALE, bool CHECK>
 __global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p) {
   constexpr int E = frag_elems(int(sizeof(S)), int(sizeof(D)));
   constexpr int U = kCopyElemsPerThread / E;
@@ -48,7 +51,7 @@ __global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p)
   const int32_t h = b.head[s];
   const int t = int(threadIdx.x);
   const bool zero_src = (src == nullptr);
-  const CopyOp<S, D> op{p.scale, p.flags};
+  const CopyOp<S, D, SCALE, CHECK> op{p.scale};
   bool bad = false;
 
   if (h >= 0) {
@@ -91,23 +94,38 @@ __global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p)
       dst[i] = op(x, bad);
     }
   } else {
+    S in[kCopyElemsPerThread];
 #pragma unroll
     for (int k = 0; k < kCopyElemsPerThread; ++k) {
       const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
-      if (i < n) {
-        const S x = zero_src ? zero_of<S>() : src[i];
-        dst[i] = op(x, bad);
-      }
+      in[k] = (i < n && !zero_src) ? src[i] : zero_of<S>();
+    }
+#pragma unroll
+    for (int k = 0; k < kCopyElemsPerThread; ++k) {
+      const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
+      if (i < n) dst[i] = op(in[k], bad);
     }
   }
-  if (p.flags & kCopyCheck) flag_nonfinite(bad, p.found_inf);
+  if constexpr (CHECK) flag_nonfinite(bad, p.found_inf);
+}
+
+template <typename S, typename D, int SCALE, bool CHECK>
+hipError_t launch4(const SpanBatch& b, const CopyParams& p, hipStream_t stream) {
+  const int blocks = b.first_block[b.count];
+  hipLaunchKernelGGL((copy_kernel<S, D, SCALE, CHECK>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
+  return hipGetLastError();
 }
 
 template <typename S, typename D>
 hipError_t launch_typed(const SpanBatch& b, const CopyParams& p, hipStream_t stream) {
-  const int blocks = b.first_block[b.count];
-  hipLaunchKernelGGL((copy_kernel<S, D>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
-  return hipGetLastError();
+  const bool check = (p.flags & kCopyCheck) != 0;
+  if (p.flags & kCopyScale) {
+    return check ? launch4<S, D, kScaleMul, true>(b, p, stream) : launch4<S, D, kScaleMul, false>(b, p, stream);
+  }
+  if (p.flags & kCopyDivide) {
+    return check ? launch4<S, D, kScaleDiv, true>(b, p, stream) : launch4<S, D, kScaleDiv, false>(b, p, stream);
+  }
+  return check ? launch4<S, D, kScaleNone, true>(b, p, stream) : launch4<S, D, kScaleNone, false>(b, p, stream);
 }
 
 }  // namespace

@@ -170,13 +170,14 @@ hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const C
 int copy_frag_elems(int src_dtype, int dst_dtype);
 
 // ----------------------------------------------------------------------------
-// W-way reduction (all-reduce sum, reduce-scatter share)
+// W-way reductions (all-reduce sum, fused all-reduce + unpack, reduce-scatter share)
 // ----------------------------------------------------------------------------
 
 struct PieceBatch {
   const void* own[kRunsPerLaunch];
   int64_t pos[kRunsPerLaunch];
   int64_t numel[kRunsPerLaunch];
+  void* grad[kRunsPerLaunch];  // fused unpack destination (all-reduce + unpack only)
   int32_t head[kRunsPerLaunch];
   int32_t first_block[kRunsPerLaunch + 1];
   int32_t count;
@@ -186,13 +187,13 @@ enum : int32_t {
   kRedPreMul = 1,      // every contribution * pre, rounded to the reduce dtype
   kRedPreDiv = 2,      // every contribution / pre, rounded to the reduce dtype
   kRedAccumulate = 4,  // out = out + result (rounded to the out dtype)
-  kRedUnscale = 8,     // out value * inv_scale, rounded to the out dtype
-  kRedCheck = 16,      // found-inf on the stored value
+  kRedUnscale = 8,     // stored value * inv_scale, rounded to its dtype
 };
 
 struct ReduceParams {
   const void* peer[MDX_MAX_WORLD];
-  void* out;
+  void* out;  // may be NULL for the fused unpack (bucket not written)
+  int32_t world;
   int32_t rank;
   int32_t flags;
   float pre;
@@ -200,13 +201,21 @@ struct ReduceParams {
   int32_t* found_inf;
 };
 
-// Fragments kept in flight per lane and contribution: W * U 16-byte loads per
-// lane before the first add (16 for W = 8).
-constexpr int reduce_unroll(int world) { return world <= 4 ? 4 : (world <= 8 ? 2 : 1); }
+// Fragments per lane and contribution kept in flight: about 128 VGPRs of
+// loads for the all-reduce (32 16-byte loads per lane at W = 8), half that
+// for the share kernel, whose width is only bounded at compile time.
+constexpr int clamp_unroll(int u) { return u < 1 ? 1 : (u > 8 ? 8 : u); }
+constexpr int allreduce_unroll(int world, int frag_bytes) {
+  return clamp_unroll(128 / (world * (frag_bytes / 4)));
+}
+constexpr int share_unroll(int wmax, int frag_bytes) { return clamp_unroll(64 / (wmax * (frag_bytes / 4))); }
 
-hipError_t launch_reduce(int in_dtype, int acc_dtype, int out_dtype, int world, const PieceBatch& b,
-                         const ReduceParams& p, hipStream_t stream);
-int reduce_frag_elems(int in_dtype, int out_dtype);
+// Host-side dispatch into the instantiating translation units.
+hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                            const ReduceParams& p, hipStream_t stream);
+hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, const PieceBatch& b,
+                        const ReduceParams& p, hipStream_t stream);
+int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world);
 
 inline int dtype_size(int dt) { return dt == MDX_BF16 ? 2 : 4; }
 

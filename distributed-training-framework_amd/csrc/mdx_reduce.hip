@@ -1,32 +1,36 @@
-// Dispatch of the W-way reduction to its per-dtype-triple instantiations.
+// Dispatch of the W-way reductions to their per-dtype instantiations.
 #include "mdx_internal.h"
 
 namespace mdx {
 
-hipError_t launch_reduce_fff(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_bbb(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_bff(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_bfb(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_ffb(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_bbf(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_fbb(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
-hipError_t launch_reduce_fbf(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_f32(int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                                const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_bf16(int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                                 const ReduceParams& p, hipStream_t stream);
+hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
+                             hipStream_t stream);
+hipError_t launch_share_generic(int in_dtype, int acc_dtype, int out_dtype, const PieceBatch& b,
+                                const ReduceParams& p, hipStream_t stream);
 
-int reduce_frag_elems(int in_dtype, int out_dtype) {
-  return frag_elems(dtype_size(in_dtype), dtype_size(out_dtype));
+hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                            const ReduceParams& p, hipStream_t stream) {
+  if (dtype == MDX_BF16) return launch_allreduce_bf16(grad_dtype, unpack, world, b, p, stream);
+  return launch_allreduce_f32(grad_dtype, unpack, world, b, p, stream);
 }
 
-hipError_t launch_reduce(int in_dtype, int acc_dtype, int out_dtype, int world, const PieceBatch& b,
-                         const ReduceParams& p, hipStream_t stream) {
-  const bool ib = in_dtype == MDX_BF16, ab = acc_dtype == MDX_BF16, ob = out_dtype == MDX_BF16;
-  if (!ib && !ab && !ob) return launch_reduce_fff(world, b, p, stream);
-  if (ib && !ab && !ob) return launch_reduce_bff(world, b, p, stream);
-  if (ib && ab && ob) return launch_reduce_bbb(world, b, p, stream);
-  if (ib && !ab && ob) return launch_reduce_bfb(world, b, p, stream);
-  if (!ib && !ab && ob) return launch_reduce_ffb(world, b, p, stream);
-  if (ib && ab && !ob) return launch_reduce_bbf(world, b, p, stream);
-  if (!ib && ab && ob) return launch_reduce_fbb(world, b, p, stream);
-  return launch_reduce_fbf(world, b, p, stream);
+static bool fast_triple(int in_dtype, int acc_dtype, int out_dtype) {
+  return acc_dtype == MDX_F32 && out_dtype == MDX_F32;
+}
+
+int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world) {
+  if (!fast_triple(in_dtype, acc_dtype, out_dtype)) return 16;
+  return world <= 2 ? 2 : (world <= 4 ? 4 : (world <= 8 ? 8 : 16));
+}
+
+hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, const PieceBatch& b,
+                        const ReduceParams& p, hipStream_t stream) {
+  if (fast_triple(in_dtype, acc_dtype, out_dtype)) return launch_share_fast(in_dtype, wmax, b, p, stream);
+  return launch_share_generic(in_dtype, acc_dtype, out_dtype, b, p, stream);
 }
 
 }  // namespace mdx

@@ -1,54 +1,40 @@
+// W-way streaming reductions over contributions resident in HBM (kernel
+// templates; instantiated per dtype by the mdx_reduce_*.hip translation units).
+//
+// allreduce_kernel<T, G, W, UNPACK>: DDP's bucket all-reduce.  For element j
+// of a piece (replica position p = pos + j):
+//     acc = x_0[p]; acc = rnd_T(acc + x_r[p]) for r = 1..W-1      (rank order)
+//     out[p] = acc                                  (the in-place all-reduce)
+//   UNPACK additionally writes the bucket slice straight into the gradient,
+//   with the loss scaler's epilogue:
+//     g = cvt_G(acc); g = rnd_G(g * inv_scale); grad[j] = g; bad |= !isfinite(g)
+//   which is scatter_from_buffer's copy_ followed by unscale_'s mul_ and
+//   isfinite, fused so the bucket is not read back.
+//
+// share_kernel<In, Acc, Out, WMAX>: FSDP's reduce-scatter share, runtime
+// W <= WMAX.  x_r = cvt_Acc(contribution_r[p]); x_r = rnd_Acc(x_r * pre | x_r / pre);
+// acc = rank-ordered sum in Acc; y = cvt_Out(acc); y = rnd_Out(out + y) when
+// accumulating; optional unscale + found-inf epilogue.  The pre-scale and the
+// accumulate are compile-time variants selected once per workgroup.
+//
+// Every contribution is read once per step, so every load is non-temporal;
+// each lane keeps U fragments of all W contributions in flight before the
+// first add (U * W = 32 16-byte loads for the all-reduce).
 #pragma once
-// W-way streaming reduction over contributions resident in HBM (kernel template;
-// instantiated per dtype triple by the mdx_reduce_*.hip translation units).
-//
-// For element j of a piece (reduced-vector position p = pos + j):
-//   x_r  = cvt_acc(contribution_r[p])          r = 0..W-1, own data for r == rank
-//   x_r  = rnd_acc(x_r * pre) | rnd_acc(x_r / pre)   (optional pre-scale)
-//   acc  = x_0; acc = rnd_acc(acc + x_r) for r = 1..W-1   (fixed rank order)
-//   y    = cvt_out(acc); y = rnd_out(out[p] + y) (accumulate); y = rnd_out(y * inv)
-//   out[p] = y; bad |= !isfinite(y)
-// which reproduces, op for op, the ATen chains of DDP's all-reduce and of
-// FSDP's reduce_scatter_grads for a rank-ordered sum.
-//
-// Each lane keeps U fragments of every contribution in flight (W*U 16-byte
-// loads issued before the first add), which is what feeds HBM: for W = 8 and
-// fp32 that is 16 outstanding 16-byte loads per lane.  Peer contributions are
-// read once per step and use non-temporal loads; the rank's own data and the
-// output use normal accesses because the neighbouring pipeline stages touch
-// the same bytes just before and after.
+
 #include "mdx_internal.h"
 
 namespace mdx {
 namespace reduce_impl {
 
-template <typename In, typename Acc, typename Out>
-struct ReduceOp {
-  int32_t flags;
-  float pre;
-  float inv_scale;
-  __device__ __forceinline__ Acc widen(In x) const {
-    Acc a = Cvt<In, Acc>::run(x);
-    if (flags & kRedPreMul) a = from_f32<Acc>(to_f32(a) * pre);
-    if (flags & kRedPreDiv) a = from_f32<Acc>(to_f32(a) / pre);
-    return a;
-  }
-  __device__ __forceinline__ Acc add(Acc a, Acc b) const {
-    return from_f32<Acc>(to_f32(a) + to_f32(b));
-  }
-  __device__ __forceinline__ Out finish(Acc a, Out prev, bool& bad) const {
-    Out y = Cvt<Acc, Out>::run(a);
-    if (flags & kRedAccumulate) y = from_f32<Out>(to_f32(prev) + to_f32(y));
-    if (flags & kRedUnscale) y = from_f32<Out>(to_f32(y) * inv_scale);
-    if (flags & kRedCheck) bad |= !is_finite(y);
-    return y;
-  }
-};
+// ---------------------------------------------------------------------------
+// all-reduce (+ fused unpack)
+// ---------------------------------------------------------------------------
 
-template <typename In, typename Acc, typename Out, int W>
-__global__ void __launch_bounds__(kBlock) reduce_kernel(PieceBatch b, ReduceParams p) {
-  constexpr int E = frag_elems(int(sizeof(In)), int(sizeof(Out)));
-  constexpr int U = reduce_unroll(W);
+template <typename T, typename G, int W, bool UNPACK>
+__global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceParams p) {
+  constexpr int E = frag_elems(int(sizeof(T)), UNPACK ? int(sizeof(G)) : int(sizeof(T)));
+  constexpr int U = allreduce_unroll(W, E * int(sizeof(T)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
 
@@ -60,36 +46,174 @@ __global__ void __launch_bounds__(kBlock) reduce_kernel(PieceBatch b, ReducePara
   const int64_t n = b.numel[s];
   const int32_t h = b.head[s];
   const int rank = p.rank;
-  const bool own_zero = (b.own[s] == nullptr);
-  const bool accumulate = (p.flags & kRedAccumulate) != 0;
-  const ReduceOp<In, Acc, Out> op{p.flags, p.pre, p.inv_scale};
   const int t = int(threadIdx.x);
+  const bool unscale = (p.flags & kRedUnscale) != 0;
+  const float inv = p.inv_scale;
 
-  const In* src[W];
+  const T* src[W];
 #pragma unroll
   for (int r = 0; r < W; ++r) {
-    src[r] = (r == rank) ? static_cast<const In*>(b.own[s])
-                         : static_cast<const In*>(p.peer[r]) + pos;
+    src[r] = (r == rank) ? static_cast<const T*>(b.own[s]) : static_cast<const T*>(p.peer[r]) + pos;
   }
-  Out* out = static_cast<Out*>(p.out) + pos;
+  T* out = p.out ? static_cast<T*>(p.out) + pos : nullptr;
+  G* grad = static_cast<G*>(b.grad[s]);
   bool bad = false;
 
-  // One element, used for ragged edges and the unaligned path.
+  auto finish = [&](T acc) -> G {
+    G g = Cvt<T, G>::run(acc);
+    const G gs = from_f32<G>(to_f32(g) * inv);
+    g = unscale ? gs : g;
+    bad |= !is_finite(g);
+    return g;
+  };
   auto element = [&](int64_t i) {
-    Acc acc = zero_of<Acc>();
+    T acc = src[0][i];
 #pragma unroll
-    for (int r = 0; r < W; ++r) {
-      const In x = (r == rank && own_zero) ? zero_of<In>() : src[r][i];
-      const Acc a = op.widen(x);
-      acc = (r == 0) ? a : op.add(acc, a);
-    }
-    const Out prev = accumulate ? out[i] : zero_of<Out>();
-    out[i] = op.finish(acc, prev, bad);
+    for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(src[r][i]));
+    if (out) out[i] = acc;
+    if constexpr (UNPACK) grad[i] = finish(acc);
   };
 
   if (h >= 0) {
     const int64_t nvec = (n - h) / E;
-    In x[U][W][E];
+    T x[U][W][E];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if (v < nvec) {
+#pragma unroll
+        for (int r = 0; r < W; ++r) vload<T, E, true>(x[u][r], src[r] + h + v * E);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if (v < nvec) {
+        const int64_t i = h + v * E;
+        T y[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          T acc = x[u][0][k];
+#pragma unroll
+          for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(x[u][r][k]));
+          y[k] = acc;
+        }
+        if (out) vstore<T, E, false>(out + i, y);
+        if constexpr (UNPACK) {
+          G gy[E];
+#pragma unroll
+          for (int k = 0; k < E; ++k) gy[k] = finish(y[k]);
+          vstore<G, E, false>(grad + i, gy);
+        }
+      }
+    }
+    if (c == 0 && t < h && t < n) element(t);
+    const int64_t tail0 = h + nvec * E;
+    if (c == nblk - 1 && tail0 + t < n) element(tail0 + t);
+  } else {
+#pragma unroll 4
+    for (int k = 0; k < U * E; ++k) {
+      const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
+      if (i < n) element(i);
+    }
+  }
+  if constexpr (UNPACK) {
+    if (p.found_inf) flag_nonfinite(bad, p.found_inf);
+  }
+}
+
+template <typename T, typename G, bool UNPACK, int W>
+hipError_t launch_allreduce_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  const int blocks = b.first_block[b.count];
+  hipLaunchKernelGGL((allreduce_kernel<T, G, W, UNPACK>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
+  return hipGetLastError();
+}
+
+template <typename T, typename G, bool UNPACK>
+hipError_t launch_allreduce(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  switch (world) {
+    case 1: return launch_allreduce_w<T, G, UNPACK, 1>(b, p, stream);
+    case 2: return launch_allreduce_w<T, G, UNPACK, 2>(b, p, stream);
+    case 3: return launch_allreduce_w<T, G, UNPACK, 3>(b, p, stream);
+    case 4: return launch_allreduce_w<T, G, UNPACK, 4>(b, p, stream);
+    case 5: return launch_allreduce_w<T, G, UNPACK, 5>(b, p, stream);
+    case 6: return launch_allreduce_w<T, G, UNPACK, 6>(b, p, stream);
+    case 7: return launch_allreduce_w<T, G, UNPACK, 7>(b, p, stream);
+    case 8: return launch_allreduce_w<T, G, UNPACK, 8>(b, p, stream);
+    case 9: return launch_allreduce_w<T, G, UNPACK, 9>(b, p, stream);
+    case 10: return launch_allreduce_w<T, G, UNPACK, 10>(b, p, stream);
+    case 11: return launch_allreduce_w<T, G, UNPACK, 11>(b, p, stream);
+    case 12: return launch_allreduce_w<T, G, UNPACK, 12>(b, p, stream);
+    case 13: return launch_allreduce_w<T, G, UNPACK, 13>(b, p, stream);
+    case 14: return launch_allreduce_w<T, G, UNPACK, 14>(b, p, stream);
+    case 15: return launch_allreduce_w<T, G, UNPACK, 15>(b, p, stream);
+    default: return launch_allreduce_w<T, G, UNPACK, 16>(b, p, stream);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// reduce-scatter share
+// ---------------------------------------------------------------------------
+
+enum : int { kPreNone = 0, kPreMul = 1, kPreDiv = 2 };
+
+template <typename In, typename Acc, typename Out, int WMAX, int PRE, bool ACC>
+__device__ __forceinline__ void share_body(const PieceBatch& b, const ReduceParams& p, int s, int c, int nblk) {
+  constexpr int E = frag_elems(int(sizeof(In)), int(sizeof(Out)));
+  constexpr int U = share_unroll(WMAX, E * int(sizeof(In)));
+  constexpr int VPB = kBlock * U;
+  constexpr int EPB = VPB * E;
+
+  const int64_t pos = b.pos[s];
+  const int64_t n = b.numel[s];
+  const int32_t h = b.head[s];
+  const int world = p.world;
+  const int rank = p.rank;
+  const bool own_zero = (b.own[s] == nullptr);
+  const int t = int(threadIdx.x);
+  const float pre = p.pre;
+  const bool unscale = (p.flags & kRedUnscale) != 0;
+  const float inv = p.inv_scale;
+
+  const In* src[WMAX];
+#pragma unroll
+  for (int r = 0; r < WMAX; ++r) {
+    src[r] = (r == rank) ? static_cast<const In*>(b.own[s]) : static_cast<const In*>(p.peer[r]) + pos;
+  }
+  Out* out = static_cast<Out*>(p.out) + pos;
+  bool bad = false;
+
+  auto widen = [&](In x) -> Acc {
+    Acc a = Cvt<In, Acc>::run(x);
+    if constexpr (PRE == kPreMul) a = from_f32<Acc>(to_f32(a) * pre);
+    if constexpr (PRE == kPreDiv) a = from_f32<Acc>(to_f32(a) / pre);
+    return a;
+  };
+  auto finish = [&](Acc acc, Out prev) -> Out {
+    Out y = Cvt<Acc, Out>::run(acc);
+    if constexpr (ACC) y = from_f32<Out>(to_f32(prev) + to_f32(y));
+    const Out ys = from_f32<Out>(to_f32(y) * inv);
+    y = unscale ? ys : y;
+    bad |= !is_finite(y);
+    return y;
+  };
+  auto element = [&](int64_t i) {
+    Acc acc = zero_of<Acc>();
+#pragma unroll
+    for (int r = 0; r < WMAX; ++r) {
+      if (r < world) {
+        const In x = (r == rank && own_zero) ? zero_of<In>() : src[r][i];
+        const Acc a = widen(x);
+        acc = (r == 0) ? a : from_f32<Acc>(to_f32(acc) + to_f32(a));
+      }
+    }
+    const Out prev = ACC ? out[i] : zero_of<Out>();
+    out[i] = finish(acc, prev);
+  };
+
+  if (h >= 0) {
+    const int64_t nvec = (n - h) / E;
+    In x[U][WMAX][E];
     Out prev[U][E];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -97,19 +221,17 @@ __global__ void __launch_bounds__(kBlock) reduce_kernel(PieceBatch b, ReducePara
       if (v < nvec) {
         const int64_t i = h + v * E;
 #pragma unroll
-        for (int r = 0; r < W; ++r) {
-          if (r == rank) {
-            if (own_zero) {
+        for (int r = 0; r < WMAX; ++r) {
+          if (r < world) {
+            if (r == rank && own_zero) {
 #pragma unroll
               for (int k = 0; k < E; ++k) x[u][r][k] = zero_of<In>();
             } else {
-              vload<In, E, false>(x[u][r], src[r] + i);
+              vload<In, E, true>(x[u][r], src[r] + i);
             }
-          } else {
-            vload<In, E, true>(x[u][r], src[r] + i);
           }
         }
-        if (accumulate) vload<Out, E, false>(prev[u], out + i);
+        if constexpr (ACC) vload<Out, E, false>(prev[u], out + i);
       }
     }
 #pragma unroll
@@ -120,10 +242,12 @@ __global__ void __launch_bounds__(kBlock) reduce_kernel(PieceBatch b, ReducePara
         Out y[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-          Acc acc = op.widen(x[u][0][k]);
+          Acc acc = widen(x[u][0][k]);
 #pragma unroll
-          for (int r = 1; r < W; ++r) acc = op.add(acc, op.widen(x[u][r][k]));
-          y[k] = op.finish(acc, accumulate ? prev[u][k] : zero_of<Out>(), bad);
+          for (int r = 1; r < WMAX; ++r) {
+            if (r < world) acc = from_f32<Acc>(to_f32(acc) + to_f32(widen(x[u][r][k])));
+          }
+          y[k] = finish(acc, ACC ? prev[u][k] : zero_of<Out>());
         }
         vstore<Out, E, false>(out + i, y);
       }
@@ -138,36 +262,33 @@ __global__ void __launch_bounds__(kBlock) reduce_kernel(PieceBatch b, ReducePara
       if (i < n) element(i);
     }
   }
-  if (p.flags & kRedCheck) flag_nonfinite(bad, p.found_inf);
+  if (p.found_inf) flag_nonfinite(bad, p.found_inf);
 }
 
-template <typename In, typename Acc, typename Out, int W>
-hipError_t launch_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
-  const int blocks = b.first_block[b.count];
-  hipLaunchKernelGGL((reduce_kernel<In, Acc, Out, W>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
-  return hipGetLastError();
-}
-
-template <typename In, typename Acc, typename Out>
-hipError_t launch_types(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
-  switch (world) {
-    case 1: return launch_w<In, Acc, Out, 1>(b, p, stream);
-    case 2: return launch_w<In, Acc, Out, 2>(b, p, stream);
-    case 3: return launch_w<In, Acc, Out, 3>(b, p, stream);
-    case 4: return launch_w<In, Acc, Out, 4>(b, p, stream);
-    case 5: return launch_w<In, Acc, Out, 5>(b, p, stream);
-    case 6: return launch_w<In, Acc, Out, 6>(b, p, stream);
-    case 7: return launch_w<In, Acc, Out, 7>(b, p, stream);
-    case 8: return launch_w<In, Acc, Out, 8>(b, p, stream);
-    case 9: return launch_w<In, Acc, Out, 9>(b, p, stream);
-    case 10: return launch_w<In, Acc, Out, 10>(b, p, stream);
-    case 11: return launch_w<In, Acc, Out, 11>(b, p, stream);
-    case 12: return launch_w<In, Acc, Out, 12>(b, p, stream);
-    case 13: return launch_w<In, Acc, Out, 13>(b, p, stream);
-    case 14: return launch_w<In, Acc, Out, 14>(b, p, stream);
-    case 15: return launch_w<In, Acc, Out, 15>(b, p, stream);
-    default: return launch_w<In, Acc, Out, 16>(b, p, stream);
+template <typename In, typename Acc, typename Out, int WMAX>
+__global__ void __launch_bounds__(kBlock) share_kernel(PieceBatch b, ReduceParams p) {
+  const int blk = int(blockIdx.x);
+  const int s = find_run(b.first_block, b.count, blk);
+  const int c = blk - b.first_block[s];
+  const int nblk = b.first_block[s + 1] - b.first_block[s];
+  const bool acc = (p.flags & kRedAccumulate) != 0;
+  if (p.flags & kRedPreMul) {
+    if (acc) share_body<In, Acc, Out, WMAX, kPreMul, true>(b, p, s, c, nblk);
+    else share_body<In, Acc, Out, WMAX, kPreMul, false>(b, p, s, c, nblk);
+  } else if (p.flags & kRedPreDiv) {
+    if (acc) share_body<In, Acc, Out, WMAX, kPreDiv, true>(b, p, s, c, nblk);
+    else share_body<In, Acc, Out, WMAX, kPreDiv, false>(b, p, s, c, nblk);
+  } else {
+    if (acc) share_body<In, Acc, Out, WMAX, kPreNone, true>(b, p, s, c, nblk);
+    else share_body<In, Acc, Out, WMAX, kPreNone, false>(b, p, s, c, nblk);
   }
+}
+
+template <typename In, typename Acc, typename Out, int WMAX>
+hipError_t launch_share_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  const int blocks = b.first_block[b.count];
+  hipLaunchKernelGGL((share_kernel<In, Acc, Out, WMAX>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
+  return hipGetLastError();
 }
 
 }  // namespace reduce_impl

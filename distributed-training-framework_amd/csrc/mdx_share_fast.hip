@@ -1,0 +1,24 @@
+// Instantiates the reduce-scatter share for FSDP's usual dtypes (bf16 or fp32
+// gradients, fp32 reduction, fp32 shard) at every width class.
+#include "mdx_reduce_impl.h"
+
+namespace mdx {
+
+template <typename In>
+static hipError_t by_width(int wmax, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  using namespace reduce_impl;
+  switch (wmax) {
+    case 2: return launch_share_w<In, float, float, 2>(b, p, stream);
+    case 4: return launch_share_w<In, float, float, 4>(b, p, stream);
+    case 8: return launch_share_w<In, float, float, 8>(b, p, stream);
+    default: return launch_share_w<In, float, float, 16>(b, p, stream);
+  }
+}
+
+hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
+                             hipStream_t stream) {
+  if (in_dtype == MDX_BF16) return by_width<bf16>(wmax, b, p, stream);
+  return by_width<float>(wmax, b, p, stream);
+}
+
+}  // namespace mdx

@@ -25,10 +25,10 @@ SOURCES = [
     "mdx_api.hip",
     "mdx_copy.hip",
     "mdx_reduce.hip",
-    "mdx_reduce_f32.hip",
-    "mdx_reduce_bf16.hip",
-    "mdx_reduce_bf16_f32.hip",
-    "mdx_reduce_mixed.hip",
+    "mdx_allreduce_f32.hip",
+    "mdx_allreduce_bf16.hip",
+    "mdx_share_fast.hip",
+    "mdx_share_generic.hip",
 ]
 HEADERS = ["mdx_internal.h", "mdx_reduce_impl.h"]
 

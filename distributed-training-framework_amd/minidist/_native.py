@@ -33,6 +33,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_unpack": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _vp]),
     "mdx_unscale_found_inf": (_i32, [_vp, _i32, _i32, _f32, _vp, _vp]),
     "mdx_allreduce_sum": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "mdx_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp]),
     "mdx_reduce_scatter_share": (
         _i32,
         [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
@@ -44,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
 
 SPAN_DTYPE = np.dtype([("src", "<u8"), ("dst", "<u8"), ("numel", "<i8")])
 PIECE_DTYPE = np.dtype([("own", "<u8"), ("pos", "<i8"), ("numel", "<i8")])
+GRAD_RUN_DTYPE = np.dtype([("offset", "<i8"), ("numel", "<i8"), ("grad", "<u8")])
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -167,6 +169,21 @@ def allreduce_sum(
     nums = (ctypes.c_int64 * n)(*numels)
     rc = lib().mdx_allreduce_sum(_ptrs(replicas), len(replicas), dtype, offs, nums, n, out, stream)
     check(rc, "mdx_allreduce_sum")
+
+
+def grad_runs_array(rows: list[tuple[int, int, int]]) -> np.ndarray:
+    return np.array(rows, dtype=GRAD_RUN_DTYPE)
+
+
+def allreduce_unpack(
+    replicas: list[int], dtype: int, runs: np.ndarray, out: int | None, grad_dtype: int,
+    inv_scale: float, found_inf: int | None, stream: int,
+) -> None:
+    rc = lib().mdx_allreduce_unpack(
+        _ptrs(replicas), len(replicas), dtype, _ptr(runs), len(runs), out, grad_dtype, inv_scale,
+        found_inf, stream,
+    )
+    check(rc, "mdx_allreduce_unpack")
 
 
 def reduce_scatter_share(

@@ -148,7 +148,7 @@ class DistributedGradScaler:
             self._flag_armed.add(device)
         return flag
 
-    def _begin_fused_unscale(self, device: torch.device, params) -> tuple[float, torch.Tensor]:
+    def _begin_fused_unscale(self, device: torch.device, param_ids: frozenset) -> tuple[float, torch.Tensor]:
         """Hand a producer (DDP's unpack) the inverse scale and the device flag.
 
         The producer writes these params' grads already multiplied by
@@ -157,13 +157,12 @@ class DistributedGradScaler:
         second synchronised backward before ``step``/``update`` is an error."""
         if self._unscaled:
             raise RuntimeError("gradients were already unscaled this step; call update() first")
-        ids = {id(p) for p in params}
-        if ids & self._prescaled:
+        if not self._prescaled.isdisjoint(param_ids):
             raise RuntimeError(
                 "a second synchronised backward ran before scaler.step()/update(): its gradients "
                 "would accumulate onto already-unscaled ones"
             )
-        self._prescaled |= ids
+        self._prescaled |= param_ids
         return 1.0 / self._scale, self._flag(device)
 
     # -- the training-loop surface -----------------------------------------

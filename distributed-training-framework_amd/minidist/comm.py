@@ -47,7 +47,9 @@ __all__ = [
     "broadcast",
     "print_rank0",
     "ResidentGroup",
+    "StreamWork",
     "zeros_for_collective",
+    "record_all_reduce",
 ]
 
 
@@ -92,6 +94,11 @@ class CommStats:
 
 
 comm_stats = CommStats()
+
+
+def record_all_reduce(payload_bytes: int, world: int) -> None:
+    """Account one all-reduce of ``payload_bytes`` (reference comm.py:232-233)."""
+    comm_stats.add("all_reduce", payload_bytes, int(2 * (world - 1) / world * payload_bytes))
 
 
 @contextmanager
@@ -189,7 +196,7 @@ def print_rank0(*args, **kwargs) -> None:
 # --------------------------------------------------------------------------
 
 
-class _EventWork:
+class StreamWork:
     """Completion handle of a collective launched on a stream.
 
     ``wait()`` has NCCL-Work semantics on a GPU: it makes the *current* stream
@@ -217,7 +224,7 @@ _ROW_ALIGN_BYTES = 256
 class _Arena:
     """W equally laid-out rows (one per replica) of one symmetric allocation."""
 
-    __slots__ = ("data", "numel", "row_elems", "dtype", "own_base", "esize")
+    __slots__ = ("data", "numel", "row_elems", "dtype", "own_base", "esize", "row_ptrs")
 
     def __init__(self, world: int, rank: int, numel: int, dtype: torch.dtype, device: torch.device):
         esize = torch.empty((), dtype=dtype).element_size()
@@ -228,6 +235,7 @@ class _Arena:
         self.dtype = dtype
         self.esize = esize
         self.own_base = self.data[rank].data_ptr()
+        self.row_ptrs = [self.data[r].data_ptr() for r in range(world)]
 
     def row(self, r: int) -> torch.Tensor:
         return self.data[r, : self.numel]
@@ -324,7 +332,7 @@ class ResidentGroup:
             entry[2].append(t.numel())
         for arena, offs, nums in groups.values():
             order = sorted(range(len(offs)), key=offs.__getitem__)
-            bases = [arena.data[r].data_ptr() for r in range(self._world)]
+            bases = arena.row_ptrs
             _native.allreduce_sum(
                 bases,
                 _native.dtype_code(arena.dtype),
@@ -333,7 +341,36 @@ class ResidentGroup:
                 arena.own_base,
                 stream.cuda_stream,
             )
-        return _EventWork(stream) if async_op else None
+        return StreamWork(stream) if async_op else None
+
+    def all_reduce_unpack(
+        self,
+        buffer: torch.Tensor,
+        runs,
+        grad_dtype: torch.dtype,
+        inv_scale: float = 1.0,
+        found_inf: torch.Tensor | None = None,
+        async_op: bool = False,
+    ):
+        """SUM over the W replicas of ``buffer``'s runs, delivered into gradients.
+
+        ``runs`` is an ``mdx_grad_run`` table (numpy, ``_native.GRAD_RUN_DTYPE``)
+        of (offset into ``buffer``, numel, gradient address) in increasing
+        offset order.  The sum is written back into ``buffer`` (the in-place
+        all-reduce) and, converted to ``grad_dtype``, multiplied by
+        ``inv_scale`` and checked for inf/NaN into ``found_inf``, into each
+        gradient -- one dispatch, the reduced values never re-read."""
+        _native.require_device_tensor(buffer, "all_reduce input")
+        arena, off = self._locate(buffer)
+        esize = arena.esize
+        bases = [b + off * esize for b in arena.row_ptrs]
+        stream = torch.cuda.current_stream(buffer.device)
+        _native.allreduce_unpack(
+            bases, _native.dtype_code(arena.dtype), runs, buffer.data_ptr(), _native.dtype_code(grad_dtype),
+            _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
+            stream.cuda_stream,
+        )
+        return StreamWork(stream) if async_op else None
 
     def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
@@ -355,7 +392,7 @@ class ResidentGroup:
             own, peers, self._rank, code, code, False, output.data_ptr(), code, False, 1.0, None,
             stream.cuda_stream,
         )
-        return _EventWork(stream) if async_op else None
+        return StreamWork(stream) if async_op else None
 
     def all_gather_into(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output[r*S:(r+1)*S] = replicas(input_)[r]`` for every rank r."""
@@ -370,7 +407,7 @@ class ResidentGroup:
         code = _native.dtype_code(input_.dtype)
         stream = torch.cuda.current_stream(input_.device)
         _native.pack(_native.spans_array(rows), code, code, 1.0, False, stream.cuda_stream)
-        return _EventWork(stream) if async_op else None
+        return StreamWork(stream) if async_op else None
 
 
 def zeros_for_collective(numel: int, dtype: torch.dtype, device: torch.device, group=None) -> torch.Tensor:
@@ -400,8 +437,7 @@ def all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op:
     world = get_world_size(group)
     if world == 1:
         return None
-    payload = _nbytes(tensor)
-    comm_stats.add("all_reduce", payload, int(2 * (world - 1) / world * payload))
+    record_all_reduce(_nbytes(tensor), world)
     if isinstance(group, ResidentGroup):
         if op != dist.ReduceOp.SUM:
             raise NotImplementedError("ResidentGroup all_reduce implements SUM")
@@ -420,8 +456,7 @@ def all_reduce_coalesced(tensors: Sequence[torch.Tensor], group=None, async_op: 
     if world == 1 or not tensors:
         return None
     for t in tensors:
-        payload = _nbytes(t)
-        comm_stats.add("all_reduce", payload, int(2 * (world - 1) / world * payload))
+        record_all_reduce(_nbytes(t), world)
     if isinstance(group, ResidentGroup):
         return group.all_reduce_sum(list(tensors), async_op=async_op)
     work = None

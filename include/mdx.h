@@ -121,6 +121,31 @@ MDX_API int mdx_unscale_found_inf(const mdx_span* spans, int n_spans, int dtype,
 MDX_API int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,
                       const int64_t* numels, int n_runs, void* out, void* stream);
 
+/* One parameter's slice of a bucket for the fused all-reduce + unpack:
+ * elements [offset, offset + numel) of the replica layout are delivered to
+ * `grad` (a device pointer to numel elements of grad_dtype). */
+typedef struct mdx_grad_run {
+  int64_t offset;
+  int64_t numel;
+  void* grad;
+} mdx_grad_run;
+
+/* W-way SUM all-reduce fused with the unpack into the gradients and the loss
+ * scaler's unscale + found-inf.  Per run k and element j, with
+ * acc = ((rep[0][o+j] + rep[1][o+j]) + ...) rounded per add in `dtype`:
+ *   out[o+j] = acc                       (skipped when out == NULL)
+ *   g = rnd_grad(acc); if inv_scale != 1: g = rnd_grad(g * inv_scale)
+ *   grad[j] = g; flag if !isfinite(g)
+ * Replaces, for one run of ready buckets, comm.all_reduce (minidist/comm.py:
+ * 223-234) + _Bucket.scatter_from_buffer (minidist/ddp.py:94-102) + the
+ * per-gradient body of DistributedGradScaler.unscale_ (minidist/amp.py:
+ * 212-213), without reading the reduced bucket back.  Runs increase and do
+ * not overlap; `out` may be one of the replica bases; gradients must not
+ * overlap the replicas or `out`. */
+MDX_API int mdx_allreduce_unpack(const void* const* replicas, int world, int dtype,
+                                 const mdx_grad_run* runs, int n_runs, void* out, int grad_dtype,
+                                 float inv_scale, int32_t* found_inf, void* stream);
+
 /* This rank's share of a SUM reduce-scatter, with FSDP's pre-division,
  * dtype changes and optional accumulation fused.
  * Replaces _FSDPUnit.reduce_scatter_grads (minidist/fsdp.py:215-237): widen

@@ -94,6 +94,15 @@ def test_argument_checks_happen_before_any_launch():
     bad_nums = (ctypes.c_int64 * 2)(4, 4)
     assert L.mdx_allreduce_sum(reps, 2, 0, bad_offs, bad_nums, 2, P(4096), None) == -1
     assert L.mdx_allreduce_sum(reps, 2, 0, offs, nums, 1, P(4096 + 4), None) == -4  # partial overlap
+    runs = nat.grad_runs_array([(0, 8, 1 << 20)])
+    assert L.mdx_allreduce_unpack(reps, 0, 0, runs.ctypes.data, 1, None, 0, 1.0, None, None) == -3
+    assert L.mdx_allreduce_unpack(reps, 2, 0, runs.ctypes.data, 1, None, 4, 1.0, None, None) == -2
+    assert L.mdx_allreduce_unpack(reps, 2, 0, None, 1, None, 0, 1.0, None, None) == -1
+    null_grad = nat.grad_runs_array([(0, 8, 0)])
+    assert L.mdx_allreduce_unpack(reps, 2, 0, null_grad.ctypes.data, 1, None, 0, 1.0, None, None) == -1
+    into_replica = nat.grad_runs_array([(0, 8, 8192 + 4)])
+    assert L.mdx_allreduce_unpack(reps, 2, 0, into_replica.ctypes.data, 1, None, 0, 1.0, None, None) == -4
+    assert L.mdx_allreduce_unpack(reps, 2, 0, None, 0, None, 0, 1.0, None, None) == 0
     pc = nat.pieces_array([(4096, 0, 8)])
     peers = (ctypes.c_void_p * 2)(0, 8192)
     assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 2, 0, 0, 1, P(1 << 20), 0, 0, 1.0, None, None) == -3

@@ -226,6 +226,59 @@ def test_allreduce_full_bucket_exact_sum_property(rng):
     assert np.array_equal(to_host(out), want)
 
 
+@pytest.mark.parametrize("bdt,gdt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.BF16, o.F32)])
+@pytest.mark.parametrize("W", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("inv_scale,write_out", [(1.0, True), (2.0**-16, True), (1.0 / 3, False)])
+def test_allreduce_unpack_matches_oracle(rng, bdt, gdt, W, inv_scale, write_out):
+    """Fused SUM + unpack + unscale + found-inf == allreduce_sum, unpack (copy_), mul_, isfinite."""
+    numels = [1, 7, 64, 4096, 3, 12345, 256, 5]
+    offs, off = [], 5
+    for n in numels:
+        offs.append(off)
+        off += n + int(rng.integers(0, 3))
+    extent = off + 4
+    reps_host = [values(rng, extent, bdt, scale=1e3) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    rank = W // 2
+    grads = [empty_dev(n + 2, gdt) for n in numels]
+    shifts = [int(rng.integers(0, 3)) for _ in numels]
+    runs = nat.grad_runs_array(
+        [(a, n, g.data_ptr() + s * esize(gdt)) for a, n, g, s in zip(offs, numels, grads, shifts, strict=True)]
+    )
+    before = to_host(reps[rank])
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.allreduce_unpack(
+        [r.data_ptr() for r in reps], code(bdt), runs, reps[rank].data_ptr() if write_out else None, code(gdt),
+        nat.f32(inv_scale), flag.data_ptr(), stream(),
+    )
+    any_bad = False
+    want_out = before.copy()
+    for a, n, g, s in zip(offs, numels, grads, shifts, strict=True):
+        acc = o.allreduce_sum([h[a : a + n] for h in reps_host], bdt)
+        want_out[a : a + n] = acc
+        v = o.convert(acc, bdt, gdt)
+        if inv_scale != 1.0:
+            v = o.mul_scalar(v, gdt, inv_scale)
+        any_bad |= bool((~o.isfinite(v, gdt)).any())
+        got = to_host(g)
+        assert same_bits(got[s : s + n], v), first_mismatch(got[s : s + n], v)
+        sent = np.concatenate([got[:s], got[s + n :]])
+        assert np.all(sent == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32))
+    got_out = to_host(reps[rank])
+    assert same_bits(got_out, want_out if write_out else before), first_mismatch(got_out, want_out)
+    for r in range(W):
+        if r != rank:
+            assert same_bits(to_host(reps[r]), reps_host[r])
+    assert bool(flag.item()) == any_bad
+
+
+def test_allreduce_unpack_rejects_grad_overlapping_a_replica():
+    reps = [torch.zeros(1024, device=DEV) for _ in range(2)]
+    runs = nat.grad_runs_array([(0, 16, reps[1][4:].data_ptr())])  # inside the reduced extent
+    with pytest.raises(RuntimeError, match="overlaps"):
+        nat.allreduce_unpack([r.data_ptr() for r in reps], 0, runs, None, 0, 1.0, None, stream())
+
+
 # ---------------------------------------------------------------------------
 # reduce-scatter share
 # ---------------------------------------------------------------------------
