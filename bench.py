@@ -6,9 +6,9 @@ peers' packed contributions staged before timing), 25 MB buckets in reverse
 parameter order, loss scale 2^16:
 
     DistributedDataParallel.finish_gradient_sync()
-        pack + 1/W       -> mdx_pack  (all 148 gradients, dispatches of 48 spans)
+        pack + 1/W       -> mdx_pack_planned (all 148 gradients, one dispatch)
         W-way SUM + unpack + unscale + found-inf
-                         -> mdx_allreduce_unpack (all 18 buckets, one dispatch:
+                         -> mdx_allreduce_unpack_planned (all 18 buckets, one dispatch:
                             average written to the bucket and into every .grad)
     DistributedGradScaler.unscale_(opt) -> flag.item()  (the path's one host sync)
     DistributedGradScaler.update()
@@ -154,7 +154,7 @@ def main() -> int:
     # dispatch, recorded on the stream it is launched on.
     red_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
     timing = {"on": False}
-    orig = ResidentGroup.all_reduce_unpack
+    orig = ResidentGroup.all_reduce_unpack_planned
 
     def timed_all_reduce(self, *a, **k):
         if not timing["on"]:
@@ -167,7 +167,7 @@ def main() -> int:
         red_events.append((e0, e1))
         return work
 
-    ResidentGroup.all_reduce_unpack = timed_all_reduce
+    ResidentGroup.all_reduce_unpack_planned = timed_all_reduce
 
     def step() -> bool:
         ddp.finish_gradient_sync()
@@ -192,7 +192,7 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     timing["on"] = False
-    ResidentGroup.all_reduce_unpack = orig
+    ResidentGroup.all_reduce_unpack_planned = orig
 
     ms_per_step = elapsed / args.steps * 1e3
     alg_bytes = 52 * N  # pack 8N + W-way (W+1)*4N + unpack 8N, fp32, W = 8
@@ -235,7 +235,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "allreduce_kernel<float,float,8,true> (mdx_allreduce_unpack, all 18 buckets per dispatch)",
+            "kernel": "allreduce_kernel<float,float,8,true> (mdx_allreduce_unpack_planned, all 18 buckets in one dispatch)",
             "achieved": round(red_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -12,4 +12,12 @@ hipError_t launch_allreduce_f32(int grad_dtype, bool unpack, int world, const Pi
   return launch_allreduce<float, float, true>(world, b, p, stream);
 }
 
+
+hipError_t launch_allreduce_dev_f32(int grad_dtype, int world, const DevTable& t, int blocks,
+                                    const ReduceParams& p, hipStream_t stream) {
+  using namespace reduce_impl;
+  if (grad_dtype == MDX_BF16) return launch_allreduce_unpack_dev<float, bf16>(world, t, blocks, p, stream);
+  return launch_allreduce_unpack_dev<float, float>(world, t, blocks, p, stream);
+}
+
 }  // namespace mdx

@@ -1,11 +1,14 @@
 // extern "C" entry points of libmdx.so (declared in include/mdx.h).
 //
 // Host-side work per call: validate every argument before anything is
-// launched, cut the caller's span / piece list into dispatches of at most
-// kRunsPerLaunch runs of at most kMaxRunElems elements, compute for each run
-// the element offset ("head") that brings all of its pointers to 16-byte
-// alignment, lay out the workgroups of each run, and launch.  Nothing here
-// allocates or synchronises.
+// launched, cut the caller's span / piece list into runs of at most
+// kMaxRunElems elements, compute for each run the element offset ("head")
+// that brings all of its pointers to 16-byte alignment and its workgroup
+// count, then either pack the runs into kernel-argument batches of at most
+// kRunsPerLaunch (the direct entry points) or write them into a plan that the
+// caller keeps in device memory (the mdx_plan_* / *_planned entry points: one
+// dispatch for any number of runs).  Nothing here allocates device memory or
+// synchronises.
 #include <string.h>
 
 #include <algorithm>
@@ -47,26 +50,26 @@ int32_t run_blocks(int64_t n, int head, int E, int64_t vec_per_block, int64_t el
   return int32_t(std::max<int64_t>(1, ceil_div(n, elems_per_block)));
 }
 
+// One run of kernel work, whichever table it ends up in.
+struct Rec {
+  const void* a;  // span src / piece own
+  void* b;        // span dst / piece grad
+  int64_t pos;
+  int64_t numel;
+  int32_t head;
+  int32_t blocks;
+};
+
 // ---------------------------------------------------------------------------
-// copy family
+// Run generation
 // ---------------------------------------------------------------------------
 
-int run_copy(const mdx_span* spans, int n_spans, int sdt, int ddt, const CopyParams& params,
-             bool in_place, hipStream_t stream) {
+template <typename Emit>
+int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool in_place, Emit&& emit) {
   const int E = copy_frag_elems(sdt, ddt);
   const int64_t VPB = int64_t(kBlock) * (kCopyElemsPerThread / E);
   const int64_t EPB = int64_t(kBlock) * kCopyElemsPerThread;
   const int ss = dtype_size(sdt), ds = dtype_size(ddt);
-
-  SpanBatch b;
-  memset(&b, 0, sizeof(b));
-  auto flush = [&]() -> int {
-    if (b.count == 0) return MDX_OK;
-    const int rc = status(launch_copy(sdt, ddt, b, params, stream));
-    memset(&b, 0, sizeof(b));
-    return rc;
-  };
-
   for (int i = 0; i < n_spans; ++i) {
     const mdx_span& sp = spans[i];
     const char* src = static_cast<const char*>(in_place ? sp.dst : sp.src);
@@ -85,57 +88,20 @@ int run_copy(const mdx_span* spans, int n_spans, int sdt, int ddt, const CopyPar
         sizes[np++] = ss;
       }
       const int head = aligned_head(ptrs, sizes, np, E, n);
-      const int k = b.count;
-      b.src[k] = rs;
-      b.dst[k] = rd;
-      b.numel[k] = n;
-      b.head[k] = head;
-      b.first_block[k + 1] = b.first_block[k] + run_blocks(n, head, E, VPB, EPB);
-      b.count = k + 1;
-      if (b.count == kRunsPerLaunch) {
-        const int rc = flush();
-        if (rc != MDX_OK) return rc;
-      }
+      const int rc = emit(Rec{rs, rd, 0, n, head, run_blocks(n, head, E, VPB, EPB)});
+      if (rc != MDX_OK) return rc;
     }
-  }
-  return flush();
-}
-
-int check_spans(const mdx_span* spans, int n_spans, bool need_src) {
-  if (n_spans < 0 || (n_spans > 0 && spans == nullptr)) return MDX_EINVAL;
-  for (int i = 0; i < n_spans; ++i) {
-    if (spans[i].numel < 0) return MDX_EINVAL;
-    if (spans[i].numel > 0 && spans[i].dst == nullptr) return MDX_EINVAL;
-    if (need_src && spans[i].numel > 0 && spans[i].src == nullptr) return MDX_EINVAL;
   }
   return MDX_OK;
 }
 
-// [a, a+na) and [b, b+nb) share at least one byte.
-bool any_overlap(const void* a, int64_t na, const void* b, int64_t nb) {
-  const uintptr_t a0 = addr(a), a1 = a0 + uintptr_t(na), b0 = addr(b), b1 = b0 + uintptr_t(nb);
-  return na > 0 && nb > 0 && a0 < b1 && b0 < a1;
-}
-
-// ---------------------------------------------------------------------------
-// reduce family
-// ---------------------------------------------------------------------------
-
-// Lays out pieces into dispatches.  `grad_size` > 0 adds each piece's grad
-// pointer to the alignment requirement (fused unpack).
-template <typename Launch>
-int run_pieces(const mdx_piece* pieces, void* const* grads, int n_pieces, const ReduceParams& params,
-               int in_size, int out_size, int grad_size, int E, int U, Launch&& launch) {
+// `grads` (may be NULL) adds each piece's gradient pointer, of `grad_size`
+// bytes per element, to the alignment requirement (fused unpack).
+template <typename Emit>
+int for_each_piece_run(const mdx_piece* pieces, void* const* grads, int n_pieces, const ReduceParams& params,
+                       int in_size, int out_size, int grad_size, int E, int U, Emit&& emit) {
   const int64_t VPB = int64_t(kBlock) * U;
   const int64_t EPB = VPB * E;
-  PieceBatch b;
-  memset(&b, 0, sizeof(b));
-  auto flush = [&]() -> int {
-    if (b.count == 0) return MDX_OK;
-    const int rc = status(launch(b));
-    memset(&b, 0, sizeof(b));
-    return rc;
-  };
   for (int i = 0; i < n_pieces; ++i) {
     const mdx_piece& pc = pieces[i];
     const char* own = static_cast<const char*>(pc.own);
@@ -166,44 +132,239 @@ int run_pieces(const mdx_piece* pieces, void* const* grads, int n_pieces, const 
         sizes[np++] = grad_size;
       }
       const int head = aligned_head(ptrs, sizes, np, E, n);
-      const int k = b.count;
-      b.own[k] = ro;
-      b.pos[k] = pos;
-      b.numel[k] = n;
-      b.grad[k] = rg;
-      b.head[k] = head;
-      b.first_block[k + 1] = b.first_block[k] + run_blocks(n, head, E, VPB, EPB);
-      b.count = k + 1;
-      if (b.count == kRunsPerLaunch) {
-        const int rc = flush();
-        if (rc != MDX_OK) return rc;
-      }
+      const int rc = emit(Rec{ro, rg, pos, n, head, run_blocks(n, head, E, VPB, EPB)});
+      if (rc != MDX_OK) return rc;
     }
-  }
-  return flush();
-}
-
-// Validates W replica bases and increasing, non-overlapping runs; returns the
-// extent (one past the last element) through `end`.
-int check_runs(const void* const* replicas, int world, const int64_t* offs, const int64_t* nums,
-               int n_runs, int64_t* end, bool* any) {
-  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
-  if (n_runs < 0 || replicas == nullptr) return MDX_EINVAL;
-  *end = 0;
-  *any = false;
-  for (int k = 0; k < n_runs; ++k) {
-    if (offs[k] < 0 || nums[k] < 0 || offs[k] < *end) return MDX_EINVAL;
-    *end = offs[k] + nums[k];
-    *any = *any || nums[k] > 0;
-  }
-  if (!*any) return MDX_OK;
-  for (int r = 0; r < world; ++r) {
-    if (replicas[r] == nullptr) return MDX_EINVAL;
   }
   return MDX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Kernel-argument batches (direct entry points)
+// ---------------------------------------------------------------------------
+
+int run_copy(const mdx_span* spans, int n_spans, int sdt, int ddt, const CopyParams& params, bool in_place,
+             hipStream_t stream) {
+  SpanBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int rc = status(launch_copy(sdt, ddt, b, params, stream));
+    memset(&b, 0, sizeof(b));
+    return rc;
+  };
+  const int rc = for_each_span_run(spans, n_spans, sdt, ddt, in_place, [&](const Rec& r) -> int {
+    const int k = b.count;
+    b.src[k] = r.a;
+    b.dst[k] = r.b;
+    b.numel[k] = r.numel;
+    b.head[k] = r.head;
+    b.first_block[k + 1] = b.first_block[k] + r.blocks;
+    b.count = k + 1;
+    return b.count == kRunsPerLaunch ? flush() : MDX_OK;
+  });
+  return rc != MDX_OK ? rc : flush();
+}
+
+// Appends a run to a piece batch; `flush` launches and clears a full batch.
+template <typename Flush>
+int push_piece(PieceBatch& b, const Rec& r, Flush&& flush) {
+  const int k = b.count;
+  b.own[k] = r.a;
+  b.grad[k] = r.b;
+  b.pos[k] = r.pos;
+  b.numel[k] = r.numel;
+  b.head[k] = r.head;
+  b.first_block[k + 1] = b.first_block[k] + r.blocks;
+  b.count = k + 1;
+  return b.count == kRunsPerLaunch ? flush() : MDX_OK;
+}
+
+template <typename Launch>
+int run_pieces(const mdx_piece* pieces, void* const* grads, int n_pieces, const ReduceParams& params,
+               int in_size, int out_size, int grad_size, int E, int U, Launch&& launch) {
+  PieceBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int rc = status(launch(b));
+    memset(&b, 0, sizeof(b));
+    return rc;
+  };
+  const int rc = for_each_piece_run(pieces, grads, n_pieces, params, in_size, out_size, grad_size, E, U,
+                                    [&](const Rec& r) { return push_piece(b, r, flush); });
+  return rc != MDX_OK ? rc : flush();
+}
+
+// ---------------------------------------------------------------------------
+// Device plans
+// ---------------------------------------------------------------------------
+
+inline int64_t align8(int64_t x) { return (x + 7) & ~int64_t(7); }
+
+void plan_layout(PlanHeader* h, int count) {
+  int64_t off = align8(sizeof(PlanHeader));
+  h->off_first_block = off;
+  off = align8(off + int64_t(count + 1) * 4);
+  h->off_head = off;
+  off = align8(off + int64_t(count) * 4);
+  h->off_numel = off;
+  off += int64_t(count) * 8;
+  h->off_a = off;
+  off += int64_t(count) * 8;
+  h->off_b = off;
+  off += int64_t(count) * 8;
+  h->off_pos = off;
+  off += int64_t(count) * 8;
+  h->bytes = off;
+}
+
+// Two passes over the runs: count, then (if the caller's buffer is large
+// enough) write.  `gen(emit)` replays the same runs both times.
+template <typename Gen>
+int build_plan(PlanHeader proto, Gen&& gen, void* plan, int64_t* plan_bytes) {
+  int count = 0;
+  int64_t blocks = 0;
+  int rc = gen([&](const Rec& r) -> int {
+    ++count;
+    blocks += r.blocks;
+    return MDX_OK;
+  });
+  if (rc != MDX_OK) return rc;
+  if (blocks > INT32_MAX) return MDX_EINVAL;
+  PlanHeader h = proto;
+  h.magic = kPlanMagic;
+  h.count = count;
+  h.blocks = int32_t(blocks);
+  plan_layout(&h, count);
+  const int64_t cap = *plan_bytes;
+  *plan_bytes = h.bytes;
+  if (plan == nullptr || cap < h.bytes || (addr(plan) & 7u) != 0) return MDX_ESIZE;
+  char* base = static_cast<char*>(plan);
+  memcpy(base, &h, sizeof(h));
+  int32_t* fb = reinterpret_cast<int32_t*>(base + h.off_first_block);
+  int32_t* hd = reinterpret_cast<int32_t*>(base + h.off_head);
+  int64_t* nm = reinterpret_cast<int64_t*>(base + h.off_numel);
+  uint64_t* a = reinterpret_cast<uint64_t*>(base + h.off_a);
+  uint64_t* b = reinterpret_cast<uint64_t*>(base + h.off_b);
+  int64_t* ps = reinterpret_cast<int64_t*>(base + h.off_pos);
+  int k = 0;
+  fb[0] = 0;
+  rc = gen([&](const Rec& r) -> int {
+    hd[k] = r.head;
+    nm[k] = r.numel;
+    a[k] = addr(r.a);
+    b[k] = addr(r.b);
+    ps[k] = r.pos;
+    fb[k + 1] = fb[k] + r.blocks;
+    ++k;
+    return MDX_OK;
+  });
+  return rc;
+}
+
+// Validates the host copy of a plan and derives the device table view.
+int plan_view(const void* plan, const void* d_plan, int32_t kind, const PlanHeader** hdr, DevTable* t) {
+  if (plan == nullptr || d_plan == nullptr) return MDX_EINVAL;
+  const PlanHeader* h = static_cast<const PlanHeader*>(plan);
+  if (h->magic != kPlanMagic || h->kind != kind) return MDX_EINVAL;
+  const char* d = static_cast<const char*>(d_plan);
+  t->first_block = reinterpret_cast<const int32_t*>(d + h->off_first_block);
+  t->head = reinterpret_cast<const int32_t*>(d + h->off_head);
+  t->numel = reinterpret_cast<const int64_t*>(d + h->off_numel);
+  t->a = reinterpret_cast<const uint64_t*>(d + h->off_a);
+  t->b = reinterpret_cast<const uint64_t*>(d + h->off_b);
+  t->pos = reinterpret_cast<const int64_t*>(d + h->off_pos);
+  t->count = h->count;
+  *hdr = h;
+  return MDX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Validation helpers
+// ---------------------------------------------------------------------------
+
+int check_spans(const mdx_span* spans, int n_spans, bool need_src) {
+  if (n_spans < 0 || (n_spans > 0 && spans == nullptr)) return MDX_EINVAL;
+  for (int i = 0; i < n_spans; ++i) {
+    if (spans[i].numel < 0) return MDX_EINVAL;
+    if (spans[i].numel > 0 && spans[i].dst == nullptr) return MDX_EINVAL;
+    if (need_src && spans[i].numel > 0 && spans[i].src == nullptr) return MDX_EINVAL;
+  }
+  return MDX_OK;
+}
+
+// [a, a+na) and [b, b+nb) share at least one byte.
+bool any_overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t a0 = addr(a), a1 = a0 + uintptr_t(na), b0 = addr(b), b1 = b0 + uintptr_t(nb);
+  return na > 0 && nb > 0 && a0 < b1 && b0 < a1;
+}
+
 bool is_pow2(int w) { return w > 0 && (w & (w - 1)) == 0; }
+
+// Arguments of a fused all-reduce + unpack, validated, with the kernel
+// parameters and launch geometry they imply.
+struct FusedArgs {
+  ReduceParams p;
+  int es, gs, E, U;
+  bool any;
+};
+
+int check_fused(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs, int n_runs,
+                void* out, int grad_dtype, FusedArgs* f) {
+  if (!valid_dtype(dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
+  if (n_runs < 0 || (n_runs > 0 && runs == nullptr) || replicas == nullptr) return MDX_EINVAL;
+  const int es = dtype_size(dtype), gs = dtype_size(grad_dtype);
+  int64_t end = 0;
+  bool any = false;
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].offset < 0 || runs[k].numel < 0 || runs[k].offset < end) return MDX_EINVAL;
+    if (runs[k].numel > 0 && runs[k].grad == nullptr) return MDX_EINVAL;
+    end = runs[k].offset + runs[k].numel;
+    any = any || runs[k].numel > 0;
+  }
+  f->any = any;
+  if (!any) return MDX_OK;
+  for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
+    if (out && replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
+  }
+  for (int k = 0; k < n_runs; ++k) {
+    const int64_t gb = runs[k].numel * gs;
+    for (int r = 0; r < world; ++r) {
+      if (any_overlap(runs[k].grad, gb, replicas[r], end * es)) return MDX_EALIAS;
+    }
+    if (out && any_overlap(runs[k].grad, gb, out, end * es)) return MDX_EALIAS;
+  }
+  memset(&f->p, 0, sizeof(f->p));
+  for (int r = 0; r < world; ++r) f->p.peer[r] = replicas[r];
+  f->p.out = out;
+  f->p.world = world;
+  f->p.rank = 0;  // replica 0 is read through the pieces, the others through peer[r] + pos
+  f->p.pre = 1.0f;
+  f->p.inv_scale = 1.0f;
+  f->es = es;
+  f->gs = gs;
+  f->E = frag_elems(es, gs);
+  f->U = allreduce_unroll(world, f->E * es);
+  return MDX_OK;
+}
+
+// Replays the fused runs as (piece, grad) runs.
+template <typename Emit>
+int for_each_fused_run(const void* const* replicas, const mdx_grad_run* runs, int n_runs, const FusedArgs& f,
+                       Emit&& emit) {
+  const char* base0 = static_cast<const char*>(replicas[0]);
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].numel == 0) continue;
+    const mdx_piece pc{base0 + runs[k].offset * f.es, runs[k].offset, runs[k].numel};
+    void* grad = runs[k].grad;
+    const int rc = for_each_piece_run(&pc, &grad, 1, f.p, f.es, f.es, f.gs, f.E, f.U, emit);
+    if (rc != MDX_OK) return rc;
+  }
+  return MDX_OK;
+}
 
 }  // namespace
 }  // namespace mdx
@@ -217,10 +378,11 @@ int mdx_abi_version(void) { return MDX_ABI_VERSION; }
 const char* mdx_strerror(int code) {
   switch (code) {
     case MDX_OK: return "success";
-    case MDX_EINVAL: return "mdx: invalid argument (NULL pointer, negative count or size)";
+    case MDX_EINVAL: return "mdx: invalid argument (NULL pointer, negative count or size, bad plan)";
     case MDX_EDTYPE: return "mdx: unsupported dtype code (expected MDX_F32 or MDX_BF16)";
     case MDX_EWORLD: return "mdx: world size outside [1, MDX_MAX_WORLD] or rank outside [0, world)";
     case MDX_EALIAS: return "mdx: output overlaps an input it must not overlap";
+    case MDX_ESIZE: return "mdx: plan buffer missing or too small (required size returned)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -269,14 +431,21 @@ int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stre
 int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,
                       const int64_t* numels, int n_runs, void* out, void* stream) {
   if (!valid_dtype(dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
+  if (n_runs < 0 || replicas == nullptr) return MDX_EINVAL;
   if (n_runs > 0 && (offsets == nullptr || numels == nullptr)) return MDX_EINVAL;
   int64_t end = 0;
   bool any = false;
-  int rc = check_runs(replicas, world, offsets, numels, n_runs, &end, &any);
-  if (rc != MDX_OK || !any) return rc;
+  for (int k = 0; k < n_runs; ++k) {
+    if (offsets[k] < 0 || numels[k] < 0 || offsets[k] < end) return MDX_EINVAL;
+    end = offsets[k] + numels[k];
+    any = any || numels[k] > 0;
+  }
+  if (!any) return MDX_OK;
   if (out == nullptr) return MDX_EINVAL;
   const int es = dtype_size(dtype);
   for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
     // Same base = the in-place case; any other overlap of the reduced extent is rejected.
     if (replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
   }
@@ -292,77 +461,45 @@ int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const i
   const int E = frag_elems(es, es);
   const int U = allreduce_unroll(world, E * es);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  mdx_piece pieces[kRunsPerLaunch];
-  int np = 0;
   auto launch = [&](const PieceBatch& b) { return launch_allreduce(dtype, dtype, false, world, b, p, st); };
+  PieceBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int r = status(launch(b));
+    memset(&b, 0, sizeof(b));
+    return r;
+  };
   for (int k = 0; k < n_runs; ++k) {
     if (numels[k] == 0) continue;
-    pieces[np++] = mdx_piece{base0 + offsets[k] * es, offsets[k], numels[k]};
-    if (np == kRunsPerLaunch) {
-      rc = run_pieces(pieces, nullptr, np, p, es, es, 0, E, U, launch);
-      if (rc != MDX_OK) return rc;
-      np = 0;
-    }
+    const mdx_piece pc{base0 + offsets[k] * es, offsets[k], numels[k]};
+    const int rc = for_each_piece_run(&pc, nullptr, 1, p, es, es, 0, E, U,
+                                      [&](const Rec& r) { return push_piece(b, r, flush); });
+    if (rc != MDX_OK) return rc;
   }
-  return run_pieces(pieces, nullptr, np, p, es, es, 0, E, U, launch);
+  return flush();
 }
 
 int mdx_allreduce_unpack(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs,
                          int n_runs, void* out, int grad_dtype, float inv_scale, int32_t* found_inf,
                          void* stream) {
-  if (!valid_dtype(dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
-  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
-  if (n_runs < 0 || (n_runs > 0 && runs == nullptr) || replicas == nullptr) return MDX_EINVAL;
-  const int es = dtype_size(dtype), gs = dtype_size(grad_dtype);
-  int64_t end = 0;
-  bool any = false;
-  for (int k = 0; k < n_runs; ++k) {
-    if (runs[k].offset < 0 || runs[k].numel < 0 || runs[k].offset < end) return MDX_EINVAL;
-    if (runs[k].numel > 0 && runs[k].grad == nullptr) return MDX_EINVAL;
-    end = runs[k].offset + runs[k].numel;
-    any = any || runs[k].numel > 0;
-  }
-  if (!any) return MDX_OK;
-  for (int r = 0; r < world; ++r) {
-    if (replicas[r] == nullptr) return MDX_EINVAL;
-    if (out && replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
-  }
-  for (int k = 0; k < n_runs; ++k) {
-    const int64_t gb = runs[k].numel * gs;
-    for (int r = 0; r < world; ++r) {
-      if (any_overlap(runs[k].grad, gb, replicas[r], end * es)) return MDX_EALIAS;
-    }
-    if (out && any_overlap(runs[k].grad, gb, out, end * es)) return MDX_EALIAS;
-  }
-  ReduceParams p;
-  memset(&p, 0, sizeof(p));
-  for (int r = 0; r < world; ++r) p.peer[r] = replicas[r];
-  p.out = out;
-  p.world = world;
-  p.rank = 0;
-  p.pre = 1.0f;
-  p.inv_scale = inv_scale;
-  p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
-  p.found_inf = found_inf;
-  const char* base0 = static_cast<const char*>(replicas[0]);
-  const int E = frag_elems(es, gs);
-  const int U = allreduce_unroll(world, E * es);
+  FusedArgs f;
+  int rc = check_fused(replicas, world, dtype, runs, n_runs, out, grad_dtype, &f);
+  if (rc != MDX_OK || !f.any) return rc;
+  f.p.inv_scale = inv_scale;
+  f.p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
+  f.p.found_inf = found_inf;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  auto launch = [&](const PieceBatch& b) { return launch_allreduce(dtype, grad_dtype, true, world, b, p, st); };
-  mdx_piece pieces[kRunsPerLaunch];
-  void* grads[kRunsPerLaunch];
-  int np = 0;
-  for (int k = 0; k < n_runs; ++k) {
-    if (runs[k].numel == 0) continue;
-    pieces[np] = mdx_piece{base0 + runs[k].offset * es, runs[k].offset, runs[k].numel};
-    grads[np++] = runs[k].grad;
-    if (np == kRunsPerLaunch) {
-      const int rc = run_pieces(pieces, grads, np, p, es, es, gs, E, U, launch);
-      if (rc != MDX_OK) return rc;
-      np = 0;
-    }
-  }
-  return run_pieces(pieces, grads, np, p, es, es, gs, E, U, launch);
+  PieceBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int r = status(launch_allreduce(dtype, grad_dtype, true, world, b, f.p, st));
+    memset(&b, 0, sizeof(b));
+    return r;
+  };
+  rc = for_each_fused_run(replicas, runs, n_runs, f, [&](const Rec& r) { return push_piece(b, r, flush); });
+  return rc != MDX_OK ? rc : flush();
 }
 
 int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const* peers, int world,
@@ -401,6 +538,7 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   }
   p.out = shard;
   p.rank = rank;
+  p.world = world;
   p.inv_scale = inv_scale;
   p.found_inf = found_inf;
   p.pre = 1.0f;
@@ -419,7 +557,6 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   if (accumulate) flags |= kRedAccumulate;
   if (inv_scale != 1.0f) flags |= kRedUnscale;
   p.flags = flags;
-  p.world = world;
   const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
   const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
   const int E = frag_elems(is, os);
@@ -429,6 +566,91 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
     return launch_share(in_dtype, reduce_dtype, shard_dtype, wmax, b, p, st);
   };
   return run_pieces(own, nullptr, n_own, p, is, os, 0, E, U, launch);
+}
+
+// -- device plans -------------------------------------------------------------
+
+int mdx_plan_spans(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, void* plan,
+                   int64_t* plan_bytes) {
+  if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype)) return MDX_EDTYPE;
+  if (plan_bytes == nullptr) return MDX_EINVAL;
+  const int rc = check_spans(spans, n_spans, false);
+  if (rc != MDX_OK) return rc;
+  PlanHeader proto;
+  memset(&proto, 0, sizeof(proto));
+  proto.kind = kPlanSpans;
+  proto.dtype_a = src_dtype;
+  proto.dtype_b = dst_dtype;
+  for (int i = 0; i < n_spans; ++i) {
+    if (spans[i].numel > 0 && spans[i].src == nullptr) proto.reserved = 1;  // some span reads zeros
+  }
+  auto gen = [&](auto&& emit) { return for_each_span_run(spans, n_spans, src_dtype, dst_dtype, false, emit); };
+  return build_plan(proto, gen, plan, plan_bytes);
+}
+
+int mdx_plan_allreduce_unpack(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs,
+                              int n_runs, void* out, int grad_dtype, void* plan, int64_t* plan_bytes) {
+  if (plan_bytes == nullptr) return MDX_EINVAL;
+  FusedArgs f;
+  const int rc = check_fused(replicas, world, dtype, runs, n_runs, out, grad_dtype, &f);
+  if (rc != MDX_OK) return rc;
+  PlanHeader proto;
+  memset(&proto, 0, sizeof(proto));
+  proto.kind = kPlanGradRuns;
+  proto.dtype_a = dtype;
+  proto.dtype_b = grad_dtype;
+  proto.world = world;
+  if (f.any) {
+    for (int r = 0; r < world; ++r) proto.replicas[r] = addr(replicas[r]);
+    proto.out = addr(out);
+  }
+  auto gen = [&](auto&& emit) { return f.any ? for_each_fused_run(replicas, runs, n_runs, f, emit) : MDX_OK; };
+  return build_plan(proto, gen, plan, plan_bytes);
+}
+
+int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream) {
+  const PlanHeader* h;
+  DevTable t;
+  const int rc = plan_view(plan, d_plan, kPlanSpans, &h, &t);
+  if (rc != MDX_OK) return rc;
+  if (h->count == 0) return MDX_OK;
+  int32_t flags = 0;
+  if (scale != 1.0f) flags = divide ? kCopyDivide : kCopyScale;
+  CopyParams p{scale, flags, nullptr};
+  return status(launch_copy_dev(h->dtype_a, h->dtype_b, t, h->blocks, p, static_cast<hipStream_t>(stream)));
+}
+
+int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,
+                       void* stream) {
+  const PlanHeader* h;
+  DevTable t;
+  const int rc = plan_view(plan, d_plan, kPlanSpans, &h, &t);
+  if (rc != MDX_OK) return rc;
+  if (h->reserved) return MDX_EINVAL;  // unpack needs a source for every span
+  if (h->count == 0) return MDX_OK;
+  CopyParams p{inv_scale, (inv_scale != 1.0f ? kCopyScale : 0) | (found_inf ? kCopyCheck : 0), found_inf};
+  return status(launch_copy_dev(h->dtype_a, h->dtype_b, t, h->blocks, p, static_cast<hipStream_t>(stream)));
+}
+
+int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,
+                                 void* stream) {
+  const PlanHeader* h;
+  DevTable t;
+  const int rc = plan_view(plan, d_plan, kPlanGradRuns, &h, &t);
+  if (rc != MDX_OK) return rc;
+  if (h->count == 0) return MDX_OK;
+  ReduceParams p;
+  memset(&p, 0, sizeof(p));
+  for (int r = 0; r < h->world; ++r) p.peer[r] = reinterpret_cast<const void*>(h->replicas[r]);
+  p.out = reinterpret_cast<void*>(h->out);
+  p.world = h->world;
+  p.rank = 0;
+  p.pre = 1.0f;
+  p.inv_scale = inv_scale;
+  p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
+  p.found_inf = found_inf;
+  return status(launch_allreduce_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p,
+                                     static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

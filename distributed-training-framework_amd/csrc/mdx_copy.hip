@@ -34,21 +34,22 @@ struct CopyOp {
   }
 };
 
-template <typename S, typename D, int SCALE, bool CHECK>
-__global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p) {
+template <typename S, typename D, int SCALE, bool CHECK, typename View>
+__device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) {
   constexpr int E = frag_elems(int(sizeof(S)), int(sizeof(D)));
   constexpr int U = kCopyElemsPerThread / E;
   constexpr int VPB = kBlock * U;
   constexpr int EPB = kBlock * kCopyElemsPerThread;
 
   const int blk = int(blockIdx.x);
-  const int s = find_run(b.first_block, b.count, blk);
-  const int c = blk - b.first_block[s];
-  const int nblk = b.first_block[s + 1] - b.first_block[s];
-  const S* src = static_cast<const S*>(b.src[s]);
-  D* dst = static_cast<D*>(b.dst[s]);
-  const int64_t n = b.numel[s];
-  const int32_t h = b.head[s];
+  const int32_t* fb = tab.first_block();
+  const int s = find_run(fb, tab.count(), blk);
+  const int c = blk - fb[s];
+  const int nblk = fb[s + 1] - fb[s];
+  const S* src = static_cast<const S*>(tab.src(s));
+  D* dst = static_cast<D*>(tab.dst(s));
+  const int64_t n = tab.numel(s);
+  const int32_t h = tab.head(s);
   const int t = int(threadIdx.x);
   const bool zero_src = (src == nullptr);
   const CopyOp<S, D, SCALE, CHECK> op{p.scale};
@@ -109,23 +110,56 @@ __global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p)
   if constexpr (CHECK) flag_nonfinite(bad, p.found_inf);
 }
 
+// Table in the kernel-argument segment.
 template <typename S, typename D, int SCALE, bool CHECK>
-hipError_t launch4(const SpanBatch& b, const CopyParams& p, hipStream_t stream) {
-  const int blocks = b.first_block[b.count];
-  hipLaunchKernelGGL((copy_kernel<S, D, SCALE, CHECK>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
-  return hipGetLastError();
+__global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p) {
+  copy_body<S, D, SCALE, CHECK>(SpanArgView{b}, p);
 }
 
-template <typename S, typename D>
-hipError_t launch_typed(const SpanBatch& b, const CopyParams& p, hipStream_t stream) {
+// Table (plan) in device memory.
+template <typename S, typename D, int SCALE, bool CHECK>
+__global__ void __launch_bounds__(kBlock) copy_kernel_dev(DevTable t, CopyParams p) {
+  copy_body<S, D, SCALE, CHECK>(DevView{t}, p);
+}
+
+// Either table kind: Batch = SpanBatch (grid from its prefix) or DevTable.
+struct ArgLaunch {
+  const SpanBatch& b;
+  template <typename S, typename D, int SCALE, bool CHECK>
+  hipError_t go(const CopyParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((copy_kernel<S, D, SCALE, CHECK>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
+                       stream, b, p);
+    return hipGetLastError();
+  }
+};
+struct DevLaunch {
+  const DevTable& t;
+  int blocks;
+  template <typename S, typename D, int SCALE, bool CHECK>
+  hipError_t go(const CopyParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((copy_kernel_dev<S, D, SCALE, CHECK>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename S, typename D, typename L>
+hipError_t launch_typed(const L& l, const CopyParams& p, hipStream_t stream) {
   const bool check = (p.flags & kCopyCheck) != 0;
   if (p.flags & kCopyScale) {
-    return check ? launch4<S, D, kScaleMul, true>(b, p, stream) : launch4<S, D, kScaleMul, false>(b, p, stream);
+    return check ? l.template go<S, D, kScaleMul, true>(p, stream) : l.template go<S, D, kScaleMul, false>(p, stream);
   }
   if (p.flags & kCopyDivide) {
-    return check ? launch4<S, D, kScaleDiv, true>(b, p, stream) : launch4<S, D, kScaleDiv, false>(b, p, stream);
+    return check ? l.template go<S, D, kScaleDiv, true>(p, stream) : l.template go<S, D, kScaleDiv, false>(p, stream);
   }
-  return check ? launch4<S, D, kScaleNone, true>(b, p, stream) : launch4<S, D, kScaleNone, false>(b, p, stream);
+  return check ? l.template go<S, D, kScaleNone, true>(p, stream) : l.template go<S, D, kScaleNone, false>(p, stream);
+}
+
+template <typename L>
+hipError_t launch_any(int src_dtype, int dst_dtype, const L& l, const CopyParams& p, hipStream_t stream) {
+  if (src_dtype == MDX_F32 && dst_dtype == MDX_F32) return launch_typed<float, float>(l, p, stream);
+  if (src_dtype == MDX_F32 && dst_dtype == MDX_BF16) return launch_typed<float, bf16>(l, p, stream);
+  if (src_dtype == MDX_BF16 && dst_dtype == MDX_F32) return launch_typed<bf16, float>(l, p, stream);
+  return launch_typed<bf16, bf16>(l, p, stream);
 }
 
 }  // namespace
@@ -136,10 +170,12 @@ int copy_frag_elems(int src_dtype, int dst_dtype) {
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
                        hipStream_t stream) {
-  if (src_dtype == MDX_F32 && dst_dtype == MDX_F32) return launch_typed<float, float>(b, p, stream);
-  if (src_dtype == MDX_F32 && dst_dtype == MDX_BF16) return launch_typed<float, bf16>(b, p, stream);
-  if (src_dtype == MDX_BF16 && dst_dtype == MDX_F32) return launch_typed<bf16, float>(b, p, stream);
-  return launch_typed<bf16, bf16>(b, p, stream);
+  return launch_any(src_dtype, dst_dtype, ArgLaunch{b}, p, stream);
+}
+
+hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int blocks, const CopyParams& p,
+                           hipStream_t stream) {
+  return launch_any(src_dtype, dst_dtype, DevLaunch{t, blocks}, p, stream);
 }
 
 }  // namespace mdx

@@ -217,6 +217,83 @@ hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, co
                         const ReduceParams& p, hipStream_t stream);
 int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world);
 
+// ----------------------------------------------------------------------------
+// Work-table views.  A kernel body reads its runs through one of two views:
+// the batch passed by value in the kernel-argument segment (at most
+// kRunsPerLaunch runs), or a plan resident in device memory (any number of
+// runs, built once on the host and reused while the addresses hold).
+// ----------------------------------------------------------------------------
+
+struct DevTable {
+  const int32_t* first_block;  // count + 1 entries
+  const int32_t* head;
+  const int64_t* numel;
+  const uint64_t* a;  // span: src    piece: own
+  const uint64_t* b;  // span: dst    piece: grad
+  const int64_t* pos;  // piece position (pieces only)
+  int32_t count;
+};
+
+struct SpanArgView {
+  const SpanBatch& t;
+  __device__ __forceinline__ int count() const { return t.count; }
+  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
+  __device__ __forceinline__ const void* src(int i) const { return t.src[i]; }
+  __device__ __forceinline__ void* dst(int i) const { return t.dst[i]; }
+  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
+  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+};
+
+struct PieceArgView {
+  const PieceBatch& t;
+  __device__ __forceinline__ int count() const { return t.count; }
+  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
+  __device__ __forceinline__ const void* own(int i) const { return t.own[i]; }
+  __device__ __forceinline__ void* grad(int i) const { return t.grad[i]; }
+  __device__ __forceinline__ int64_t pos(int i) const { return t.pos[i]; }
+  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
+  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+};
+
+struct DevView {
+  DevTable t;
+  __device__ __forceinline__ int count() const { return t.count; }
+  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
+  __device__ __forceinline__ const void* src(int i) const { return reinterpret_cast<const void*>(t.a[i]); }
+  __device__ __forceinline__ void* dst(int i) const { return reinterpret_cast<void*>(t.b[i]); }
+  __device__ __forceinline__ const void* own(int i) const { return reinterpret_cast<const void*>(t.a[i]); }
+  __device__ __forceinline__ void* grad(int i) const { return reinterpret_cast<void*>(t.b[i]); }
+  __device__ __forceinline__ int64_t pos(int i) const { return t.pos[i]; }
+  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
+  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+};
+
+// Plan blob: this header followed by the DevTable arrays at the recorded
+// byte offsets.  The same bytes live on the host (read at launch for the grid
+// size and kernel arguments) and in device memory (read by the kernel).
+constexpr uint32_t kPlanMagic = 0x5058444du;  // "MDXP"
+enum : int32_t { kPlanSpans = 1, kPlanGradRuns = 2 };
+
+struct PlanHeader {
+  uint32_t magic;
+  int32_t kind;
+  int32_t count;
+  int32_t blocks;
+  int32_t dtype_a;  // spans: source dtype   grad runs: bucket dtype
+  int32_t dtype_b;  // spans: dest dtype     grad runs: gradient dtype
+  int32_t world;
+  int32_t reserved;
+  uint64_t replicas[MDX_MAX_WORLD];
+  uint64_t out;
+  int64_t off_first_block, off_head, off_numel, off_a, off_b, off_pos;
+  int64_t bytes;
+};
+
+hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int blocks, const CopyParams& p,
+                           hipStream_t stream);
+hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
+                                const ReduceParams& p, hipStream_t stream);
+
 inline int dtype_size(int dt) { return dt == MDX_BF16 ? 2 : 4; }
 
 }  // namespace mdx

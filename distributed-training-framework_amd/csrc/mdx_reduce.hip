@@ -7,6 +7,10 @@ hipError_t launch_allreduce_f32(int grad_dtype, bool unpack, int world, const Pi
                                 const ReduceParams& p, hipStream_t stream);
 hipError_t launch_allreduce_bf16(int grad_dtype, bool unpack, int world, const PieceBatch& b,
                                  const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_dev_f32(int grad_dtype, int world, const DevTable& t, int blocks,
+                                   const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_dev_bf16(int grad_dtype, int world, const DevTable& t, int blocks,
+                                    const ReduceParams& p, hipStream_t stream);
 hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
                              hipStream_t stream);
 hipError_t launch_share_generic(int in_dtype, int acc_dtype, int out_dtype, const PieceBatch& b,
@@ -16,6 +20,12 @@ hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, c
                             const ReduceParams& p, hipStream_t stream) {
   if (dtype == MDX_BF16) return launch_allreduce_bf16(grad_dtype, unpack, world, b, p, stream);
   return launch_allreduce_f32(grad_dtype, unpack, world, b, p, stream);
+}
+
+hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
+                                const ReduceParams& p, hipStream_t stream) {
+  if (dtype == MDX_BF16) return launch_allreduce_dev_bf16(grad_dtype, world, t, blocks, p, stream);
+  return launch_allreduce_dev_f32(grad_dtype, world, t, blocks, p, stream);
 }
 
 static bool fast_triple(int in_dtype, int acc_dtype, int out_dtype) {

@@ -31,20 +31,21 @@ namespace reduce_impl {
 // all-reduce (+ fused unpack)
 // ---------------------------------------------------------------------------
 
-template <typename T, typename G, int W, bool UNPACK>
-__global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceParams p) {
+template <typename T, typename G, int W, bool UNPACK, typename View>
+__device__ __forceinline__ void allreduce_body(const View& tab, const ReduceParams& p) {
   constexpr int E = frag_elems(int(sizeof(T)), UNPACK ? int(sizeof(G)) : int(sizeof(T)));
   constexpr int U = allreduce_unroll(W, E * int(sizeof(T)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
 
   const int blk = int(blockIdx.x);
-  const int s = find_run(b.first_block, b.count, blk);
-  const int c = blk - b.first_block[s];
-  const int nblk = b.first_block[s + 1] - b.first_block[s];
-  const int64_t pos = b.pos[s];
-  const int64_t n = b.numel[s];
-  const int32_t h = b.head[s];
+  const int32_t* fb = tab.first_block();
+  const int s = find_run(fb, tab.count(), blk);
+  const int c = blk - fb[s];
+  const int nblk = fb[s + 1] - fb[s];
+  const int64_t pos = tab.pos(s);
+  const int64_t n = tab.numel(s);
+  const int32_t h = tab.head(s);
   const int rank = p.rank;
   const int t = int(threadIdx.x);
   const bool unscale = (p.flags & kRedUnscale) != 0;
@@ -53,10 +54,10 @@ __global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceP
   const T* src[W];
 #pragma unroll
   for (int r = 0; r < W; ++r) {
-    src[r] = (r == rank) ? static_cast<const T*>(b.own[s]) : static_cast<const T*>(p.peer[r]) + pos;
+    src[r] = (r == rank) ? static_cast<const T*>(tab.own(s)) : static_cast<const T*>(p.peer[r]) + pos;
   }
   T* out = p.out ? static_cast<T*>(p.out) + pos : nullptr;
-  G* grad = static_cast<G*>(b.grad[s]);
+  G* grad = static_cast<G*>(tab.grad(s));
   bool bad = false;
 
   auto finish = [&](T acc) -> G {
@@ -122,33 +123,71 @@ __global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceP
   }
 }
 
-template <typename T, typename G, bool UNPACK, int W>
-hipError_t launch_allreduce_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
-  const int blocks = b.first_block[b.count];
-  hipLaunchKernelGGL((allreduce_kernel<T, G, W, UNPACK>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
-  return hipGetLastError();
+// Table in the kernel-argument segment.
+template <typename T, typename G, int W, bool UNPACK>
+__global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceParams p) {
+  allreduce_body<T, G, W, UNPACK>(PieceArgView{b}, p);
+}
+
+// Table (plan) in device memory; the fused all-reduce + unpack only.
+template <typename T, typename G, int W>
+__global__ void __launch_bounds__(kBlock) allreduce_unpack_kernel_dev(DevTable t, ReduceParams p) {
+  allreduce_body<T, G, W, true>(DevView{t}, p);
+}
+
+template <typename T, typename G, bool UNPACK>
+struct ArgAllreduce {
+  const PieceBatch& b;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_kernel<T, G, W, UNPACK>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
+                       stream, b, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename T, typename G>
+struct DevAllreduceUnpack {
+  const DevTable& t;
+  int blocks;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_unpack_kernel_dev<T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename L>
+hipError_t by_world(int world, const L& l, const ReduceParams& p, hipStream_t stream) {
+  switch (world) {
+    case 1: return l.template go<1>(p, stream);
+    case 2: return l.template go<2>(p, stream);
+    case 3: return l.template go<3>(p, stream);
+    case 4: return l.template go<4>(p, stream);
+    case 5: return l.template go<5>(p, stream);
+    case 6: return l.template go<6>(p, stream);
+    case 7: return l.template go<7>(p, stream);
+    case 8: return l.template go<8>(p, stream);
+    case 9: return l.template go<9>(p, stream);
+    case 10: return l.template go<10>(p, stream);
+    case 11: return l.template go<11>(p, stream);
+    case 12: return l.template go<12>(p, stream);
+    case 13: return l.template go<13>(p, stream);
+    case 14: return l.template go<14>(p, stream);
+    case 15: return l.template go<15>(p, stream);
+    default: return l.template go<16>(p, stream);
+  }
 }
 
 template <typename T, typename G, bool UNPACK>
 hipError_t launch_allreduce(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
-  switch (world) {
-    case 1: return launch_allreduce_w<T, G, UNPACK, 1>(b, p, stream);
-    case 2: return launch_allreduce_w<T, G, UNPACK, 2>(b, p, stream);
-    case 3: return launch_allreduce_w<T, G, UNPACK, 3>(b, p, stream);
-    case 4: return launch_allreduce_w<T, G, UNPACK, 4>(b, p, stream);
-    case 5: return launch_allreduce_w<T, G, UNPACK, 5>(b, p, stream);
-    case 6: return launch_allreduce_w<T, G, UNPACK, 6>(b, p, stream);
-    case 7: return launch_allreduce_w<T, G, UNPACK, 7>(b, p, stream);
-    case 8: return launch_allreduce_w<T, G, UNPACK, 8>(b, p, stream);
-    case 9: return launch_allreduce_w<T, G, UNPACK, 9>(b, p, stream);
-    case 10: return launch_allreduce_w<T, G, UNPACK, 10>(b, p, stream);
-    case 11: return launch_allreduce_w<T, G, UNPACK, 11>(b, p, stream);
-    case 12: return launch_allreduce_w<T, G, UNPACK, 12>(b, p, stream);
-    case 13: return launch_allreduce_w<T, G, UNPACK, 13>(b, p, stream);
-    case 14: return launch_allreduce_w<T, G, UNPACK, 14>(b, p, stream);
-    case 15: return launch_allreduce_w<T, G, UNPACK, 15>(b, p, stream);
-    default: return launch_allreduce_w<T, G, UNPACK, 16>(b, p, stream);
-  }
+  return by_world(world, ArgAllreduce<T, G, UNPACK>{b}, p, stream);
+}
+
+template <typename T, typename G>
+hipError_t launch_allreduce_unpack_dev(int world, const DevTable& t, int blocks, const ReduceParams& p,
+                                       hipStream_t stream) {
+  return by_world(world, DevAllreduceUnpack<T, G>{t, blocks}, p, stream);
 }
 
 // ---------------------------------------------------------------------------

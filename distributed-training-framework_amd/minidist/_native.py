@@ -39,6 +39,11 @@ SIGNATURES: dict[str, tuple] = {
         [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
     ),
     "mdx_cast_f32_bf16": (_i32, [_vp, _vp, _i64, _vp]),
+    "mdx_plan_spans": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
+    "mdx_plan_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp]),
+    "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp]),
+    "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
+    "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_strerror": (ctypes.c_char_p, [_i32]),
     "mdx_abi_version": (_i32, []),
 }
@@ -205,6 +210,69 @@ def reduce_scatter_share(
         shard, shard_dtype, int(accumulate), inv_scale, found_inf, stream,
     )
     check(rc, "mdx_reduce_scatter_share")
+
+
+MDX_ESIZE = -5
+
+
+class Plan:
+    """A device-resident work plan: host bytes (kernel arguments, grid) + device copy.
+
+    Built once by ``mdx_plan_*``; launched any number of times while the
+    addresses frozen into it stay valid.  Keeping the object alive keeps the
+    device copy alive (it is released to torch's stream-ordered allocator)."""
+
+    __slots__ = ("host", "device", "host_ptr", "device_ptr")
+
+    def __init__(self, host: np.ndarray, device_tensor):
+        self.host = host
+        self.device = device_tensor
+        self.host_ptr = host.ctypes.data
+        self.device_ptr = device_tensor.data_ptr()
+
+
+def _build_plan(call, what: str, device) -> Plan:
+    size = ctypes.c_int64(0)
+    rc = call(None, ctypes.byref(size))
+    if rc not in (0, MDX_ESIZE):
+        check(rc, what)
+    host = np.zeros((size.value + 7) // 8, dtype=np.uint64)  # 8-byte aligned
+    cap = ctypes.c_int64(host.nbytes)
+    check(call(host.ctypes.data, ctypes.byref(cap)), what)
+    dev = torch.from_numpy(host.view(np.uint8)).to(device)
+    return Plan(host, dev)
+
+
+def plan_spans(spans: np.ndarray, src_dtype: int, dst_dtype: int, device) -> Plan:
+    return _build_plan(
+        lambda buf, size: lib().mdx_plan_spans(_ptr(spans), len(spans), src_dtype, dst_dtype, buf, size),
+        "mdx_plan_spans", device,
+    )
+
+
+def plan_allreduce_unpack(
+    replicas: list[int], dtype: int, runs: np.ndarray, out: int | None, grad_dtype: int, device
+) -> Plan:
+    reps = _ptrs(replicas)
+    return _build_plan(
+        lambda buf, size: lib().mdx_plan_allreduce_unpack(
+            reps, len(replicas), dtype, _ptr(runs), len(runs), out, grad_dtype, buf, size
+        ),
+        "mdx_plan_allreduce_unpack", device,
+    )
+
+
+def pack_planned(plan: Plan, scale: float, divide: bool, stream: int) -> None:
+    check(lib().mdx_pack_planned(plan.host_ptr, plan.device_ptr, scale, int(divide), stream), "mdx_pack_planned")
+
+
+def unpack_planned(plan: Plan, inv_scale: float, found_inf: int | None, stream: int) -> None:
+    check(lib().mdx_unpack_planned(plan.host_ptr, plan.device_ptr, inv_scale, found_inf, stream), "mdx_unpack_planned")
+
+
+def allreduce_unpack_planned(plan: Plan, inv_scale: float, found_inf: int | None, stream: int) -> None:
+    rc = lib().mdx_allreduce_unpack_planned(plan.host_ptr, plan.device_ptr, inv_scale, found_inf, stream)
+    check(rc, "mdx_allreduce_unpack_planned")
 
 
 def cast_f32_bf16(src: int, dst: int, numel: int, stream: int) -> None:

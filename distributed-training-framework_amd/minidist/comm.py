@@ -372,6 +372,28 @@ class ResidentGroup:
         )
         return StreamWork(stream) if async_op else None
 
+    def plan_all_reduce_unpack(self, buffer: torch.Tensor, runs, grad_dtype: torch.dtype) -> "_native.Plan":
+        """Device plan of :meth:`all_reduce_unpack` for fixed ``runs`` (one dispatch per launch)."""
+        _native.require_device_tensor(buffer, "all_reduce input")
+        arena, off = self._locate(buffer)
+        bases = [b + off * arena.esize for b in arena.row_ptrs]
+        return _native.plan_allreduce_unpack(
+            bases, _native.dtype_code(arena.dtype), runs, buffer.data_ptr(), _native.dtype_code(grad_dtype),
+            buffer.device,
+        )
+
+    def all_reduce_unpack_planned(
+        self, plan: "_native.Plan", device: torch.device, inv_scale: float = 1.0,
+        found_inf: torch.Tensor | None = None, async_op: bool = False,
+    ):
+        """Launch a plan from :meth:`plan_all_reduce_unpack` on the current stream."""
+        stream = torch.cuda.current_stream(device)
+        _native.allreduce_unpack_planned(
+            plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
+            stream.cuda_stream,
+        )
+        return StreamWork(stream) if async_op else None
+
     def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
         _native.require_device_tensor(input_, "reduce_scatter input")

@@ -56,6 +56,7 @@ enum {
   MDX_EDTYPE = -2,    /* dtype code not in {MDX_F32, MDX_BF16}            */
   MDX_EWORLD = -3,    /* world outside [1, MDX_MAX_WORLD] or rank >= world */
   MDX_EALIAS = -4,    /* an output overlaps an input it must not overlap  */
+  MDX_ESIZE = -5,     /* plan buffer missing or too small                 */
 };
 
 #define MDX_MAX_WORLD 16
@@ -168,6 +169,49 @@ MDX_API int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void
  * Replaces `src = flat_shard.to(param_dtype)` in _FSDPUnit.unshard
  * (minidist/fsdp.py:178-180). */
 MDX_API int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Device-resident plans: the same work as mdx_pack / mdx_unpack /
+ * mdx_allreduce_unpack, for any number of spans or runs in ONE dispatch.
+ *
+ * A plan is the kernel-ready form of a span or grad-run table (with every
+ * run's alignment head, workgroup range and the reduction's replica bases).
+ * mdx_plan_* writes it into caller-provided host memory (8-byte aligned);
+ * the caller copies those bytes to device memory and then launches with both
+ * copies -- the host copy supplies the grid and kernel arguments, the device
+ * copy is what the workgroups read -- for as long as the addresses inside
+ * stay valid.  This is the device-side pointer/offset table that lets the
+ * ~150 gradients of a GPT-2 step (most of them small biases and norms) move
+ * in one launch per stage.
+ *
+ * Sizing: on entry *plan_bytes is the capacity of `plan`; on return it is the
+ * size the plan needs.  With plan == NULL or too small a capacity nothing is
+ * written and MDX_ESIZE is returned.  Inputs are validated as by the direct
+ * entry points.
+ * ------------------------------------------------------------------------- */
+
+/* Plan for mdx_pack_planned / mdx_unpack_planned over `spans` (whose addresses
+ * are frozen into the plan).  Replaces, for a fixed set of gradients, the
+ * per-bucket tables of _Bucket.gather_into_buffer / scatter_from_buffer
+ * (minidist/ddp.py:75-102). */
+MDX_API int mdx_plan_spans(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, void* plan,
+                           int64_t* plan_bytes);
+
+/* Plan for mdx_allreduce_unpack_planned (arguments as mdx_allreduce_unpack). */
+MDX_API int mdx_plan_allreduce_unpack(const void* const* replicas, int world, int dtype,
+                                      const mdx_grad_run* runs, int n_runs, void* out, int grad_dtype,
+                                      void* plan, int64_t* plan_bytes);
+
+/* mdx_pack over a plan: one dispatch.  `plan` = host copy, `d_plan` = device copy. */
+MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream);
+
+/* mdx_unpack over a plan whose every span has a source: one dispatch. */
+MDX_API int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,
+                               void* stream);
+
+/* mdx_allreduce_unpack over a plan: one dispatch. */
+MDX_API int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale,
+                                         int32_t* found_inf, void* stream);
 
 /* Static description of a status code. */
 MDX_API const char* mdx_strerror(int code);

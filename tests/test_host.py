@@ -239,3 +239,60 @@ def test_span_table_layout_is_the_c_struct():
     assert a.itemsize == 24 and a.tobytes() == np.array([1, 2, 3], dtype="<i8").tobytes()
     b = nat.pieces_array([(5, 6, 7)])
     assert b.itemsize == 24
+
+
+# ---------------------------------------------------------------------------
+# Device plans: building is host-only work
+# ---------------------------------------------------------------------------
+
+
+def _plan_header(buf: np.ndarray) -> dict:
+    h = buf.view(np.int32)
+    return {"magic": int(h[0]) & 0xFFFFFFFF, "kind": int(h[1]), "count": int(h[2]), "blocks": int(h[3])}
+
+
+def test_plan_spans_sizing_and_layout():
+    L = nat.lib()
+    # 150 spans (more than one kernel-argument batch), 16-byte aligned, 4096 fp32 each
+    rows = [(0x10000000 + i * 65536, 0x40000000 + i * 65536, 4096) for i in range(150)]
+    spans = nat.spans_array(rows)
+    size = ctypes.c_int64(0)
+    assert L.mdx_plan_spans(spans.ctypes.data, 150, 0, 0, None, ctypes.byref(size)) == nat.MDX_ESIZE
+    need = size.value
+    assert need > 150 * 36
+    buf = np.zeros((need + 7) // 8, dtype=np.uint64)
+    small = ctypes.c_int64(need - 8)
+    assert L.mdx_plan_spans(spans.ctypes.data, 150, 0, 0, buf.ctypes.data, ctypes.byref(small)) == nat.MDX_ESIZE
+    cap = ctypes.c_int64(buf.nbytes)
+    assert L.mdx_plan_spans(spans.ctypes.data, 150, 0, 0, buf.ctypes.data, ctypes.byref(cap)) == 0
+    h = _plan_header(buf)
+    assert h["magic"] == 0x5058444D and h["kind"] == 1 and h["count"] == 150
+    assert h["blocks"] == 150  # 4096 fp32 = one workgroup (256 lanes x 16 elements) per span
+
+
+def test_plan_allreduce_unpack_builds_and_rejects_overlap():
+    L = nat.lib()
+    reps = (ctypes.c_void_p * 8)(*[0x100000000 + r * (1 << 24) for r in range(8)])
+    runs = nat.grad_runs_array([(i * 1024, 1000, 0x900000000 + i * 8192) for i in range(100)])
+    size = ctypes.c_int64(0)
+    rc = L.mdx_plan_allreduce_unpack(reps, 8, 0, runs.ctypes.data, 100, reps[0], 0, None, ctypes.byref(size))
+    assert rc == nat.MDX_ESIZE
+    buf = np.zeros((size.value + 7) // 8, dtype=np.uint64)
+    cap = ctypes.c_int64(buf.nbytes)
+    assert L.mdx_plan_allreduce_unpack(reps, 8, 0, runs.ctypes.data, 100, reps[0], 0, buf.ctypes.data, ctypes.byref(cap)) == 0
+    h = _plan_header(buf)
+    assert h["kind"] == 2 and h["count"] == 100 and h["blocks"] == 100
+    bad = nat.grad_runs_array([(0, 16, 0x100000000 + 8)])  # gradient inside replica 0
+    assert L.mdx_plan_allreduce_unpack(reps, 8, 0, bad.ctypes.data, 1, reps[0], 0, buf.ctypes.data, ctypes.byref(cap)) == -4
+
+
+def test_planned_launch_rejects_bad_plans_before_launch():
+    L = nat.lib()
+    junk = np.zeros(64, dtype=np.uint64)
+    assert L.mdx_pack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, 0, None) == -1  # no magic
+    assert L.mdx_pack_planned(None, None, 1.0, 0, None) == -1
+    spans = nat.spans_array([(0, 0x40000000, 64)])  # a zero-source span
+    size = ctypes.c_int64(junk.nbytes)
+    assert L.mdx_plan_spans(spans.ctypes.data, 1, 0, 0, junk.ctypes.data, ctypes.byref(size)) == 0
+    assert L.mdx_unpack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, None, None) == -1  # unpack needs sources
+    assert L.mdx_allreduce_unpack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, None, None) == -1  # wrong kind

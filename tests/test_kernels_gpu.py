@@ -417,3 +417,63 @@ def test_reduce_scatter_rejects_shard_overlapping_a_peer():
             nat.pieces_array([(own.data_ptr(), 0, 128)]), [0, peers[1].data_ptr()], 0, 0, 0, True,
             peers[1, 64:].data_ptr(), 0, False, 1.0, None, stream(),
         )
+
+
+# ---------------------------------------------------------------------------
+# Device plans: one dispatch for any number of runs
+# ---------------------------------------------------------------------------
+
+
+def test_pack_and_unpack_planned_match_direct(rng):
+    """150 spans (beyond one kernel-argument batch) through a device plan, vs the oracle."""
+    sizes = [int(x) for x in rng.integers(0, 3000, 150)]
+    srcs = [to_dev(values(rng, n + 1, o.F32))[1:] for n in sizes]  # odd offsets: misaligned sources
+    offs, off = [], 0
+    for n in sizes:
+        offs.append(off)
+        off += n
+    bucket = empty_dev(off + 3, o.F32)
+    rows = [(s.data_ptr(), bucket.data_ptr() + a * 4, n) for s, a, n in zip(srcs, offs, sizes, strict=True)]
+    plan = nat.plan_spans(nat.spans_array(rows), 0, 0, DEV)
+    nat.pack_planned(plan, nat.f32(1.0 / 8), False, stream())
+    got = to_host(bucket)
+    for s, a, n in zip(srcs, offs, sizes, strict=True):
+        want = o.mul_scalar(to_host(s), o.F32, 1.0 / 8)
+        assert same_bits(got[a : a + n], want)
+    # unpack back into bf16 gradients with unscale + found-inf
+    grads = [empty_dev(n, o.BF16) for n in sizes]
+    urows = [(bucket.data_ptr() + a * 4, g.data_ptr(), n) for g, a, n in zip(grads, offs, sizes, strict=True)]
+    uplan = nat.plan_spans(nat.spans_array(urows), 0, 1, DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.unpack_planned(uplan, nat.f32(0.5), flag.data_ptr(), stream())
+    bad = False
+    for g, a, n in zip(grads, offs, sizes, strict=True):
+        want = o.mul_scalar(o.convert(got[a : a + n], o.F32, o.BF16), o.BF16, 0.5)
+        bad |= bool((~o.isfinite(want, o.BF16)).any())
+        assert same_bits(to_host(g), want)
+    assert bool(flag.item()) == bad
+
+
+@pytest.mark.parametrize("W,bdt,gdt", [(8, o.F32, o.F32), (4, o.F32, o.BF16), (3, o.BF16, o.BF16)])
+def test_allreduce_unpack_planned_matches_oracle(rng, W, bdt, gdt):
+    numels = [int(x) for x in rng.integers(1, 5000, 120)]
+    offs, off = [], 0
+    for n in numels:
+        offs.append(off)
+        off += n + int(rng.integers(0, 3))
+    reps_host = [values(rng, off, bdt, scale=1e3) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    grads = [empty_dev(n, gdt) for n in numels]
+    runs = nat.grad_runs_array([(a, n, g.data_ptr()) for a, n, g in zip(offs, numels, grads, strict=True)])
+    plan = nat.plan_allreduce_unpack([r.data_ptr() for r in reps], code(bdt), runs, reps[0].data_ptr(), code(gdt), DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for _ in range(2):  # a plan is reusable; the second launch reduces the first one's output
+        before = [to_host(r) for r in reps]
+        nat.allreduce_unpack_planned(plan, nat.f32(2.0**-10), flag.data_ptr(), stream())
+        want0 = before[0].copy()
+        for a, n, g in zip(offs, numels, grads, strict=True):
+            acc = o.allreduce_sum([b[a : a + n] for b in before], bdt)
+            want0[a : a + n] = acc
+            v = o.mul_scalar(o.convert(acc, bdt, gdt), gdt, 2.0**-10)
+            assert same_bits(to_host(g), v)
+        assert same_bits(to_host(reps[0]), want0)
