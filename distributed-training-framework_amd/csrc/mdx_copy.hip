@@ -12,7 +12,8 @@
 // (a fragment = E elements = one or two 16-byte vectors).  Lane t of chunk c
 // handles fragments c*VPB + u*kBlock + t, so every vector instruction of a
 // wave touches 64 consecutive 16-byte vectors; all U fragments are loaded
-// (non-temporal: each byte is read once per step) before the first store.
+// (non-temporal: each byte is read once per step) before the first store,
+// and stored non-temporally (the next reader is a later pipeline stage).
 // A span whose src and dst cannot both be brought to 16-byte alignment by the
 // same element offset is processed with coalesced scalar accesses instead.
 #include "mdx_internal.h"
@@ -79,7 +80,7 @@ __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) 
         D out[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) out[k] = op(in[u][k], bad);
-        vstore<D, E, false>(vd + v * E, out);
+        vstore<D, E, true>(vd + v * E, out);
       }
     }
     // Ragged edges: the head before the aligned body (first chunk) and the

@@ -163,7 +163,7 @@ struct CopyParams {
 constexpr int frag_elems(int src_size, int dst_size) {
   return 16 / (src_size < dst_size ? src_size : dst_size);
 }
-constexpr int kCopyElemsPerThread = 16;
+constexpr int kCopyElemsPerThread = 32;
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
                        hipStream_t stream);

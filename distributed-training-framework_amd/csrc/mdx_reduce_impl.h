@@ -99,12 +99,12 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
           for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(x[u][r][k]));
           y[k] = acc;
         }
-        if (out) vstore<T, E, false>(out + i, y);
+        if (out) vstore<T, E, true>(out + i, y);
         if constexpr (UNPACK) {
           G gy[E];
 #pragma unroll
           for (int k = 0; k < E; ++k) gy[k] = finish(y[k]);
-          vstore<G, E, false>(grad + i, gy);
+          vstore<G, E, true>(grad + i, gy);
         }
       }
     }
@@ -288,7 +288,7 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
           }
           y[k] = finish(acc, ACC ? prev[u][k] : zero_of<Out>());
         }
-        vstore<Out, E, false>(out + i, y);
+        vstore<Out, E, true>(out + i, y);
       }
     }
     if (c == 0 && t < h && t < n) element(t);
