@@ -204,7 +204,7 @@ def main() -> int:
     red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
 
     traffic = None
-    tfile = ROOT / "profiles" / "allreduce_sum_gpt2_124m_w8_traffic.json"
+    tfile = ROOT / "profiles" / "allreduce_unpack_gpt2_124m_w8_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
 
