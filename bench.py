@@ -235,7 +235,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "allreduce_kernel<float,float,8,true> (mdx_allreduce_unpack_planned, all 18 buckets in one dispatch)",
+            "kernel": "allreduce_unpack_kernel_dev<float, float, 8> (mdx_allreduce_unpack_planned, all 18 buckets in one dispatch)",
             "achieved": round(red_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

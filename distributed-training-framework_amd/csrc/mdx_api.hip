@@ -306,16 +306,18 @@ bool is_pow2(int w) { return w > 0 && (w & (w - 1)) == 0; }
 // parameters and launch geometry they imply.
 struct FusedArgs {
   ReduceParams p;
-  int es, gs, E, U;
+  int es, os, gs, E, U;
   bool any;
 };
 
-int check_fused(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs, int n_runs,
-                void* out, int grad_dtype, FusedArgs* f) {
-  if (!valid_dtype(dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
+// `dtype` is the contributions' dtype, `out_dtype` the bucket's (equal, or
+// bf16 -> fp32 for the widening variant).
+int check_fused(const void* const* replicas, int world, int dtype, int out_dtype, const mdx_grad_run* runs,
+                int n_runs, void* out, int grad_dtype, FusedArgs* f) {
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
   if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
   if (n_runs < 0 || (n_runs > 0 && runs == nullptr) || replicas == nullptr) return MDX_EINVAL;
-  const int es = dtype_size(dtype), gs = dtype_size(grad_dtype);
+  const int es = dtype_size(dtype), os = dtype_size(out_dtype), gs = dtype_size(grad_dtype);
   int64_t end = 0;
   bool any = false;
   for (int k = 0; k < n_runs; ++k) {
@@ -326,16 +328,21 @@ int check_fused(const void* const* replicas, int world, int dtype, const mdx_gra
   }
   f->any = any;
   if (!any) return MDX_OK;
+  // In place (out == a replica's base) is the same element read then written
+  // by one lane, which needs equal element sizes; every other overlap races.
+  const bool same_size = es == os;
   for (int r = 0; r < world; ++r) {
     if (replicas[r] == nullptr) return MDX_EINVAL;
-    if (out && replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
+    if (out && !(same_size && replicas[r] == out) && any_overlap(replicas[r], end * es, out, end * os)) {
+      return MDX_EALIAS;
+    }
   }
   for (int k = 0; k < n_runs; ++k) {
     const int64_t gb = runs[k].numel * gs;
     for (int r = 0; r < world; ++r) {
       if (any_overlap(runs[k].grad, gb, replicas[r], end * es)) return MDX_EALIAS;
     }
-    if (out && any_overlap(runs[k].grad, gb, out, end * es)) return MDX_EALIAS;
+    if (out && any_overlap(runs[k].grad, gb, out, end * os)) return MDX_EALIAS;
   }
   memset(&f->p, 0, sizeof(f->p));
   for (int r = 0; r < world; ++r) f->p.peer[r] = replicas[r];
@@ -345,11 +352,15 @@ int check_fused(const void* const* replicas, int world, int dtype, const mdx_gra
   f->p.pre = 1.0f;
   f->p.inv_scale = 1.0f;
   f->es = es;
+  f->os = os;
   f->gs = gs;
-  f->E = frag_elems(es, gs);
+  f->E = frag_elems(min_size(es, os), gs);  // as the kernel's compile-time fragment
   f->U = allreduce_unroll(world, f->E * es);
   return MDX_OK;
 }
+
+// The widening variant exists for bf16 contributions into fp32 buckets.
+bool wide_dtypes(int dtype, int out_dtype) { return dtype == MDX_BF16 && out_dtype == MDX_F32; }
 
 // Replays the fused runs as (piece, grad) runs.
 template <typename Emit>
@@ -360,10 +371,33 @@ int for_each_fused_run(const void* const* replicas, const mdx_grad_run* runs, in
     if (runs[k].numel == 0) continue;
     const mdx_piece pc{base0 + runs[k].offset * f.es, runs[k].offset, runs[k].numel};
     void* grad = runs[k].grad;
-    const int rc = for_each_piece_run(&pc, &grad, 1, f.p, f.es, f.es, f.gs, f.E, f.U, emit);
+    const int rc = for_each_piece_run(&pc, &grad, 1, f.p, f.es, f.os, f.gs, f.E, f.U, emit);
     if (rc != MDX_OK) return rc;
   }
   return MDX_OK;
+}
+
+// Plan of a fused all-reduce + unpack (widening when out_dtype != dtype).
+int plan_grad_runs(const void* const* replicas, int world, int dtype, int out_dtype, const mdx_grad_run* runs,
+                   int n_runs, void* out, int grad_dtype, float prescale, void* plan, int64_t* plan_bytes) {
+  if (plan_bytes == nullptr) return MDX_EINVAL;
+  FusedArgs f;
+  const int rc = check_fused(replicas, world, dtype, out_dtype, runs, n_runs, out, grad_dtype, &f);
+  if (rc != MDX_OK) return rc;
+  PlanHeader proto;
+  memset(&proto, 0, sizeof(proto));
+  proto.kind = kPlanGradRuns;
+  proto.dtype_a = dtype;
+  proto.dtype_b = grad_dtype;
+  proto.reduce_dtype = out_dtype;
+  proto.prescale = prescale;
+  proto.world = world;
+  if (f.any) {
+    for (int r = 0; r < world; ++r) proto.replicas[r] = addr(replicas[r]);
+    proto.out = addr(out);
+  }
+  auto gen = [&](auto&& emit) { return f.any ? for_each_fused_run(replicas, runs, n_runs, f, emit) : MDX_OK; };
+  return build_plan(proto, gen, plan, plan_bytes);
 }
 
 }  // namespace
@@ -484,7 +518,7 @@ int mdx_allreduce_unpack(const void* const* replicas, int world, int dtype, cons
                          int n_runs, void* out, int grad_dtype, float inv_scale, int32_t* found_inf,
                          void* stream) {
   FusedArgs f;
-  int rc = check_fused(replicas, world, dtype, runs, n_runs, out, grad_dtype, &f);
+  int rc = check_fused(replicas, world, dtype, dtype, runs, n_runs, out, grad_dtype, &f);
   if (rc != MDX_OK || !f.any) return rc;
   f.p.inv_scale = inv_scale;
   f.p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
@@ -495,6 +529,30 @@ int mdx_allreduce_unpack(const void* const* replicas, int world, int dtype, cons
   auto flush = [&]() -> int {
     if (b.count == 0) return MDX_OK;
     const int r = status(launch_allreduce(dtype, grad_dtype, true, world, b, f.p, st));
+    memset(&b, 0, sizeof(b));
+    return r;
+  };
+  rc = for_each_fused_run(replicas, runs, n_runs, f, [&](const Rec& r) { return push_piece(b, r, flush); });
+  return rc != MDX_OK ? rc : flush();
+}
+
+int mdx_allreduce_unpack_wide(const void* const* replicas, int world, int wire_dtype, const mdx_grad_run* runs,
+                              int n_runs, void* out, int reduce_dtype, int grad_dtype, float prescale,
+                              float inv_scale, int32_t* found_inf, void* stream) {
+  if (!wide_dtypes(wire_dtype, reduce_dtype)) return MDX_EDTYPE;
+  FusedArgs f;
+  int rc = check_fused(replicas, world, wire_dtype, reduce_dtype, runs, n_runs, out, grad_dtype, &f);
+  if (rc != MDX_OK || !f.any) return rc;
+  f.p.pre = prescale;
+  f.p.inv_scale = inv_scale;
+  f.p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
+  f.p.found_inf = found_inf;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  PieceBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int r = status(launch_allreduce_wide(grad_dtype, world, b, f.p, st));
     memset(&b, 0, sizeof(b));
     return r;
   };
@@ -590,22 +648,15 @@ int mdx_plan_spans(const mdx_span* spans, int n_spans, int src_dtype, int dst_dt
 
 int mdx_plan_allreduce_unpack(const void* const* replicas, int world, int dtype, const mdx_grad_run* runs,
                               int n_runs, void* out, int grad_dtype, void* plan, int64_t* plan_bytes) {
-  if (plan_bytes == nullptr) return MDX_EINVAL;
-  FusedArgs f;
-  const int rc = check_fused(replicas, world, dtype, runs, n_runs, out, grad_dtype, &f);
-  if (rc != MDX_OK) return rc;
-  PlanHeader proto;
-  memset(&proto, 0, sizeof(proto));
-  proto.kind = kPlanGradRuns;
-  proto.dtype_a = dtype;
-  proto.dtype_b = grad_dtype;
-  proto.world = world;
-  if (f.any) {
-    for (int r = 0; r < world; ++r) proto.replicas[r] = addr(replicas[r]);
-    proto.out = addr(out);
-  }
-  auto gen = [&](auto&& emit) { return f.any ? for_each_fused_run(replicas, runs, n_runs, f, emit) : MDX_OK; };
-  return build_plan(proto, gen, plan, plan_bytes);
+  return plan_grad_runs(replicas, world, dtype, dtype, runs, n_runs, out, grad_dtype, 1.0f, plan, plan_bytes);
+}
+
+int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int world, int wire_dtype,
+                                   const mdx_grad_run* runs, int n_runs, void* out, int reduce_dtype,
+                                   int grad_dtype, float prescale, void* plan, int64_t* plan_bytes) {
+  if (!wide_dtypes(wire_dtype, reduce_dtype)) return MDX_EDTYPE;
+  return plan_grad_runs(replicas, world, wire_dtype, reduce_dtype, runs, n_runs, out, grad_dtype, prescale, plan,
+                        plan_bytes);
 }
 
 int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream) {
@@ -645,12 +696,15 @@ int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv
   p.out = reinterpret_cast<void*>(h->out);
   p.world = h->world;
   p.rank = 0;
-  p.pre = 1.0f;
+  p.pre = h->prescale;
   p.inv_scale = inv_scale;
   p.flags = inv_scale != 1.0f ? kRedUnscale : 0;
   p.found_inf = found_inf;
-  return status(launch_allreduce_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p,
-                                     static_cast<hipStream_t>(stream)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (h->reduce_dtype != h->dtype_a) {
+    return status(launch_allreduce_wide_dev(h->dtype_b, h->world, t, h->blocks, p, st));
+  }
+  return status(launch_allreduce_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p, st));
 }
 
 }  // extern "C"

@@ -160,9 +160,8 @@ struct CopyParams {
 };
 
 // Elements per 16-byte-aligned fragment and per thread for a dtype pair.
-constexpr int frag_elems(int src_size, int dst_size) {
-  return 16 / (src_size < dst_size ? src_size : dst_size);
-}
+constexpr int min_size(int a, int b) { return a < b ? a : b; }
+constexpr int frag_elems(int src_size, int dst_size) { return 16 / min_size(src_size, dst_size); }
 constexpr int kCopyElemsPerThread = 32;
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
@@ -216,6 +215,9 @@ hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, c
 hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, const PieceBatch& b,
                         const ReduceParams& p, hipStream_t stream);
 int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world);
+// Widening fused all-reduce + unpack: bf16 contributions, fp32 bucket.
+hipError_t launch_allreduce_wide(int grad_dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                                 hipStream_t stream);
 
 // ----------------------------------------------------------------------------
 // Work-table views.  A kernel body reads its runs through one of two views:
@@ -279,10 +281,12 @@ struct PlanHeader {
   int32_t kind;
   int32_t count;
   int32_t blocks;
-  int32_t dtype_a;  // spans: source dtype   grad runs: bucket dtype
+  int32_t dtype_a;  // spans: source dtype   grad runs: contribution dtype
   int32_t dtype_b;  // spans: dest dtype     grad runs: gradient dtype
   int32_t world;
   int32_t reserved;
+  int32_t reduce_dtype;  // grad runs: bucket (out) dtype; differs from dtype_a when widening
+  float prescale;        // grad runs: receiver-side pre-scale of every contribution (widening only)
   uint64_t replicas[MDX_MAX_WORLD];
   uint64_t out;
   int64_t off_first_block, off_head, off_numel, off_a, off_b, off_pos;
@@ -293,6 +297,8 @@ hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int 
                            hipStream_t stream);
 hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
                                 const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_wide_dev(int grad_dtype, int world, const DevTable& t, int blocks,
+                                     const ReduceParams& p, hipStream_t stream);
 
 inline int dtype_size(int dt) { return dt == MDX_BF16 ? 2 : 4; }
 

@@ -11,6 +11,14 @@
 //   which is scatter_from_buffer's copy_ followed by unscale_'s mul_ and
 //   isfinite, fused so the bucket is not read back.
 //
+// allreduce_wide_kernel<In, T, G, W> (+ _dev): the same fused all-reduce +
+// unpack for contributions that travel in a narrower dtype In than the bucket
+// dtype T (bf16 gradients summed into fp32 buckets).  Each contribution is
+// widened and pre-scaled at the receiver, x_r = rnd_T(cvt_T(c_r[p]) * pre),
+// which is exactly the value the sender's pack (`copy_` into a T bucket, then
+// `mul_(1/W)`) would have put on the wire; the rank-ordered sum, the write of
+// the T bucket and the unpack epilogue are as above.
+//
 // share_kernel<In, Acc, Out, WMAX>: FSDP's reduce-scatter share, runtime
 // W <= WMAX.  x_r = cvt_Acc(contribution_r[p]); x_r = rnd_Acc(x_r * pre | x_r / pre);
 // acc = rank-ordered sum in Acc; y = cvt_Out(acc); y = rnd_Out(out + y) when
@@ -31,10 +39,11 @@ namespace reduce_impl {
 // all-reduce (+ fused unpack)
 // ---------------------------------------------------------------------------
 
-template <typename T, typename G, int W, bool UNPACK, typename View>
+template <typename In, typename T, typename G, int W, bool UNPACK, bool PRE, typename View>
 __device__ __forceinline__ void allreduce_body(const View& tab, const ReduceParams& p) {
-  constexpr int E = frag_elems(int(sizeof(T)), UNPACK ? int(sizeof(G)) : int(sizeof(T)));
-  constexpr int U = allreduce_unroll(W, E * int(sizeof(T)));
+  constexpr int E = frag_elems(min_size(int(sizeof(In)), int(sizeof(T))),
+                               UNPACK ? int(sizeof(G)) : int(sizeof(T)));
+  constexpr int U = allreduce_unroll(W, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
 
@@ -50,15 +59,22 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   const int t = int(threadIdx.x);
   const bool unscale = (p.flags & kRedUnscale) != 0;
   const float inv = p.inv_scale;
+  const float pre = p.pre;
 
-  const T* src[W];
+  const In* src[W];
 #pragma unroll
   for (int r = 0; r < W; ++r) {
-    src[r] = (r == rank) ? static_cast<const T*>(tab.own(s)) : static_cast<const T*>(p.peer[r]) + pos;
+    src[r] = (r == rank) ? static_cast<const In*>(tab.own(s)) : static_cast<const In*>(p.peer[r]) + pos;
   }
   T* out = p.out ? static_cast<T*>(p.out) + pos : nullptr;
   G* grad = static_cast<G*>(tab.grad(s));
   bool bad = false;
+
+  auto widen = [&](In x) -> T {
+    T a = Cvt<In, T>::run(x);
+    if constexpr (PRE) a = from_f32<T>(to_f32(a) * pre);
+    return a;
+  };
 
   auto finish = [&](T acc) -> G {
     G g = Cvt<T, G>::run(acc);
@@ -68,22 +84,22 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
     return g;
   };
   auto element = [&](int64_t i) {
-    T acc = src[0][i];
+    T acc = widen(src[0][i]);
 #pragma unroll
-    for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(src[r][i]));
+    for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(src[r][i])));
     if (out) out[i] = acc;
     if constexpr (UNPACK) grad[i] = finish(acc);
   };
 
   if (h >= 0) {
     const int64_t nvec = (n - h) / E;
-    T x[U][W][E];
+    In x[U][W][E];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
       if (v < nvec) {
 #pragma unroll
-        for (int r = 0; r < W; ++r) vload<T, E, true>(x[u][r], src[r] + h + v * E);
+        for (int r = 0; r < W; ++r) vload<In, E, true>(x[u][r], src[r] + h + v * E);
       }
     }
 #pragma unroll
@@ -94,9 +110,9 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
         T y[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-          T acc = x[u][0][k];
+          T acc = widen(x[u][0][k]);
 #pragma unroll
-          for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(x[u][r][k]));
+          for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(x[u][r][k])));
           y[k] = acc;
         }
         if (out) vstore<T, E, true>(out + i, y);
@@ -126,13 +142,24 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
 // Table in the kernel-argument segment.
 template <typename T, typename G, int W, bool UNPACK>
 __global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceParams p) {
-  allreduce_body<T, G, W, UNPACK>(PieceArgView{b}, p);
+  allreduce_body<T, T, G, W, UNPACK, false>(PieceArgView{b}, p);
 }
 
 // Table (plan) in device memory; the fused all-reduce + unpack only.
 template <typename T, typename G, int W>
 __global__ void __launch_bounds__(kBlock) allreduce_unpack_kernel_dev(DevTable t, ReduceParams p) {
-  allreduce_body<T, G, W, true>(DevView{t}, p);
+  allreduce_body<T, T, G, W, true, false>(DevView{t}, p);
+}
+
+// Widening variants (fused all-reduce + unpack with pre-scale at the receiver).
+template <typename In, typename T, typename G, int W>
+__global__ void __launch_bounds__(kBlock) allreduce_wide_kernel(PieceBatch b, ReduceParams p) {
+  allreduce_body<In, T, G, W, true, true>(PieceArgView{b}, p);
+}
+
+template <typename In, typename T, typename G, int W>
+__global__ void __launch_bounds__(kBlock) allreduce_wide_kernel_dev(DevTable t, ReduceParams p) {
+  allreduce_body<In, T, G, W, true, true>(DevView{t}, p);
 }
 
 template <typename T, typename G, bool UNPACK>
@@ -153,6 +180,28 @@ struct DevAllreduceUnpack {
   template <int W>
   hipError_t go(const ReduceParams& p, hipStream_t stream) const {
     hipLaunchKernelGGL((allreduce_unpack_kernel_dev<T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename In, typename T, typename G>
+struct ArgWide {
+  const PieceBatch& b;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_wide_kernel<In, T, G, W>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
+                       stream, b, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename In, typename T, typename G>
+struct DevWide {
+  const DevTable& t;
+  int blocks;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_wide_kernel_dev<In, T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
     return hipGetLastError();
   }
 };
@@ -188,6 +237,17 @@ template <typename T, typename G>
 hipError_t launch_allreduce_unpack_dev(int world, const DevTable& t, int blocks, const ReduceParams& p,
                                        hipStream_t stream) {
   return by_world(world, DevAllreduceUnpack<T, G>{t, blocks}, p, stream);
+}
+
+template <typename In, typename T, typename G>
+hipError_t launch_allreduce_wide(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  return by_world(world, ArgWide<In, T, G>{b}, p, stream);
+}
+
+template <typename In, typename T, typename G>
+hipError_t launch_allreduce_wide_dev(int world, const DevTable& t, int blocks, const ReduceParams& p,
+                                     hipStream_t stream) {
+  return by_world(world, DevWide<In, T, G>{t, blocks}, p, stream);
 }
 
 // ---------------------------------------------------------------------------

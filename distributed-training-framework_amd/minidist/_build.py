@@ -26,6 +26,7 @@ SOURCES = [
     "mdx_copy.hip",
     "mdx_reduce.hip",
     "mdx_allreduce_f32.hip",
+    "mdx_allreduce_wide.hip",
     "mdx_allreduce_bf16.hip",
     "mdx_share_fast.hip",
     "mdx_share_generic.hip",

@@ -24,7 +24,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libmdx.so"
 MDX_F32 = 0
 MDX_BF16 = 1
 MDX_MAX_WORLD = 16
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_unscale_found_inf": (_i32, [_vp, _i32, _i32, _f32, _vp, _vp]),
     "mdx_allreduce_sum": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "mdx_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp]),
+    "mdx_allreduce_unpack_wide": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _f32, _f32, _vp, _vp]),
     "mdx_reduce_scatter_share": (
         _i32,
         [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
@@ -41,6 +42,9 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_cast_f32_bf16": (_i32, [_vp, _vp, _i64, _vp]),
     "mdx_plan_spans": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "mdx_plan_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp]),
+    "mdx_plan_allreduce_unpack_wide": (
+        _i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
+    ),
     "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp]),
     "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
@@ -191,6 +195,17 @@ def allreduce_unpack(
     check(rc, "mdx_allreduce_unpack")
 
 
+def allreduce_unpack_wide(
+    replicas: list[int], wire_dtype: int, runs: np.ndarray, out: int | None, reduce_dtype: int, grad_dtype: int,
+    prescale: float, inv_scale: float, found_inf: int | None, stream: int,
+) -> None:
+    rc = lib().mdx_allreduce_unpack_wide(
+        _ptrs(replicas), len(replicas), wire_dtype, _ptr(runs), len(runs), out, reduce_dtype, grad_dtype,
+        prescale, inv_scale, found_inf, stream,
+    )
+    check(rc, "mdx_allreduce_unpack_wide")
+
+
 def reduce_scatter_share(
     own: np.ndarray,
     peers: list[int],
@@ -259,6 +274,20 @@ def plan_allreduce_unpack(
             reps, len(replicas), dtype, _ptr(runs), len(runs), out, grad_dtype, buf, size
         ),
         "mdx_plan_allreduce_unpack", device,
+    )
+
+
+def plan_allreduce_unpack_wide(
+    replicas: list[int], wire_dtype: int, runs: np.ndarray, out: int | None, reduce_dtype: int, grad_dtype: int,
+    prescale: float, device,
+) -> Plan:
+    reps = _ptrs(replicas)
+    return _build_plan(
+        lambda buf, size: lib().mdx_plan_allreduce_unpack_wide(
+            reps, len(replicas), wire_dtype, _ptr(runs), len(runs), out, reduce_dtype, grad_dtype, prescale,
+            buf, size,
+        ),
+        "mdx_plan_allreduce_unpack_wide", device,
     )
 
 

@@ -382,6 +382,27 @@ class ResidentGroup:
             buffer.device,
         )
 
+    def plan_all_reduce_unpack_wide(
+        self, wire: torch.Tensor, bucket: torch.Tensor, runs, grad_dtype: torch.dtype, prescale: float
+    ) -> "_native.Plan":
+        """Device plan of a widening fused all-reduce + unpack.
+
+        ``wire`` is this rank's row of bf16 contributions (a symmetric
+        buffer); every replica's element is widened to fp32 and multiplied by
+        ``prescale`` where it is read, the W values are summed in rank order
+        into ``bucket`` (fp32, same element offsets as ``wire``) and unpacked
+        into the gradients of ``runs``."""
+        _native.require_device_tensor(wire, "all_reduce input")
+        _native.require_device_tensor(bucket, "all_reduce output")
+        arena, off = self._locate(wire)
+        bases = [b + off * arena.esize for b in arena.row_ptrs]
+        if bucket.numel() < wire.numel():
+            raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
+        return _native.plan_allreduce_unpack_wide(
+            bases, _native.dtype_code(arena.dtype), runs, bucket.data_ptr(), _native.dtype_code(bucket.dtype),
+            _native.dtype_code(grad_dtype), _native.f32(prescale), wire.device,
+        )
+
     def all_reduce_unpack_planned(
         self, plan: "_native.Plan", device: torch.device, inv_scale: float = 1.0,
         found_inf: torch.Tensor | None = None, async_op: bool = False,

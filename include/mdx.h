@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 1
+#define MDX_ABI_VERSION 2
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -147,6 +147,27 @@ MDX_API int mdx_allreduce_unpack(const void* const* replicas, int world, int dty
                                  const mdx_grad_run* runs, int n_runs, void* out, int grad_dtype,
                                  float inv_scale, int32_t* found_inf, void* stream);
 
+/* mdx_allreduce_unpack for contributions narrower than the bucket: bf16
+ * contributions (wire_dtype = MDX_BF16) summed into an fp32 bucket
+ * (reduce_dtype = MDX_F32; other pairs return MDX_EDTYPE).  Each contribution
+ * is widened and pre-scaled where it is received,
+ *   x_r = rnd_f32(f32(rep[r][o+j]) * prescale),
+ * then acc = ((x_0 + x_1) + ...) in fp32, out[o+j] = acc (fp32, when out !=
+ * NULL) and the unpack / unscale / found-inf epilogue of mdx_allreduce_unpack.
+ * With prescale = fp32(1/W) this is bit-identical to the reference chain for a
+ * bucket of fp32 holding bf16 gradients: _Bucket.gather_into_buffer's
+ * `flat.copy_(p.grad)` (widening) + `buffer.mul_(1/W)` (minidist/ddp.py:
+ * 85-91), comm.all_reduce (minidist/comm.py:223-234), scatter_from_buffer's
+ * `p.grad.copy_(reduced)` (ddp.py:100-101, fp32 -> bf16 RNE) and unscale_
+ * (minidist/amp.py:212-213) -- while the contributions travel at half the
+ * bytes.  The fp32 accumulation is FSDP's reduce_dtype arithmetic
+ * (minidist/fsdp.py:218-229) applied to DDP buckets.  `out` must not overlap
+ * any replica. */
+MDX_API int mdx_allreduce_unpack_wide(const void* const* replicas, int world, int wire_dtype,
+                                      const mdx_grad_run* runs, int n_runs, void* out, int reduce_dtype,
+                                      int grad_dtype, float prescale, float inv_scale, int32_t* found_inf,
+                                      void* stream);
+
 /* This rank's share of a SUM reduce-scatter, with FSDP's pre-division,
  * dtype changes and optional accumulation fused.
  * Replaces _FSDPUnit.reduce_scatter_grads (minidist/fsdp.py:215-237): widen
@@ -202,6 +223,12 @@ MDX_API int mdx_plan_allreduce_unpack(const void* const* replicas, int world, in
                                       const mdx_grad_run* runs, int n_runs, void* out, int grad_dtype,
                                       void* plan, int64_t* plan_bytes);
 
+/* Plan for mdx_allreduce_unpack_planned with the widening of
+ * mdx_allreduce_unpack_wide (arguments as there; prescale is frozen into the plan). */
+MDX_API int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int world, int wire_dtype,
+                                           const mdx_grad_run* runs, int n_runs, void* out, int reduce_dtype,
+                                           int grad_dtype, float prescale, void* plan, int64_t* plan_bytes);
+
 /* mdx_pack over a plan: one dispatch.  `plan` = host copy, `d_plan` = device copy. */
 MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream);
 
@@ -209,7 +236,7 @@ MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, 
 MDX_API int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,
                                void* stream);
 
-/* mdx_allreduce_unpack over a plan: one dispatch. */
+/* mdx_allreduce_unpack (or _wide, by the plan) over a plan: one dispatch. */
 MDX_API int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale,
                                          int32_t* found_inf, void* stream);
 

@@ -241,14 +241,17 @@ def ddp_pipeline(
     cap_mb: float,
     rank: int,
     inv_scale: float | None,
+    bucket_dtype: str | None = None,
 ) -> dict:
     """The whole per-rank bucket pipeline for one step.
 
     pack(1/W) per replica (ddp.py:243-244) -> rank-ordered SUM (comm.py:234)
     -> unpack into rank ``rank``'s grads (ddp.py:269-273) -> optional
     unscale + found-inf (amp.py:201-219).  Grads are assumed to carry their
-    parameter's dtype.  Returns the layout, the reduced buckets, and the final
-    grads of ``rank`` with their dtypes.
+    parameter's dtype.  The bucket dtype is the first parameter's
+    (ddp.py:84) unless ``bucket_dtype`` overrides it; a parameter without a
+    gradient gets one of its own dtype.  Returns the layout, the reduced
+    buckets, and the final grads of ``rank`` with their dtypes.
     """
     W = len(replica_grads)
     nbytes = [n * itemsize(d) for n, d in zip(numels, param_dtypes, strict=True)]
@@ -257,7 +260,7 @@ def ddp_pipeline(
     final_dtypes: list[str] = list(param_dtypes)
     reduced_buckets = []
     for idxs in layout:
-        bdt = param_dtypes[idxs[0]]
+        bdt = bucket_dtype or param_dtypes[idxs[0]]
         bn = [numels[i] for i in idxs]
         packed = [
             pack([replica_grads[r][i] for i in idxs], [param_dtypes[i] for i in idxs], bn, bdt, 1.0 / W)
@@ -265,10 +268,9 @@ def ddp_pipeline(
         ]
         red = allreduce_sum(packed, bdt)
         reduced_buckets.append(red)
-        own = [param_dtypes[i] if replica_grads[rank][i] is not None else None for i in idxs]
-        for i, g, gd in zip(idxs, unpack(red, bdt, bn, own), own, strict=True):
+        own = [param_dtypes[i] for i in idxs]
+        for i, g in zip(idxs, unpack(red, bdt, bn, own), strict=True):
             final[i] = g
-            final_dtypes[i] = bdt if gd is None else gd
     found = None
     if inv_scale is not None:
         final, found = unscale_found_inf(final, final_dtypes, inv_scale)

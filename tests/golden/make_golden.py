@@ -78,7 +78,14 @@ def _build_buckets(nbytes: list[int], cap_mb: float) -> list[list[int]]:
     return buckets
 
 
-def ddp_case(dtype: torch.dtype, W: int, rank: int, cap_mb: float, scale: float, seed: int, inject_inf: bool) -> dict:
+def ddp_case(
+    dtype: torch.dtype, W: int, rank: int, cap_mb: float, scale: float, seed: int, inject_inf: bool,
+    bucket_dtype: torch.dtype | None = None,
+) -> dict:
+    """``bucket_dtype`` replays a bucket whose dtype differs from the gradients'
+    (the first parameter's dtype in the reference, ddp.py:84): ``copy_`` then
+    widens on pack and rounds on unpack."""
+    bucket_dtype = bucket_dtype or dtype
     g = torch.Generator().manual_seed(seed)
     n_params = len(DDP_NUMELS)
     grads: list[list[torch.Tensor | None]] = []
@@ -102,7 +109,7 @@ def ddp_case(dtype: torch.dtype, W: int, rank: int, cap_mb: float, scale: float,
         numel = sum(DDP_NUMELS[i] for i in idxs)
         packed = []
         for r in range(W):
-            buf = torch.zeros(numel, dtype=dtype)  # ddp.py:83-84
+            buf = torch.zeros(numel, dtype=bucket_dtype)  # ddp.py:83-84
             off = 0
             for i in idxs:
                 flat = buf[off : off + DDP_NUMELS[i]]
@@ -121,7 +128,8 @@ def ddp_case(dtype: torch.dtype, W: int, rank: int, cap_mb: float, scale: float,
         for i in idxs:
             sl = acc[off : off + DDP_NUMELS[i]]
             if grads[rank][i] is None:
-                final[i] = sl.clone()  # ddp.py:98-99
+                # ddp.py:98-99; torch only accepts a gradient of the parameter dtype
+                final[i] = sl.clone() if bucket_dtype == dtype else torch.empty(sl.shape, dtype=dtype).copy_(sl)
             else:
                 final[i] = grads[rank][i].clone().copy_(sl)  # ddp.py:100-101
             off += DDP_NUMELS[i]
@@ -133,6 +141,7 @@ def ddp_case(dtype: torch.dtype, W: int, rank: int, cap_mb: float, scale: float,
         unscaled.append(u)
     out = {
         "W": W, "rank": rank, "cap_mb": cap_mb, "scale": scale, "dtype": str(dtype),
+        "bucket_dtype": str(bucket_dtype),
         "numels": np.array(DDP_NUMELS), "found_inf": bool(found_inf.item() > 0),
         "layout": json.dumps(layout),
     }
@@ -211,6 +220,11 @@ def main() -> None:
     np.savez_compressed(
         HERE / "ddp_bf16_w8.npz",
         **ddp_case(torch.bfloat16, W=8, rank=5, cap_mb=0.0005, scale=2.0**12, seed=7, inject_inf=False),
+    )
+    np.savez_compressed(
+        HERE / "ddp_bf16_f32bucket_w8.npz",
+        **ddp_case(torch.bfloat16, W=8, rank=3, cap_mb=0.0005, scale=2.0**12, seed=13, inject_inf=True,
+                   bucket_dtype=torch.float32),
     )
     np.savez_compressed(HERE / "fsdp_bf16_w4.npz", **fsdp_case(4, torch.bfloat16, torch.float32, seed=8))
     np.savez_compressed(HERE / "fsdp_bf16_w3.npz", **fsdp_case(3, torch.bfloat16, torch.float32, seed=9))

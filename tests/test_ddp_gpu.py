@@ -50,18 +50,19 @@ class Flat(nn.Module):
 
 
 def stage_peers(ddp: DDP, replica_grads, dtypes, rank: int, W: int) -> None:
-    """Write every peer's packed, 1/W-scaled bucket into its resident row."""
+    """Write every peer's contribution into its resident row, in the bucket's wire format:
+    its packed, 1/W-scaled bucket, or for a widening bucket its raw gradients."""
     params = [p for p in ddp.module.parameters() if p.requires_grad]
     index = {id(p): i for i, p in enumerate(params)}
     for b, bucket in enumerate(ddp._buckets):
         idxs = [index[id(p)] for p in bucket.params]
         rows = ddp.bucket_replicas(b)
-        bdt = dtypes[idxs[0]]
+        wire_dtype, prescaled = ddp.bucket_wire_format(b)
         for r in range(W):
             if r == rank:
                 continue
             packed = o.pack([replica_grads[r][i] for i in idxs], [dtypes[i] for i in idxs],
-                            [params[i].numel() for i in idxs], bdt, 1.0 / W)
+                            [params[i].numel() for i in idxs], odt(wire_dtype), 1.0 / W if prescaled else 1.0)
             rows[r].copy_(dev_from(packed, rows[r].shape))
 
 
@@ -300,3 +301,60 @@ def test_fused_unscale_in_ddp_unpack(rng, inject):
         ddp.finish_gradient_sync()  # second sync before update(): refused
     scaler.update()
 
+
+
+# ---------------------------------------------------------------------------
+# reduce_dtype: bf16 gradients accumulated in fp32 buckets (BASELINE cfg4 at small scale)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("W,rank", [(2, 1), (8, 5), (3, 0)])
+@pytest.mark.parametrize("cap", [1e-6, 0.01, 25.0])
+@pytest.mark.parametrize("inject", [False, True])
+def test_reduce_dtype_widening_bitwise(rng, W, rank, cap, inject):
+    """Widening buckets == the reference chain with an fp32 bucket (copy_, mul_(1/W), SUM, copy_, unscale)."""
+    shapes = [(33,), (64, 8), (5,), (130,), (1,), (7, 9), (256, 4), (3,)]
+    S = 2.0**12
+    model = Flat(shapes, torch.bfloat16)
+    scaler = DistributedGradScaler(init_scale=S)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, grad_scaler=scaler,
+              reduce_dtype=torch.float32)
+    assert all(b.widening and b.buffer is None for b in ddp._buckets)
+    grads = synthetic_grads(rng, shapes, W, torch.bfloat16, S)
+    grads[rank][2] = None
+    if inject:
+        grads[(rank + 1) % W][5][7] = np.uint16(0x7F80)  # +inf in a peer's bf16 gradient
+    dts = [o.BF16] * len(shapes)
+    stage_peers(ddp, grads, dts, rank, W)
+    for p, g in zip(model.parameters(), grads[rank], strict=True):
+        p.grad = None if g is None else dev_from(g, p.shape)
+    opt = torch.optim.SGD(model.parameters(), lr=0.0)
+    ddp.finish_gradient_sync()
+    found = scaler.unscale_(opt)
+    want = o.ddp_pipeline(grads, dts, [int(np.prod(s)) for s in shapes], cap, rank, 1.0 / S, bucket_dtype=o.F32)
+    for i, p in enumerate(model.parameters()):
+        assert p.grad.dtype == torch.bfloat16
+        got = host_bits(p.grad)
+        assert same_bits(got, want["grads"][i]), f"param {i}: " + first_mismatch(got, want["grads"][i])
+    for b, bucket in enumerate(ddp._buckets):
+        assert bucket.buffer.dtype == torch.float32 and bucket.wire.dtype == torch.bfloat16
+        assert same_bits(host_bits(bucket.buffer), want["reduced"][b])
+    assert found == want["found_inf"] == inject
+    scaler.update()
+
+
+def test_reduce_dtype_on_matching_params_is_the_plain_path(rng):
+    """fp32 parameters with reduce_dtype=fp32: ordinary (non-widening) buckets, same results."""
+    shapes = [(300, 7), (11,), (1024,)]
+    W, rank = 4, 2
+    grads = synthetic_grads(rng, shapes, W, torch.float32, 1.0)
+    model = Flat(shapes)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=0.01, reduce_dtype=torch.float32)
+    assert not any(b.widening for b in ddp._buckets)
+    stage_peers(ddp, grads, [o.F32] * 3, rank, W)
+    for p, g in zip(model.parameters(), grads[rank], strict=True):
+        p.grad = dev_from(g, p.shape)
+    ddp.finish_gradient_sync()
+    want = o.ddp_pipeline(grads, [o.F32] * 3, [int(np.prod(s)) for s in shapes], 0.01, rank, None)
+    for i, p in enumerate(model.parameters()):
+        assert same_bits(host_bits(p.grad), want["grads"][i])

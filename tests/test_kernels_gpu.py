@@ -477,3 +477,142 @@ def test_allreduce_unpack_planned_matches_oracle(rng, W, bdt, gdt):
             v = o.mul_scalar(o.convert(acc, bdt, gdt), gdt, 2.0**-10)
             assert same_bits(to_host(g), v)
         assert same_bits(to_host(reps[0]), want0)
+
+
+# ---------------------------------------------------------------------------
+# Widening fused all-reduce + unpack (bf16 contributions, fp32 bucket)
+# ---------------------------------------------------------------------------
+
+
+def _wide_want(reps_host, a, n, W, gdt, inv_scale):
+    """The reference chain for an fp32 bucket of bf16 gradients: copy_ (widen), mul_(1/W), SUM, copy_, mul_."""
+    xs = [o.mul_scalar(o.convert(h[a : a + n], o.BF16, o.F32), o.F32, 1.0 / W) for h in reps_host]
+    acc = o.allreduce_sum(xs, o.F32)
+    v = o.convert(acc, o.F32, gdt)
+    if inv_scale != 1.0:
+        v = o.mul_scalar(v, gdt, inv_scale)
+    return acc, v
+
+
+@pytest.mark.parametrize("gdt", [o.BF16, o.F32])
+@pytest.mark.parametrize("W", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("inv_scale,write_out", [(1.0, True), (2.0**-12, True), (1.0 / 3, False)])
+def test_allreduce_unpack_wide_matches_oracle(rng, gdt, W, inv_scale, write_out):
+    numels = [1, 7, 64, 4096, 3, 12345, 256, 5, 8, 9]
+    offs, off = [], 3
+    for n in numels:
+        offs.append(off)
+        off += n + int(rng.integers(0, 3))
+    extent = off + 4
+    reps_host = [values(rng, extent, o.BF16, scale=1e3) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    out = empty_dev(extent, o.F32)
+    out_before = to_host(out)
+    grads = [empty_dev(n + 2, gdt) for n in numels]
+    shifts = [int(rng.integers(0, 3)) for _ in numels]
+    runs = nat.grad_runs_array(
+        [(a, n, g.data_ptr() + s * esize(gdt)) for a, n, g, s in zip(offs, numels, grads, shifts, strict=True)]
+    )
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.allreduce_unpack_wide(
+        [r.data_ptr() for r in reps], nat.MDX_BF16, runs, out.data_ptr() if write_out else None, nat.MDX_F32,
+        code(gdt), nat.f32(1.0 / W), nat.f32(inv_scale), flag.data_ptr(), stream(),
+    )
+    any_bad = False
+    want_out = out_before.copy()
+    for a, n, g, s in zip(offs, numels, grads, shifts, strict=True):
+        acc, v = _wide_want(reps_host, a, n, W, gdt, inv_scale)
+        want_out[a : a + n] = acc
+        any_bad |= bool((~o.isfinite(v, gdt)).any())
+        got = to_host(g)
+        assert same_bits(got[s : s + n], v), first_mismatch(got[s : s + n], v)
+        sent = np.concatenate([got[:s], got[s + n :]])
+        assert np.all(sent == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32))
+    got_out = to_host(out)
+    assert same_bits(got_out, want_out if write_out else out_before), first_mismatch(got_out, want_out)
+    for r in range(W):
+        assert same_bits(to_host(reps[r]), reps_host[r])
+    assert bool(flag.item()) == any_bad
+
+
+@pytest.mark.parametrize("W,gdt", [(8, o.BF16), (4, o.F32), (5, o.BF16)])
+def test_allreduce_unpack_wide_planned_matches_oracle(rng, W, gdt):
+    numels = [int(x) for x in rng.integers(1, 5000, 120)]
+    offs, off = [], 0
+    for n in numels:
+        offs.append(off)
+        off += n + int(rng.integers(0, 3))
+    reps_host = [values(rng, off, o.BF16, scale=1e3) for _ in range(W)]
+    reps = [to_dev(h) for h in reps_host]
+    out = empty_dev(off, o.F32)
+    grads = [empty_dev(n, gdt) for n in numels]
+    runs = nat.grad_runs_array([(a, n, g.data_ptr()) for a, n, g in zip(offs, numels, grads, strict=True)])
+    plan = nat.plan_allreduce_unpack_wide(
+        [r.data_ptr() for r in reps], nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_F32, code(gdt),
+        nat.f32(1.0 / W), DEV,
+    )
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for _ in range(2):  # reusable: the second launch gives the same result
+        nat.allreduce_unpack_planned(plan, nat.f32(2.0**-10), flag.data_ptr(), stream())
+        got_out = to_host(out)
+        bad = False
+        for a, n, g in zip(offs, numels, grads, strict=True):
+            acc, v = _wide_want(reps_host, a, n, W, gdt, 2.0**-10)
+            bad |= bool((~o.isfinite(v, gdt)).any())
+            assert same_bits(got_out[a : a + n], acc)
+            assert same_bits(to_host(g), v)
+        assert bool(flag.item()) == bad
+
+
+def test_allreduce_unpack_wide_rejects_bad_dtypes_and_overlap():
+    reps = [torch.zeros(1024, dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    out = torch.zeros(1024, device=DEV)
+    g = torch.zeros(16, dtype=torch.bfloat16, device=DEV)
+    runs = nat.grad_runs_array([(0, 16, g.data_ptr())])
+    ptrs = [r.data_ptr() for r in reps]
+    with pytest.raises(RuntimeError, match="dtype"):  # only bf16 -> fp32 widens
+        nat.allreduce_unpack_wide(ptrs, nat.MDX_F32, runs, out.data_ptr(), nat.MDX_F32, 1, 0.5, 1.0, None, stream())
+    with pytest.raises(RuntimeError, match="dtype"):
+        nat.allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_BF16, 1, 0.5, 1.0, None, stream())
+    with pytest.raises(RuntimeError, match="overlaps"):  # the fp32 bucket may not alias a bf16 row
+        nat.allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, reps[0].data_ptr(), nat.MDX_F32, 1, 0.5, 1.0, None,
+                                  stream())
+
+
+def test_golden_widening_replay():
+    """The fixture replays torch's chain for an fp32 bucket of bf16 grads; the wide kernel must match it."""
+    d = load_golden("ddp_bf16_f32bucket_w8.npz")
+    W, rank = int(d["W"]), int(d["rank"])
+    numels = [int(n) for n in d["numels"]]
+    layout = json.loads(str(d["layout"]))
+    scale = float(d["scale"])
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for b, idxs in enumerate(layout):
+        bn = sum(numels[i] for i in idxs)
+        reps = [torch.zeros(bn + 8, dtype=torch.bfloat16, device=DEV) for _ in range(W)]
+        keep = []
+        for r in range(W):
+            rows, off = [], 0
+            for i in idxs:
+                g = d.get(f"grad_r{r}_p{i}")
+                t = None if g is None else to_dev(g)
+                keep.append(t)
+                rows.append((0 if t is None else t.data_ptr(), reps[r].data_ptr() + off * 2, numels[i]))
+                off += numels[i]
+            nat.pack(nat.spans_array(rows), nat.MDX_BF16, nat.MDX_BF16, 1.0, False, stream())
+        out = empty_dev(bn, o.F32)
+        grads, rows, off = [], [], 0
+        for i in idxs:
+            g = empty_dev(numels[i], o.BF16)
+            grads.append((i, g))
+            rows.append((off, numels[i], g.data_ptr()))
+            off += numels[i]
+        nat.allreduce_unpack_wide(
+            [x.data_ptr() for x in reps], nat.MDX_BF16, nat.grad_runs_array(rows), out.data_ptr(), nat.MDX_F32,
+            nat.MDX_BF16, nat.f32(1.0 / W), nat.f32(1.0 / scale), flag.data_ptr(), stream(),
+        )
+        got = to_host(out)
+        assert same_bits(got, d[f"reduced_b{b}"]), f"bucket {b}: " + first_mismatch(got, d[f"reduced_b{b}"])
+        for i, g in grads:
+            assert same_bits(to_host(g), d[f"unscaled_p{i}"]), f"param {i}"
+    assert bool(flag.item()) == bool(d["found_inf"])

@@ -225,11 +225,16 @@ def _golden_ddp_inputs(d):
     return W, rank, numels, dt, grads
 
 
-@pytest.mark.parametrize("name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz"])
+@pytest.mark.parametrize(
+    "name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz", "ddp_bf16_f32bucket_w8.npz"]
+)
 def test_ddp_pipeline_matches_golden(name):
     d = load_golden(name)
     W, rank, numels, dt, grads = _golden_ddp_inputs(d)
-    res = o.ddp_pipeline(grads, [dt] * len(numels), numels, float(d["cap_mb"]), rank, 1.0 / float(d["scale"]))
+    bdt = o.BF16 if "bfloat16" in str(d["bucket_dtype"]) else o.F32
+    res = o.ddp_pipeline(
+        grads, [dt] * len(numels), numels, float(d["cap_mb"]), rank, 1.0 / float(d["scale"]), bucket_dtype=bdt
+    )
     assert res["layout"] == json.loads(str(d["layout"]))
     for b, red in enumerate(res["reduced"]):
         assert same_bits(red, d[f"reduced_b{b}"]), f"bucket {b}: " + first_mismatch(red, d[f"reduced_b{b}"])
