@@ -103,3 +103,18 @@ LLAMA_7B = dict(n_layer=32, h=4096, ffn=11008, vocab=32000)         # cfg4, W=8 
 
 def total_numel(specs: list[ParamSpec]) -> int:
     return sum(s.numel for s in specs)
+
+
+class SpecModule(torch.nn.Module):
+    """A module whose parameters have the given specs' shapes and dtypes, registered in order.
+
+    Values are left uninitialised: DDP's bucket layout and FSDP's unit layout
+    depend only on the ordered shapes and dtypes, and the workloads supply the
+    gradients themselves."""
+
+    def __init__(self, specs: list[ParamSpec], device: torch.device | str):
+        super().__init__()
+        self.specs = list(specs)
+        self.ps = torch.nn.ParameterList(
+            [torch.nn.Parameter(torch.empty(s.shape, dtype=s.dtype, device=device)) for s in specs]
+        )
