@@ -1,16 +1,16 @@
-"""Benchmark: minidist's grad-bucket pipeline on one MI355X (BASELINE cfg1).
+"""Benchmark: minidist's gradient-communication path on one MI355X.
 
-One step = the per-rank gradient-communication path over GPT-2-124M's fp32
-gradients with W = 8 data-parallel replicas resident in HBM (rank 0 live,
-peers' packed contributions staged before timing), 25 MB buckets in reverse
-parameter order, loss scale 2^16:
+Default workload (the BASELINE metric, cfg1): the per-rank path over
+GPT-2-124M's fp32 gradients with W = 8 data-parallel replicas resident in HBM
+(rank 0 live, peers' packed contributions staged before timing), 25 MB
+buckets in reverse parameter order, loss scale 2^16.  One step is
 
     DistributedDataParallel.finish_gradient_sync()
         pack + 1/W       -> mdx_pack_planned (all 148 gradients, one dispatch)
         W-way SUM + unpack + unscale + found-inf
                          -> mdx_allreduce_unpack_planned (all 18 buckets, one dispatch:
                             average written to the bucket and into every .grad)
-    DistributedGradScaler.unscale_(opt) -> flag.item()  (the path's one host sync)
+    DistributedGradScaler.unscale_(opt) -> the found-inf flag read (the path's one host sync)
     DistributedGradScaler.update()
 
 value = the metric's algorithmic bytes of the staged pipeline, 52*N (pack 8N,
@@ -20,10 +20,21 @@ back); config.hbm_gbs reports that actual traffic over the same time.  The
 roofline object is for the dominant kernel, the fused W-way reduction:
 (W+2)*N*4 bytes per dispatch (W buckets read, bucket and gradients written)
 over its HIP-event time, measured on its own stream over a second pass of the
-same steps (events would perturb the timed region itself).  The CPU baseline (reference op chain on torch CPU + gloo, W processes)
-runs first, before anything touches the GPU.
+same steps (events would perturb the timed region itself).  The CPU baseline
+(reference op chain on torch CPU + gloo, W processes) runs first, before
+anything touches the GPU.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 10] [--no-cpu-baseline]
+The other BASELINE configurations are parity cases; ``--workload`` measures
+them too (one JSON line each, same fields, no CPU baseline):
+
+    cfg0  tiny GPT fp32, W = 4, one 13 MiB bucket      (staged bytes 36*N)
+    cfg2  GPT-2-medium fp32, W = 4, 25 MB buckets       (staged bytes 36*N)
+    cfg3  FSDP units of GPT-2-XL (48 blocks), W = 8: bf16 gather cast + fp32
+          reduce-scatter share per unit                  (26*S per unit)
+    cfg4  Llama-7B bf16 grads, W = 8, fp32 buckets (reduce_dtype widening)
+                                                         (26*N)
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 10] [--no-cpu-baseline] [--workload cfg1]
 """
 
 from __future__ import annotations
@@ -41,14 +52,14 @@ sys.path.insert(0, str(ROOT / "distributed-training-framework_amd"))
 
 METRIC = "grad-bucket pipeline HBM GB/s (% of 8 TB/s) GPT-2-124M W=8; ms/step"
 HBM_PEAK_GBS = 8000.0
-W = 8
+W_CFG1 = 8
 CAP_MB = 25.0
 LOSS_SCALE = 2.0**16
 
 
 def cpu_baseline(steps: int, threads: int) -> dict | None:
     """Time the reference's CPU path (oracle/gloo_path.py) in a child process."""
-    cmd = [sys.executable, "-m", "oracle.gloo_path", "--world", str(W), "--steps", str(steps),
+    cmd = [sys.executable, "-m", "oracle.gloo_path", "--world", str(W_CFG1), "--steps", str(steps),
            "--warmup", "1", "--threads", str(threads)]
     res = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
     if res.returncode != 0:
@@ -84,66 +95,61 @@ def calibrate_copy() -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument(
-        "--calibrate-copy", action="store_true",
-        help="only run a plain 1 GiB fp32 copy (mdx_pack, scale 1) 10 times: the known-size "
-             "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings",
-    )
-    args = ap.parse_args()
-    if args.calibrate_copy:
-        return calibrate_copy()
-    if args.gpus != 1:
-        print(
-            f"bench.py measures one GPU: this build emulates the W={W} data-parallel replicas on a single "
-            f"MI355X (no inter-GPU collectives), so --gpus {args.gpus} is not supported",
-            file=sys.stderr,
-        )
-        return 2
+# ---------------------------------------------------------------------------
+# DDP workloads (cfg0, cfg1, cfg2, cfg4)
+# ---------------------------------------------------------------------------
 
-    # ---- CPU baseline first: nothing has touched the GPU yet ------------------
-    cpu = None
-    if not args.no_cpu_baseline:
-        cores = max(W, min(16, host_cores()))
-        threads = max(1, cores // W)
-        t0 = time.perf_counter()
-        cpu = cpu_baseline(args.cpu_steps, threads)
-        print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
+DDP_WORKLOADS = {
+    "cfg1": dict(model="GPT2_SMALL", W=8, grad_scale=1e-3, dtype="f32", reduce_dtype=None,
+                 desc="cfg1: GPT-2-124M fp32 grads (148 tensors, N=124,439,808), W=8 replicas on one GPU, "
+                      "25 MB buckets in reverse parameter order (18 buckets), loss scale 2^16"),
+    "cfg0": dict(model="TINY_GPT", W=4, grad_scale=1e-2, dtype="f32", reduce_dtype=None,
+                 desc="cfg0: tiny GPT (4L, h256, V1024, ctx128) fp32 grads (52 tensors, N=3,454,464), W=4, "
+                      "25 MB cap (one bucket), loss scale 2^16"),
+    "cfg2": dict(model="GPT2_MEDIUM", W=4, grad_scale=1e-3, dtype="f32", reduce_dtype=None,
+                 desc="cfg2: GPT-2-medium fp32 grads (292 tensors, N=354,823,168), W=4, 25 MB buckets "
+                      "(74 buckets), loss scale 2^16"),
+    "cfg4": dict(model="LLAMA_7B", W=8, grad_scale=1e-3, dtype="bf16", reduce_dtype="f32",
+                 desc="cfg4: Llama-7B bf16 grads (291 tensors, N=6,738,415,616), W=8 bf16 contributions "
+                      "(~108 GB) summed in fp32 into fp32 25 MB buckets (291), unpacked to bf16, loss scale 2^12"),
+}
 
+
+def bench_ddp(name: str, args) -> dict:
     import torch
-    from torch import nn
 
     from minidist import DDP, DistributedGradScaler, ResidentGroup
     from minidist import workloads as wl
 
+    cfg = DDP_WORKLOADS[name]
+    W = cfg["W"]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    specs = wl.gpt_specs(**wl.GPT2_SMALL)
+    if cfg["model"] == "LLAMA_7B":
+        specs = wl.llama_specs(**wl.LLAMA_7B)
+        loss_scale = 2.0**12
+    else:
+        specs = wl.gpt_specs(**getattr(wl, cfg["model"]))
+        loss_scale = LOSS_SCALE
     N = wl.total_numel(specs)
+    reduce_dtype = torch.float32 if cfg["reduce_dtype"] == "f32" else None
 
-    class Params(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.ps = nn.ParameterList([nn.Parameter(torch.zeros(s.shape, device=dev)) for s in specs])
-
-    model = Params()
-    scaler = DistributedGradScaler(init_scale=LOSS_SCALE)
+    model = wl.SpecModule(specs, dev)
+    scaler = DistributedGradScaler(init_scale=loss_scale)
     group = ResidentGroup(W, 0, dev)
-    ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+    ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler, reduce_dtype=reduce_dtype)
     ddp.allocate_buckets()
     gen = torch.Generator(device=dev).manual_seed(1234)
+    scale = cfg["grad_scale"] * loss_scale
     for p in model.parameters():
-        p.grad = torch.randn(p.shape, device=dev, generator=gen) * (1e-3 * LOSS_SCALE)
+        p.grad = (torch.randn(p.shape, device=dev, generator=gen) * scale).to(p.dtype)
     for b in range(len(ddp._buckets)):
         rows = ddp.bucket_replicas(b)
+        wire_dtype, prescaled = ddp.bucket_wire_format(b)
         for r in range(1, W):
-            rows[r].copy_(torch.randn(rows[r].shape, device=dev, generator=gen) * (1e-3 * LOSS_SCALE / W))
+            x = torch.randn(rows[r].shape, device=dev, generator=gen) * (scale / W if prescaled else scale)
+            rows[r].copy_(x.to(wire_dtype))
+            del x
 
     class _Opt:  # the scaler only reads param_groups
         param_groups = [{"params": list(model.parameters())}]
@@ -152,7 +158,7 @@ def main() -> int:
 
     # Dominant kernel timing: HIP events around the fused W-way reduction
     # dispatch, recorded on the stream it is launched on.
-    red_events: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+    red_events: list = []
     timing = {"on": False}
     orig = ResidentGroup.all_reduce_unpack_planned
 
@@ -175,6 +181,7 @@ def main() -> int:
         scaler.update()
         return found
 
+    steps = args.steps if name != "cfg4" else min(args.steps, 20)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -182,52 +189,66 @@ def main() -> int:
     # reduction costs a visible share of a ~1 ms step).
     t0 = time.perf_counter()
     found_any = False
-    for _ in range(args.steps):
+    for _ in range(steps):
         found_any |= step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     # Kernel pass: the same steps again, HIP events around the dominant dispatch.
     timing["on"] = True
-    for _ in range(min(args.steps, 50)):
+    for _ in range(min(steps, 50)):
         step()
     torch.cuda.synchronize()
     timing["on"] = False
     ResidentGroup.all_reduce_unpack_planned = orig
 
-    ms_per_step = elapsed / args.steps * 1e3
-    alg_bytes = 52 * N  # pack 8N + W-way (W+1)*4N + unpack 8N, fp32, W = 8
+    b0 = ddp._buckets[0]
+    s_w = b0.wire.element_size()
+    s_b = b0.buffer.element_size()
+    s_g = b0.params[0].element_size()
+    ms_per_step = elapsed / steps * 1e3
+    if b0.widening:
+        # pack: own bf16 grads -> own bf16 row (4N); fused: W bf16 rows read, fp32 bucket + bf16 grads written
+        alg_bytes = N * (W * s_w + s_b + s_b + s_g)  # the configuration's accounting (26*N)
+        hbm_bytes = N * (2 * s_g + W * s_w + s_b + s_g)
+        alg_note = "W*N*2 + N*4 + N*4 + N*2 = 26*N (bf16 contributions, fp32 bucket, bf16 grads)"
+    else:
+        alg_bytes = N * (2 * s_g + (W + 3) * s_b)  # pack + W-way + unpack, staged
+        hbm_bytes = N * (s_g + s_b) + N * (W * s_b + s_b + s_g)
+        alg_note = f"staged pack + W-way + unpack: N*(2*s_g + (W+3)*s_b) = {2 * s_g + (W + 3) * s_b}*N"
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
     red_avg_ms = sum(red_ms) / len(red_ms)
-    red_bytes = (W + 2) * N * 4
-    hbm_bytes = 48 * N
+    red_bytes = N * (W * s_w + s_b + s_g)
     red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
+    kname = ("allreduce_wide_kernel_dev<bf16, float, bf16, 8>" if b0.widening
+             else f"allreduce_unpack_kernel_dev<float, float, {W}>")
 
     traffic = None
     tfile = ROOT / "profiles" / "allreduce_unpack_gpt2_124m_w8_traffic.json"
-    if tfile.exists():
+    if name == "cfg1" and tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
 
-    out = {
-        "metric": METRIC,
+    return {
+        "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded randn grads x 2^16 loss scale; peers' contributions staged in HBM)",
+        "dtype": cfg["dtype"],
+        "data": f"synthetic (seeded randn grads x {cfg['grad_scale']:g} x loss scale; peers' contributions staged "
+                "in HBM)",
         "config": {
-            "workload": "cfg1: GPT-2-124M fp32 grads (148 tensors, N=124,439,808), W=8 replicas on one GPU, "
-                        "25 MB buckets in reverse parameter order (18 buckets), loss scale 2^16",
+            "workload": cfg["desc"],
             "world": W,
             "numel": N,
             "buckets": len(ddp._buckets),
             "alg_bytes_per_step": alg_bytes,
+            "alg_bytes_formula": alg_note,
             "hbm_bytes_per_step": hbm_bytes,
             "hbm_gbs": round(hbm_bytes / (ms_per_step * 1e-3) / 1e9, 2),
             "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
@@ -235,7 +256,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "allreduce_unpack_kernel_dev<float, float, 8> (mdx_allreduce_unpack_planned, all 18 buckets in one dispatch)",
+            "kernel": f"{kname} (mdx_allreduce_unpack_planned, all {len(ddp._buckets)} buckets in one dispatch)",
             "achieved": round(red_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -246,7 +267,180 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+
+
+# ---------------------------------------------------------------------------
+# FSDP workload (cfg3)
+# ---------------------------------------------------------------------------
+
+
+def bench_fsdp(args) -> dict:
+    """48 FSDP units of GPT-2-XL blocks, W = 8: per unit the fp32 -> bf16 gather
+    cast into this rank's slot and the reduce-scatter share of 8 bf16 full-size
+    contributions into the fp32 shard gradient.
+
+    The two kernels of a unit take ~20 us together, far less than the Python
+    around them, so the step's dispatches are enqueued behind a spin kernel and
+    the step is timed on the GPU (first to last dispatch, HIP events): the
+    number is the dispatch sequence's own throughput, as when FSDP's launches
+    overlap forward/backward compute."""
+    import torch
+    from torch import nn
+
+    from minidist import FSDP, MixedPrecisionPolicy, ResidentGroup
+    from minidist import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    W, n_units = 8, wl.GPT2_XL["n_layer"]
+    specs = wl.gpt_block_specs(0, wl.GPT2_XL["n_embd"])
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ps = nn.ParameterList([nn.Parameter(torch.empty(s.shape, device=dev)) for s in specs])
+
+    class Model(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = nn.ModuleList([Block() for _ in range(n_units)])
+
+    gen = torch.Generator(device=dev).manual_seed(33)
+    model = Model()
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, device=dev, generator=gen) * 0.02)
+    policy = MixedPrecisionPolicy(param_dtype=torch.bfloat16, reduce_dtype=torch.float32)
+    fsdp = FSDP(model, unit_types=(Block,), process_group=ResidentGroup(W, 0, dev), mixed_precision=policy)
+    units = fsdp._units
+    assert len(units) == n_units
+    own_grads = []
+    for u in units:
+        u.unshard()  # keep the gather buffers allocated: the step re-casts into them
+        peers = u.peer_grad_contributions()
+        for r in range(1, W):
+            peers[r].copy_((torch.randn(u.padded_numel, device=dev, generator=gen) * 1e-3).to(torch.bfloat16))
+        own_grads.append([(torch.randn(p.shape, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+                          for p in u.params])
+    S = units[0].shard_numel
+
+    def step(events=None):
+        for i, u in enumerate(units):
+            if events is not None:
+                events[i][0].record()
+            u._cast_into_own_slot()
+            if events is not None:
+                events[i][1].record()
+            u.flat_shard.grad = None  # the shard gradient is set, not accumulated
+            for p, g in zip(u.params, own_grads[i], strict=True):
+                p.grad = g
+            u.reduce_scatter_grads()
+            if events is not None:
+                events[i][2].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # Spin-kernel length that holds the stream ~30 ms (calibrated: its clock rate is the device's).
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    torch.cuda._sleep(1_000_000)
+    c1.record()
+    torch.cuda.synchronize()
+    hold_cycles = int(1_000_000 * 30.0 / max(c0.elapsed_time(c1), 1e-3))
+    steps = min(args.steps, 20)
+    per_step, cast_ms, share_ms = [], [], []
+    for _ in range(steps):
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in units]
+        torch.cuda._sleep(hold_cycles)  # hold the stream while the host enqueues the whole step
+        step(ev)
+        torch.cuda.synchronize()
+        per_step.append(ev[0][0].elapsed_time(ev[-1][2]))
+        cast_ms += [e[0].elapsed_time(e[1]) for e in ev]
+        share_ms += [e[1].elapsed_time(e[2]) for e in ev]
+    ms_per_step = sorted(per_step)[len(per_step) // 2]
+    alg_bytes = n_units * 26 * S  # cast 6S (fp32 read, bf16 write) + share 20S (8 bf16 reads, fp32 write)
+    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    share_avg = sum(share_ms) / len(share_ms)
+    cast_avg = sum(cast_ms) / len(cast_ms)
+    share_gbs = 20 * S / (share_avg * 1e-3) / 1e9
+    return {
+        "metric": "FSDP unit gather-cast + reduce-scatter share HBM GB/s (% of 8 TB/s) cfg3; ms/step",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16->f32",
+        "data": "synthetic (master randn x 0.02, bf16 grads randn x 1e-3; peers' contributions staged in HBM)",
+        "config": {
+            "workload": "cfg3: 48 FSDP units of GPT-2-XL blocks (12 tensors, 30,740,800 elements each, shard "
+                        "S=3,842,600), W=8, param bf16 / reduce fp32; per unit mdx_cast_f32_bf16 + "
+                        "mdx_reduce_scatter_share; GPU time of the step's dispatches",
+            "world": W,
+            "units": n_units,
+            "shard_numel": S,
+            "alg_bytes_per_step": alg_bytes,
+            "alg_bytes_formula": "per unit 6*S (cast) + 20*S (share: W*S*2 read, S*4 written)",
+            "cast_avg_ms": round(cast_avg, 5),
+            "cast_gbs": round(6 * S / (cast_avg * 1e-3) / 1e9, 1),
+            "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "share_kernel<bf16, float, float, 8> (mdx_reduce_scatter_share)",
+            "achieved": round(share_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(share_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": 20 * S,
+            "avg_launch_ms": round(share_avg, 5),
+        },
+        "cpu_baseline": None,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="cfg1", choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument(
+        "--calibrate-copy", action="store_true",
+        help="only run a plain 1 GiB fp32 copy (mdx_pack, scale 1) 10 times: the known-size "
+             "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings",
+    )
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: this build emulates the W={W_CFG1} data-parallel replicas on a single "
+            f"MI355X (no inter-GPU collectives), so --gpus {args.gpus} is not supported",
+            file=sys.stderr,
+        )
+        return 2
+
+    # ---- CPU baseline first (headline workload only): nothing has touched the GPU yet
+    cpu = None
+    if args.workload == "cfg1" and not args.no_cpu_baseline:
+        cores = max(W_CFG1, min(16, host_cores()))
+        threads = max(1, cores // W_CFG1)
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(args.cpu_steps, threads)
+        print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
+
+    out = bench_fsdp(args) if args.workload == "cfg3" else bench_ddp(args.workload, args)
     if cpu is not None:
+        alg_bytes = out["config"]["alg_bytes_per_step"]
         cpu_gbs = alg_bytes / (cpu["median_ms"] * 1e-3) / 1e9
         out["cpu_baseline"] = {
             "value": round(cpu_gbs, 3),
@@ -254,10 +448,10 @@ def main() -> int:
             "cores": cpu["cores"],
             "kind": "port",
             "sample": f"{cpu['steps']} timed steps (+1 warmup) of the full cfg1 pipeline, reference op chain on "
-                      f"torch CPU + gloo, {W} processes x {cpu['threads_per_rank']} threads; "
+                      f"torch CPU + gloo, {W_CFG1} processes x {cpu['threads_per_rank']} threads; "
                       f"median {cpu['median_ms']:.1f} ms/step",
             "ms_per_step": round(cpu["median_ms"], 2),
-            "speedup": round(cpu["median_ms"] / ms_per_step, 1),
+            "speedup": round(cpu["median_ms"] / out["ms_per_step"], 1),
         }
     print(json.dumps(out), flush=True)
     return 0
