@@ -1,6 +1,6 @@
 """Benchmark: minidist's gradient-communication path on one MI355X.
 
-Default workload (the BASELINE metric, cfg1): the per-rank path over
+Default workload (the headline metric, cfg1): the per-rank path over
 GPT-2-124M's fp32 gradients with W = 8 data-parallel replicas resident in HBM
 (rank 0 live, peers' packed contributions staged before timing), 25 MB
 buckets in reverse parameter order, loss scale 2^16.  One step is
@@ -24,7 +24,7 @@ same steps (events would perturb the timed region itself).  The CPU baseline
 (reference op chain on torch CPU + gloo, W processes) runs first, before
 anything touches the GPU.
 
-The other BASELINE configurations are parity cases; ``--workload`` measures
+The other benchmark configurations are parity cases; ``--workload`` measures
 them too (one JSON line each, same fields, no CPU baseline):
 
     cfg0  tiny GPT fp32, W = 4, one 13 MiB bucket      (staged bytes 36*N)
@@ -349,13 +349,24 @@ def bench_fsdp(args) -> dict:
     torch.cuda.synchronize()
     hold_cycles = int(1_000_000 * 30.0 / max(c0.elapsed_time(c1), 1e-3))
     steps = min(args.steps, 20)
-    per_step, cast_ms, share_ms = [], [], []
+    # Step pass: one event before the first dispatch and one after the last
+    # (an event between two dispatches costs a few microseconds of its own).
+    per_step = []
     for _ in range(steps):
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in units]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(hold_cycles)  # hold the stream while the host enqueues the whole step
+        e0.record()
+        step()
+        e1.record()
+        torch.cuda.synchronize()
+        per_step.append(e0.elapsed_time(e1))
+    # Kernel pass: the same steps with events around every dispatch.
+    cast_ms, share_ms = [], []
+    for _ in range(min(steps, 5)):
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in units]
+        torch.cuda._sleep(hold_cycles)
         step(ev)
         torch.cuda.synchronize()
-        per_step.append(ev[0][0].elapsed_time(ev[-1][2]))
         cast_ms += [e[0].elapsed_time(e[1]) for e in ev]
         share_ms += [e[1].elapsed_time(e[2]) for e in ev]
     ms_per_step = sorted(per_step)[len(per_step) // 2]
@@ -412,7 +423,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="cfg1", choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument(
         "--calibrate-copy", action="store_true",
         help="only run a plain 1 GiB fp32 copy (mdx_pack, scale 1) 10 times: the known-size "

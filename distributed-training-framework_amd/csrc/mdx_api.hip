@@ -67,8 +67,8 @@ struct Rec {
 template <typename Emit>
 int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool in_place, Emit&& emit) {
   const int E = copy_frag_elems(sdt, ddt);
-  const int64_t VPB = int64_t(kBlock) * (kCopyElemsPerThread / E);
-  const int64_t EPB = int64_t(kBlock) * kCopyElemsPerThread;
+  const int64_t VPB = int64_t(kBlock) * kCopyFragsPerThread;
+  const int64_t EPB = VPB * E;
   const int ss = dtype_size(sdt), ds = dtype_size(ddt);
   for (int i = 0; i < n_spans; ++i) {
     const mdx_span& sp = spans[i];
@@ -202,7 +202,9 @@ int run_pieces(const mdx_piece* pieces, void* const* grads, int n_pieces, const 
 
 inline int64_t align8(int64_t x) { return (x + 7) & ~int64_t(7); }
 
-void plan_layout(PlanHeader* h, int count) {
+inline int64_t hint_groups(int64_t blocks) { return (blocks + kHintBlocks - 1) >> kHintShift; }
+
+void plan_layout(PlanHeader* h, int count, int64_t blocks) {
   int64_t off = align8(sizeof(PlanHeader));
   h->off_first_block = off;
   off = align8(off + int64_t(count + 1) * 4);
@@ -216,6 +218,8 @@ void plan_layout(PlanHeader* h, int count) {
   off += int64_t(count) * 8;
   h->off_pos = off;
   off += int64_t(count) * 8;
+  h->off_hint = off;
+  off = align8(off + (hint_groups(blocks) + 1) * 4);
   h->bytes = off;
 }
 
@@ -236,7 +240,7 @@ int build_plan(PlanHeader proto, Gen&& gen, void* plan, int64_t* plan_bytes) {
   h.magic = kPlanMagic;
   h.count = count;
   h.blocks = int32_t(blocks);
-  plan_layout(&h, count);
+  plan_layout(&h, count, blocks);
   const int64_t cap = *plan_bytes;
   *plan_bytes = h.bytes;
   if (plan == nullptr || cap < h.bytes || (addr(plan) & 7u) != 0) return MDX_ESIZE;
@@ -260,7 +264,19 @@ int build_plan(PlanHeader proto, Gen&& gen, void* plan, int64_t* plan_bytes) {
     ++k;
     return MDX_OK;
   });
-  return rc;
+  if (rc != MDX_OK) return rc;
+  // Run hints (find_run_hinted): every run has at least one workgroup, so
+  // first_block is strictly increasing and one forward sweep finds them.
+  int32_t* hint = reinterpret_cast<int32_t*>(base + h.off_hint);
+  const int64_t groups = hint_groups(blocks);
+  int run = 0;
+  for (int64_t g = 0; g < groups; ++g) {
+    const int64_t b0 = g << kHintShift;
+    while (run + 1 < count && fb[run + 1] <= b0) ++run;
+    hint[g] = run;
+  }
+  hint[groups] = count - 1;
+  return MDX_OK;
 }
 
 // Validates the host copy of a plan and derives the device table view.
@@ -275,6 +291,7 @@ int plan_view(const void* plan, const void* d_plan, int32_t kind, const PlanHead
   t->a = reinterpret_cast<const uint64_t*>(d + h->off_a);
   t->b = reinterpret_cast<const uint64_t*>(d + h->off_b);
   t->pos = reinterpret_cast<const int64_t*>(d + h->off_pos);
+  t->hint = reinterpret_cast<const int32_t*>(d + h->off_hint);
   t->count = h->count;
   *hdr = h;
   return MDX_OK;

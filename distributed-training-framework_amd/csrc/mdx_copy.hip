@@ -38,13 +38,14 @@ struct CopyOp {
 template <typename S, typename D, int SCALE, bool CHECK, typename View>
 __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) {
   constexpr int E = frag_elems(int(sizeof(S)), int(sizeof(D)));
-  constexpr int U = kCopyElemsPerThread / E;
+  constexpr int U = kCopyFragsPerThread;
   constexpr int VPB = kBlock * U;
-  constexpr int EPB = kBlock * kCopyElemsPerThread;
+  constexpr int EPT = U * E;
+  constexpr int EPB = kBlock * EPT;
 
   const int blk = int(blockIdx.x);
   const int32_t* fb = tab.first_block();
-  const int s = find_run(fb, tab.count(), blk);
+  const int s = tab.run_of(blk);
   const int c = blk - fb[s];
   const int nblk = fb[s + 1] - fb[s];
   const S* src = static_cast<const S*>(tab.src(s));
@@ -96,14 +97,14 @@ __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) 
       dst[i] = op(x, bad);
     }
   } else {
-    S in[kCopyElemsPerThread];
+    S in[EPT];
 #pragma unroll
-    for (int k = 0; k < kCopyElemsPerThread; ++k) {
+    for (int k = 0; k < EPT; ++k) {
       const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
       in[k] = (i < n && !zero_src) ? src[i] : zero_of<S>();
     }
 #pragma unroll
-    for (int k = 0; k < kCopyElemsPerThread; ++k) {
+    for (int k = 0; k < EPT; ++k) {
       const int64_t i = int64_t(c) * EPB + int64_t(k) * kBlock + t;
       if (i < n) dst[i] = op(in[k], bad);
     }

@@ -17,7 +17,7 @@
 
 namespace mdx {
 
-constexpr int kBlock = 256;               // 4 wave64 per workgroup
+constexpr int kBlock = 64;  // one wave64 per workgroup (measured: beats 128, 256, 512 and 1024 lanes)
 constexpr int kRunsPerLaunch = 48;        // runs per dispatch (kernarg budget)
 constexpr int64_t kMaxRunElems = int64_t(1) << 26;
 
@@ -116,9 +116,9 @@ __device__ __forceinline__ void vstore(T* p, const T (&src)[E]) {
   }
 }
 
-// Workgroup -> run lookup: largest s with first_block[s] <= blk.
-__device__ __forceinline__ int find_run(const int32_t* first_block, int count, int blk) {
-  int lo = 0, hi = count;
+// Workgroup -> run lookup: largest s in [lo, hi) with first_block[s] <= blk
+// (first_block[lo] <= blk must hold).
+__device__ __forceinline__ int find_run_in(const int32_t* first_block, int lo, int hi, int blk) {
   while (hi - lo > 1) {
     int mid = (lo + hi) >> 1;
     if (first_block[mid] <= blk) {
@@ -128,6 +128,23 @@ __device__ __forceinline__ int find_run(const int32_t* first_block, int count, i
     }
   }
   return lo;
+}
+
+__device__ __forceinline__ int find_run(const int32_t* first_block, int count, int blk) {
+  return find_run_in(first_block, 0, count, blk);
+}
+
+// Device plans also hold one hint per kHintBlocks workgroups: hint[g] is the
+// run that contains workgroup g * kHintBlocks, and hint[groups] = count - 1.
+// The run of workgroup blk then lies in [hint[g], hint[g + 1]], g = blk /
+// kHintBlocks, usually a range of one or two runs: a workgroup resolves its
+// run with two or three dependent scalar loads instead of log2(count) of them.
+constexpr int kHintShift = 6;
+constexpr int kHintBlocks = 1 << kHintShift;
+
+__device__ __forceinline__ int find_run_hinted(const int32_t* first_block, const int32_t* hint, int blk) {
+  const int g = blk >> kHintShift;
+  return find_run_in(first_block, hint[g], hint[g + 1] + 1, blk);
 }
 
 // One wave stores 1 into *flag if any of its lanes saw a non-finite value.
@@ -159,10 +176,12 @@ struct CopyParams {
   int32_t* found_inf;
 };
 
-// Elements per 16-byte-aligned fragment and per thread for a dtype pair.
+// Elements per 16-byte-aligned fragment for a dtype pair, and fragments per
+// lane of the copy kernel (one fragment = one 16-byte vector of the narrower
+// dtype; the scalar path of a misaligned span handles as many elements).
 constexpr int min_size(int a, int b) { return a < b ? a : b; }
 constexpr int frag_elems(int src_size, int dst_size) { return 16 / min_size(src_size, dst_size); }
-constexpr int kCopyElemsPerThread = 32;
+constexpr int kCopyFragsPerThread = 1;  // measured on MI355X: 1 beats 2 and 4
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
                        hipStream_t stream);
@@ -200,14 +219,20 @@ struct ReduceParams {
   int32_t* found_inf;
 };
 
-// Fragments per lane and contribution kept in flight: about 128 VGPRs of
-// loads for the all-reduce (32 16-byte loads per lane at W = 8), half that
-// for the share kernel, whose width is only bounded at compile time.
+// Fragments per lane and contribution (U) of the W-way reductions: each lane
+// keeps U fragments of all W contributions in flight, about 8 16-byte loads
+// (one fragment per contribution at W = 8).  Measured on MI355X with one-wave
+// workgroups: 16 or 32 loads per lane cost 2-6% of the W = 8 all-reduce's
+// bandwidth, and a workgroup that streams several chunks in a double-buffered
+// loop loses to one short-lived workgroup per chunk.
+constexpr int kReduceVecsPerLane = 8;
 constexpr int clamp_unroll(int u) { return u < 1 ? 1 : (u > 8 ? 8 : u); }
 constexpr int allreduce_unroll(int world, int frag_bytes) {
-  return clamp_unroll(128 / (world * (frag_bytes / 4)));
+  return clamp_unroll(kReduceVecsPerLane / (world * (frag_bytes / 16)));
 }
-constexpr int share_unroll(int wmax, int frag_bytes) { return clamp_unroll(64 / (wmax * (frag_bytes / 4))); }
+constexpr int share_unroll(int wmax, int frag_bytes) {
+  return clamp_unroll(kReduceVecsPerLane / (wmax * (frag_bytes / 16)));
+}
 
 // Host-side dispatch into the instantiating translation units.
 hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, const PieceBatch& b,
@@ -228,6 +253,7 @@ hipError_t launch_allreduce_wide(int grad_dtype, int world, const PieceBatch& b,
 
 struct DevTable {
   const int32_t* first_block;  // count + 1 entries
+  const int32_t* hint;         // blocks / kHintBlocks + 2 entries (see find_run_hinted)
   const int32_t* head;
   const int64_t* numel;
   const uint64_t* a;  // span: src    piece: own
@@ -238,6 +264,7 @@ struct DevTable {
 
 struct SpanArgView {
   const SpanBatch& t;
+  __device__ __forceinline__ int run_of(int blk) const { return find_run(t.first_block, t.count, blk); }
   __device__ __forceinline__ int count() const { return t.count; }
   __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
   __device__ __forceinline__ const void* src(int i) const { return t.src[i]; }
@@ -248,6 +275,7 @@ struct SpanArgView {
 
 struct PieceArgView {
   const PieceBatch& t;
+  __device__ __forceinline__ int run_of(int blk) const { return find_run(t.first_block, t.count, blk); }
   __device__ __forceinline__ int count() const { return t.count; }
   __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
   __device__ __forceinline__ const void* own(int i) const { return t.own[i]; }
@@ -259,6 +287,7 @@ struct PieceArgView {
 
 struct DevView {
   DevTable t;
+  __device__ __forceinline__ int run_of(int blk) const { return find_run_hinted(t.first_block, t.hint, blk); }
   __device__ __forceinline__ int count() const { return t.count; }
   __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
   __device__ __forceinline__ const void* src(int i) const { return reinterpret_cast<const void*>(t.a[i]); }
@@ -291,6 +320,7 @@ struct PlanHeader {
   uint64_t out;
   int64_t off_first_block, off_head, off_numel, off_a, off_b, off_pos;
   int64_t bytes;
+  int64_t off_hint;
 };
 
 hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int blocks, const CopyParams& p,

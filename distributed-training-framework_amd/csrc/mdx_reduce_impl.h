@@ -27,7 +27,7 @@
 //
 // Every contribution is read once per step, so every load is non-temporal;
 // each lane keeps U fragments of all W contributions in flight before the
-// first add (U * W = 32 16-byte loads for the all-reduce).
+// first add (U * W = 8 16-byte loads for the all-reduce at W = 8).
 #pragma once
 
 #include "mdx_internal.h"
@@ -49,7 +49,7 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
 
   const int blk = int(blockIdx.x);
   const int32_t* fb = tab.first_block();
-  const int s = find_run(fb, tab.count(), blk);
+  const int s = tab.run_of(blk);
   const int c = blk - fb[s];
   const int nblk = fb[s + 1] - fb[s];
   const int64_t pos = tab.pos(s);
@@ -109,17 +109,17 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
         const int64_t i = h + v * E;
         T y[E];
 #pragma unroll
-        for (int k = 0; k < E; ++k) {
-          T acc = widen(x[u][0][k]);
+        for (int e = 0; e < E; ++e) {
+          T acc = widen(x[u][0][e]);
 #pragma unroll
-          for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(x[u][r][k])));
-          y[k] = acc;
+          for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(x[u][r][e])));
+          y[e] = acc;
         }
         if (out) vstore<T, E, true>(out + i, y);
         if constexpr (UNPACK) {
           G gy[E];
 #pragma unroll
-          for (int k = 0; k < E; ++k) gy[k] = finish(y[k]);
+          for (int e = 0; e < E; ++e) gy[e] = finish(y[e]);
           vstore<G, E, true>(grad + i, gy);
         }
       }

@@ -7,7 +7,7 @@ by that list.  GPT shapes follow the reference model's registration order
 minidist/tensor_parallel.py:246-420): ``nn.Module.parameters()`` yields a
 module's own parameters before its children's, so the embedding's ``wpe``
 comes before ``wte.weight``.  The Llama table is the standard decoder layout
-the BASELINE configuration names (the reference has no Llama model).
+the Llama-7B benchmark configuration names (the reference has no Llama model).
 """
 
 from __future__ import annotations
@@ -93,7 +93,7 @@ def llama_specs(
     return specs
 
 
-# The BASELINE configurations (cfg0..cfg4).
+# The benchmark configurations (cfg0..cfg4) the bench and the full-size tests use.
 TINY_GPT = dict(n_layer=4, n_embd=256, vocab=1024, ctx=128)        # cfg0, W=4
 GPT2_SMALL = dict(n_layer=12, n_embd=768, vocab=50257, ctx=1024)    # cfg1, W=8
 GPT2_MEDIUM = dict(n_layer=24, n_embd=1024, vocab=50257, ctx=1024)  # cfg2, W=4

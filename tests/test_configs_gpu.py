@@ -1,4 +1,4 @@
-"""The BASELINE configurations at their real shapes, through the Python API, on the GPU.
+"""The benchmark configurations at their real shapes, through the Python API, on the GPU.
 
 cfg0 (tiny GPT, W=4) is small enough for the oracle on every element.  The
 large configurations use three checks that do not depend on size:

@@ -304,7 +304,7 @@ def test_fused_unscale_in_ddp_unpack(rng, inject):
 
 
 # ---------------------------------------------------------------------------
-# reduce_dtype: bf16 gradients accumulated in fp32 buckets (BASELINE cfg4 at small scale)
+# reduce_dtype: bf16 gradients accumulated in fp32 buckets (the Llama-7B configuration, cfg4, at small scale)
 # ---------------------------------------------------------------------------
 
 

@@ -248,7 +248,36 @@ def test_span_table_layout_is_the_c_struct():
 
 def _plan_header(buf: np.ndarray) -> dict:
     h = buf.view(np.int32)
-    return {"magic": int(h[0]) & 0xFFFFFFFF, "kind": int(h[1]), "count": int(h[2]), "blocks": int(h[3])}
+    q = buf.view(np.int64)
+    # PlanHeader (csrc/mdx_internal.h): 10 int32 fields, replicas[16] and out (uint64), then the
+    # int64 offsets first_block, head, numel, a, b, pos, the total size and the hint offset.
+    return {"magic": int(h[0]) & 0xFFFFFFFF, "kind": int(h[1]), "count": int(h[2]), "blocks": int(h[3]),
+            "off_first_block": int(q[22]), "bytes": int(q[28]), "off_hint": int(q[29])}
+
+
+HINT_SHIFT = 6  # kHintShift: one run hint per 64 workgroups
+
+
+def _plan_runs(buf: np.ndarray) -> tuple[np.ndarray, np.ndarray, dict]:
+    h = _plan_header(buf)
+    raw = buf.view(np.uint8)
+    fb = raw[h["off_first_block"] : h["off_first_block"] + 4 * (h["count"] + 1)].view(np.int32)
+    groups = (h["blocks"] + (1 << HINT_SHIFT) - 1) >> HINT_SHIFT
+    hint = raw[h["off_hint"] : h["off_hint"] + 4 * (groups + 1)].view(np.int32)
+    return fb, hint, h
+
+
+def _hinted_run(fb: np.ndarray, hint: np.ndarray, blk: int) -> int:
+    """The kernels' find_run_hinted, step for step: binary search in [hint[g], hint[g+1]]."""
+    g = blk >> HINT_SHIFT
+    lo, hi = int(hint[g]), int(hint[g + 1]) + 1
+    while hi - lo > 1:
+        mid = (lo + hi) >> 1
+        if fb[mid] <= blk:
+            lo = mid
+        else:
+            hi = mid
+    return lo
 
 
 def test_plan_spans_sizing_and_layout():
@@ -267,7 +296,36 @@ def test_plan_spans_sizing_and_layout():
     assert L.mdx_plan_spans(spans.ctypes.data, 150, 0, 0, buf.ctypes.data, ctypes.byref(cap)) == 0
     h = _plan_header(buf)
     assert h["magic"] == 0x5058444D and h["kind"] == 1 and h["count"] == 150
-    assert h["blocks"] == 150  # 4096 fp32 = one workgroup (256 lanes x 16 elements) per span
+    # one 16-byte fragment (4 fp32) per lane: 4096 fp32 = 16 one-wave workgroups per span
+    assert h["blocks"] == 150 * 16
+    assert h["bytes"] == need and h["off_hint"] + 4 * ((2400 >> HINT_SHIFT) + 2) <= need
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_plan_run_hints_resolve_every_workgroup(seed):
+    """Every workgroup's hinted lookup lands on the run brute force assigns it.
+
+    Run sizes mix one-workgroup runs (many runs per hint group) with runs of
+    hundreds of workgroups (many groups per run)."""
+    L = nat.lib()
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 400))
+    sizes = np.where(rng.random(n) < 0.6, rng.integers(1, 1024, n), rng.integers(1, 1 << 20, n))
+    rows, addr = [], 0x10000000
+    for k in sizes:
+        rows.append((addr, addr + (1 << 34), int(k)))
+        addr += (int(k) * 4 + 255) // 256 * 256
+    spans = nat.spans_array(rows)
+    size = ctypes.c_int64(0)
+    assert L.mdx_plan_spans(spans.ctypes.data, n, 0, 0, None, ctypes.byref(size)) == nat.MDX_ESIZE
+    buf = np.zeros((size.value + 7) // 8, dtype=np.uint64)
+    cap = ctypes.c_int64(buf.nbytes)
+    assert L.mdx_plan_spans(spans.ctypes.data, n, 0, 0, buf.ctypes.data, ctypes.byref(cap)) == 0
+    fb, hint, h = _plan_runs(buf)
+    assert h["count"] == n and fb[0] == 0 and fb[-1] == h["blocks"] and np.all(np.diff(fb) >= 1)
+    brute = np.searchsorted(fb, np.arange(h["blocks"]), side="right") - 1
+    got = np.array([_hinted_run(fb, hint, b) for b in range(h["blocks"])])
+    assert np.array_equal(got, brute)
 
 
 def test_plan_allreduce_unpack_builds_and_rejects_overlap():
@@ -281,7 +339,7 @@ def test_plan_allreduce_unpack_builds_and_rejects_overlap():
     cap = ctypes.c_int64(buf.nbytes)
     assert L.mdx_plan_allreduce_unpack(reps, 8, 0, runs.ctypes.data, 100, reps[0], 0, buf.ctypes.data, ctypes.byref(cap)) == 0
     h = _plan_header(buf)
-    assert h["kind"] == 2 and h["count"] == 100 and h["blocks"] == 100
+    assert h["kind"] == 2 and h["count"] == 100 and h["blocks"] == 100 * 4  # 250 fragments per run, 64 per one-wave workgroup
     bad = nat.grad_runs_array([(0, 16, 0x100000000 + 8)])  # gradient inside replica 0
     assert L.mdx_plan_allreduce_unpack(reps, 8, 0, bad.ctypes.data, 1, reps[0], 0, buf.ctypes.data, ctypes.byref(cap)) == -4
 
