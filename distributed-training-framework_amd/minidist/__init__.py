@@ -6,9 +6,11 @@ flat-parameter unit and the collective hook keep their names, signatures and
 hook semantics; their data movement runs as hand-written HIP kernels in
 ``libmdx.so`` (C ABI: include/mdx.h).
 
-Names of the reference outside this path (tensor / pipeline parallelism, the
-3D mesh, profiling helpers) are not part of this package; importing one
-raises an ImportError that says so.
+:mod:`minidist.profiling` keeps the reference's collective breakdown and
+overlap analysis, and knows the path's own kernels as collectives.  Names
+of the reference outside this path (tensor / pipeline parallelism, the 3D
+mesh) are not part of this package; importing one raises an ImportError
+that says so.
 """
 
 from .amp import DistributedGradScaler, PrecisionConfig, resolve_precision
@@ -26,6 +28,7 @@ from .comm import (
 )
 from .ddp import DDP, DistributedDataParallel
 from .fsdp import FSDP, FullyShardedDataParallel, MixedPrecisionPolicy
+from .profiling import analyze_kernel_trace, analyze_trace, format_collective_table, profile_steps, summarize_collectives
 
 __version__ = "0.1.0"
 
@@ -39,17 +42,13 @@ _OUT_OF_SCOPE = {
     "RowParallelLinear",
     "VocabParallelEmbedding",
     "vocab_parallel_cross_entropy",
-    "profile_steps",
-    "summarize_collectives",
-    "format_collective_table",
-    "analyze_trace",
 }
 
 
 def __getattr__(name: str):
     if name in _OUT_OF_SCOPE:
         raise ImportError(
-            f"minidist.{name} belongs to the reference's tensor/pipeline/profiling layers, which this "
+            f"minidist.{name} belongs to the reference's tensor/pipeline/mesh layers, which this "
             "build does not provide (it implements the data-parallel gradient path only)"
         )
     raise AttributeError(f"module 'minidist' has no attribute {name!r}")
@@ -74,5 +73,10 @@ __all__ = [
     "print_rank0",
     "comm_stats",
     "record_comm",
+    "profile_steps",
+    "summarize_collectives",
+    "format_collective_table",
+    "analyze_trace",
+    "analyze_kernel_trace",
     "__version__",
 ]

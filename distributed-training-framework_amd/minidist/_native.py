@@ -254,7 +254,11 @@ def _build_plan(call, what: str, device) -> Plan:
     host = np.zeros((size.value + 7) // 8, dtype=np.uint64)  # 8-byte aligned
     cap = ctypes.c_int64(host.nbytes)
     check(call(host.ctypes.data, ctypes.byref(cap)), what)
-    dev = torch.from_numpy(host.view(np.uint8)).to(device)
+    # Staged through pinned memory so the upload is an asynchronous copy on the
+    # current stream: rebuilding a plan never waits for the GPU to drain.
+    staged = torch.empty(host.nbytes, dtype=torch.uint8, pin_memory=True)
+    staged.copy_(torch.from_numpy(host.view(np.uint8)))
+    dev = staged.to(device, non_blocking=True)
     return Plan(host, dev)
 
 

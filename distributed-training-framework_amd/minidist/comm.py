@@ -372,6 +372,38 @@ class ResidentGroup:
         )
         return StreamWork(stream) if async_op else None
 
+    def all_reduce_unpack_wide(
+        self,
+        wire: torch.Tensor,
+        bucket: torch.Tensor,
+        runs,
+        grad_dtype: torch.dtype,
+        prescale: float,
+        inv_scale: float = 1.0,
+        found_inf: torch.Tensor | None = None,
+        async_op: bool = False,
+    ):
+        """:meth:`all_reduce_unpack` for contributions narrower than the bucket.
+
+        ``wire`` is this rank's row of bf16 contributions (a symmetric buffer);
+        every replica's element is widened to fp32 and multiplied by
+        ``prescale`` where it is read, the W values are summed in rank order
+        into ``bucket`` (fp32, same element offsets as ``wire``) and unpacked
+        into the gradients of ``runs``."""
+        _native.require_device_tensor(wire, "all_reduce input")
+        _native.require_device_tensor(bucket, "all_reduce output")
+        arena, off = self._locate(wire)
+        if bucket.numel() < wire.numel():
+            raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
+        bases = [b + off * arena.esize for b in arena.row_ptrs]
+        stream = torch.cuda.current_stream(wire.device)
+        _native.allreduce_unpack_wide(
+            bases, _native.dtype_code(arena.dtype), runs, bucket.data_ptr(), _native.dtype_code(bucket.dtype),
+            _native.dtype_code(grad_dtype), _native.f32(prescale), _native.f32(inv_scale),
+            found_inf.data_ptr() if found_inf is not None else None, stream.cuda_stream,
+        )
+        return StreamWork(stream) if async_op else None
+
     def plan_all_reduce_unpack(self, buffer: torch.Tensor, runs, grad_dtype: torch.dtype) -> "_native.Plan":
         """Device plan of :meth:`all_reduce_unpack` for fixed ``runs`` (one dispatch per launch)."""
         _native.require_device_tensor(buffer, "all_reduce input")

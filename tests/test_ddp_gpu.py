@@ -127,10 +127,14 @@ def _capture_hook(store):
     return hook
 
 
+@pytest.mark.parametrize("comm_stream", [False, True])
 @pytest.mark.parametrize("W", [2, 4])
 @pytest.mark.parametrize("cap,overlap", [(25.0, True), (1e-6, True), (1e6, True), (25.0, False)])
-def test_backward_matches_full_batch_and_oracle(W, cap, overlap):
-    """Reference tests/test_ddp.py:32-77 on one GPU: rank r's DDP grads == full-batch grads."""
+def test_backward_matches_full_batch_and_oracle(W, cap, overlap, comm_stream):
+    """Reference tests/test_ddp.py:32-77 on one GPU: rank r's DDP grads == full-batch grads.
+
+    With ``comm_stream`` the bucket pipelines run on a dedicated stream while
+    backward continues on the default one; the result must not change by a bit."""
     c = tiny_gpt.Config()
     ids, tgt = tiny_gpt.batch(c, 8)
     full = tiny_gpt.GPT(c).to(DEV)
@@ -151,7 +155,8 @@ def test_backward_matches_full_batch_and_oracle(W, cap, overlap):
     captured: dict[int, torch.Tensor] = {}
     for p in model.parameters():
         p.register_post_accumulate_grad_hook(_capture_hook(captured))  # runs before DDP's hook
-    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap,
+              comm_stream=comm_stream)
     dts = [o.F32] * len(expected)
     stage_peers(ddp, replica, dts, rank, W)
     _, l = ddp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
@@ -165,6 +170,139 @@ def test_backward_matches_full_batch_and_oracle(W, cap, overlap):
         diff = (p.grad - e).abs().max().item()
         denom = max(e.abs().max().item(), 1.0)
         assert diff / denom <= 2e-5, f"param {i}: relative error {diff / denom:.3e}"
+
+
+def test_comm_stream_carries_every_launch(monkeypatch):
+    """With a caller's stream every pack and fused reduction is enqueued on it, never on
+    the default stream, and the default stream sees the results after backward returns."""
+    from minidist import _native
+
+    seen = []
+    for name in ("pack", "pack_planned", "allreduce_unpack", "allreduce_unpack_planned"):
+        orig = getattr(_native, name)
+
+        def spy(*a, _orig=orig, _name=name):
+            seen.append((_name, a[-1]))
+            return _orig(*a)
+
+        monkeypatch.setattr(_native, name, spy)
+    c = tiny_gpt.Config()
+    W, rank = 4, 2
+    ids, tgt = tiny_gpt.batch(c, 8)
+    replica = []
+    for r in range(W):
+        m = tiny_gpt.GPT(c).to(DEV)
+        _, l_r = m(ids.chunk(W)[r].to(DEV), tgt.chunk(W)[r].to(DEV))
+        l_r.backward()
+        replica.append([host_bits(p.grad) for p in m.parameters()])
+    side = torch.cuda.Stream(DEV)
+
+    scale = 2.0**10
+    peers = [[(g * scale).astype(g.dtype) for g in row] for row in replica]
+    dts = [o.F32] * len(replica[0])
+
+    def run(stream):
+        model = tiny_gpt.GPT(c).to(DEV)
+        captured: dict[int, torch.Tensor] = {}
+        for p in model.parameters():
+            p.register_post_accumulate_grad_hook(_capture_hook(captured))  # runs before DDP's hook
+        scaler = DistributedGradScaler(init_scale=scale)
+        ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=0.01, grad_scaler=scaler,
+                  comm_stream=stream)
+        stage_peers(ddp, peers, dts, rank, W)
+        _, l = ddp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
+        scaler.scale_loss(l).backward()
+
+        class _Opt:
+            param_groups = [{"params": list(model.parameters())}]
+
+        found = scaler.unscale_(_Opt())
+        own = [host_bits(captured[id(p)]) for p in model.parameters()]
+        want = o.ddp_pipeline([own if r == rank else peers[r] for r in range(W)], dts,
+                              [p.numel() for p in model.parameters()], 0.01, rank, 1.0 / scale)
+        assert not found and not want["found_inf"]
+        for i, p in enumerate(model.parameters()):
+            assert same_bits(host_bits(p.grad), want["grads"][i]), f"param {i}"
+        return len(ddp._buckets)
+
+    nb = run(side)
+    launches = list(seen)
+    assert nb > 2 and len(launches) >= 2
+    assert {s for _, s in launches} == {side.cuda_stream}
+    assert side.cuda_stream != torch.cuda.current_stream(DEV).cuda_stream
+    seen.clear()
+    run(False)
+    assert {s for _, s in seen} == {torch.cuda.current_stream(DEV).cuda_stream}
+
+
+@pytest.mark.parametrize("n_params", [10, 60])
+@pytest.mark.parametrize("comm_stream", [False, True])
+def test_new_gradient_tensors_every_step(rng, n_params, comm_stream, monkeypatch):
+    """``zero_grad(set_to_none=True)``: every step brings new gradient tensors.
+
+    10 gradients fit one kernel-argument table (their pointer columns are
+    patched, the tables are built once); 60 need a device plan (rebuilt and
+    re-uploaded each step).  Every step is bit-exact against the oracle."""
+    from minidist import ddp as ddp_mod
+
+    builds = []
+    orig_build = ddp_mod._RunPlan._build
+    monkeypatch.setattr(ddp_mod._RunPlan, "_build", lambda self, *a: (builds.append(1), orig_build(self, *a))[1])
+    W, rank = 4, 1
+    shapes = [(int(rng.integers(1, 300)),) if i % 3 else (int(rng.integers(1, 40)), 33) for i in range(n_params)]
+    model = Flat(shapes)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=1e6, comm_stream=comm_stream)
+    numels = [int(np.prod(s)) for s in shapes]
+    keep = []  # old gradients stay alive, so every step's gradients sit at new addresses
+    for step in range(3):
+        grads = synthetic_grads(rng, shapes, W, torch.float32, 1.0)
+        stage_peers(ddp, grads, [o.F32] * n_params, rank, W)
+        keep.append([p.grad for p in model.parameters()])
+        for p, g in zip(model.parameters(), grads[rank], strict=True):
+            p.grad = dev_from(g, p.shape)
+        ddp.finish_gradient_sync()
+        want = o.ddp_pipeline(grads, [o.F32] * n_params, numels, 1e6, rank, None)
+        for i, p in enumerate(model.parameters()):
+            assert same_bits(host_bits(p.grad), want["grads"][i]), f"step {step} param {i}"
+    assert len(builds) == (1 if n_params <= 48 else 3)
+
+
+@pytest.mark.parametrize("comm_stream", [False, True])
+def test_set_to_none_backward_steps(comm_stream):
+    """Three overlapped backwards with the gradients dropped in between: per-bucket
+    launches during backward, new gradient tensors every step, oracle-exact each time."""
+    c = tiny_gpt.Config()
+    W, rank = 4, 3
+    ids, tgt = tiny_gpt.batch(c, 8)
+    replica = []
+    for r in range(W):
+        m = tiny_gpt.GPT(c).to(DEV)
+        _, l_r = m(ids.chunk(W)[r].to(DEV), tgt.chunk(W)[r].to(DEV))
+        l_r.backward()
+        replica.append([host_bits(p.grad) for p in m.parameters()])
+    model = tiny_gpt.GPT(c).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture_hook(captured))
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=0.01, comm_stream=comm_stream)
+    dts = [o.F32] * len(replica[0])
+    numels = [p.numel() for p in model.parameters()]
+    for step in range(3):
+        peers = [[(g * (step + 1)).astype(g.dtype) for g in row] for row in replica]
+        stage_peers(ddp, peers, dts, rank, W)
+        for p in model.parameters():
+            p.grad = None
+        _, l = ddp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
+        l.backward()
+        own = [host_bits(captured[id(p)]) for p in model.parameters()]
+        want = o.ddp_pipeline([own if r == rank else peers[r] for r in range(W)], dts, numels, 0.01, rank, None)
+        for i, p in enumerate(model.parameters()):
+            assert same_bits(host_bits(p.grad), want["grads"][i]), f"step {step} param {i}"
+
+
+def test_comm_stream_argument_is_checked():
+    with pytest.raises(TypeError):
+        DDP(Flat([(4,)]), process_group=ResidentGroup(2, 0, DEV), comm_stream="yes")
 
 
 def test_no_sync_accumulation_then_sync():
