@@ -27,6 +27,11 @@ struct bf16 {
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// The same vector in the global address space.  Every buffer this library
+// touches is device memory, but pointers read from a work table are generic
+// (flat) pointers; casting them makes the compiler emit global_load/store
+// instead of flat_load/store (no aperture check, no LDS counter).
+typedef __attribute__((address_space(1))) u32x4 gu32x4;
 
 // ----------------------------------------------------------------------------
 // Element conversions (IEEE, round to nearest even, NaN -> 0xFFFF for bf16)
@@ -85,7 +90,7 @@ __device__ __forceinline__ void vload(T (&dst)[E], const T* p) {
   static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
   constexpr int NV = int(E * sizeof(T) / 16);
   constexpr int PER = int(16 / sizeof(T));
-  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  const gu32x4* q = (const gu32x4*)(p);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     u32x4 w;
@@ -103,7 +108,7 @@ __device__ __forceinline__ void vstore(T* p, const T (&src)[E]) {
   static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
   constexpr int NV = int(E * sizeof(T) / 16);
   constexpr int PER = int(16 / sizeof(T));
-  u32x4* q = reinterpret_cast<u32x4*>(p);
+  gu32x4* q = (gu32x4*)(p);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     u32x4 w;
