@@ -200,22 +200,36 @@ class StreamWork:
     """Completion handle of a collective launched on a stream.
 
     ``wait()`` has NCCL-Work semantics on a GPU: it makes the *current* stream
-    wait for the collective; the host does not block.
+    wait for the collective; the host does not block.  Nothing is recorded at
+    launch: a waiter on the producing stream is already ordered after the
+    collective, and any other waiter gets an event recorded on the producing
+    stream when it waits -- later than the collective, so it may wait for more
+    work than the collective, never for less.
     """
 
+    __slots__ = ("_stream", "_event")
+
     def __init__(self, stream: torch.cuda.Stream):
-        self._event = torch.cuda.Event()
-        self._event.record(stream)
+        self._stream = stream
+        self._event: torch.cuda.Event | None = None
+
+    def _marker(self) -> torch.cuda.Event:
+        if self._event is None:
+            self._event = torch.cuda.Event()
+            self._event.record(self._stream)
+        return self._event
 
     def wait(self, timeout=None) -> bool:  # noqa: ARG002 - mirrors dist.Work.wait
-        torch.cuda.current_stream().wait_event(self._event)
+        current = torch.cuda.current_stream(self._stream.device)
+        if current != self._stream:
+            current.wait_event(self._marker())
         return True
 
     def is_completed(self) -> bool:
-        return self._event.query()
+        return self._marker().query()
 
     def synchronize(self) -> None:
-        self._event.synchronize()
+        self._marker().synchronize()
 
 
 _ROW_ALIGN_BYTES = 256
