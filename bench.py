@@ -95,6 +95,24 @@ def calibrate_copy() -> int:
     return 0
 
 
+# Committed rocprofv3 FETCH_SIZE + WRITE_SIZE summaries of each workload's dominant kernel.
+TRAFFIC_FILES = {
+    "cfg0": "allreduce_unpack_tiny_gpt_w4_traffic.json",
+    "cfg1": "allreduce_unpack_gpt2_124m_w8_traffic.json",
+    "cfg2": "allreduce_unpack_gpt2_medium_w4_traffic.json",
+    "cfg3": "share_cast_gpt2_xl_fsdp_w8_traffic.json",
+    "cfg4": "allreduce_wide_llama7b_w8_traffic.json",
+}
+
+
+def measured_traffic(workload: str) -> int | None:
+    """HBM bytes per dispatch of the dominant kernel, from the committed PMC summary."""
+    path = ROOT / "profiles" / TRAFFIC_FILES.get(workload, "")
+    if not path.is_file():
+        return None
+    return json.loads(path.read_text()).get("bytes_per_launch")
+
+
 # ---------------------------------------------------------------------------
 # DDP workloads (cfg0, cfg1, cfg2, cfg4)
 # ---------------------------------------------------------------------------
@@ -219,10 +237,7 @@ def bench_ddp(name: str, args) -> dict:
     kname = ("allreduce_wide_kernel_dev<bf16, float, bf16, 8>" if b0.widening
              else f"allreduce_unpack_kernel_dev<float, float, {W}>")
 
-    traffic = None
-    tfile = ROOT / "profiles" / "allreduce_unpack_gpt2_124m_w8_traffic.json"
-    if name == "cfg1" and tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
+    traffic = measured_traffic(name)
 
     return {
         "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",
@@ -404,7 +419,7 @@ def bench_fsdp(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(share_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("cfg3"),
             "bytes_per_launch": 20 * S,
             "avg_launch_ms": round(share_avg, 5),
         },

@@ -24,11 +24,11 @@ inline int status(hipError_t e) { return e == hipSuccess ? MDX_OK : int(e); }
 
 inline uintptr_t addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }
 
-// Smallest h in [0, E) such that every (pointer, element size) advanced by h
-// elements is 16-byte aligned; -1 if none exists or the run has no full
-// fragment after it.
+// Smallest h in [0, kHeadRange) such that every (pointer, element size)
+// advanced by h elements is 16-byte aligned; -1 if none exists or the run has
+// no full fragment of E elements after it.
 int aligned_head(const uintptr_t* ptrs, const int* sizes, int count, int E, int64_t n) {
-  for (int h = 0; h < E; ++h) {
+  for (int h = 0; h < kHeadRange; ++h) {
     bool ok = true;
     for (int k = 0; k < count && ok; ++k) {
       ok = ((ptrs[k] + uintptr_t(h) * uintptr_t(sizes[k])) & 15u) == 0;
@@ -67,9 +67,9 @@ struct Rec {
 template <typename Emit>
 int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool in_place, Emit&& emit) {
   const int E = copy_frag_elems(sdt, ddt);
-  const int64_t VPB = int64_t(kBlock) * kCopyFragsPerThread;
-  const int64_t EPB = VPB * E;
   const int ss = dtype_size(sdt), ds = dtype_size(ddt);
+  const int64_t VPB = int64_t(kBlock) * copy_unroll(E * ss);
+  const int64_t EPB = VPB * E;
   for (int i = 0; i < n_spans; ++i) {
     const mdx_span& sp = spans[i];
     const char* src = static_cast<const char*>(in_place ? sp.dst : sp.src);
@@ -371,7 +371,7 @@ int check_fused(const void* const* replicas, int world, int dtype, int out_dtype
   f->es = es;
   f->os = os;
   f->gs = gs;
-  f->E = frag_elems(min_size(es, os), gs);  // as the kernel's compile-time fragment
+  f->E = store_frag_elems(max_size(os, gs));  // as the kernel's compile-time fragment
   f->U = allreduce_unroll(world, f->E * es);
   return MDX_OK;
 }
@@ -509,7 +509,7 @@ int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const i
   p.pre = 1.0f;
   p.inv_scale = 1.0f;
   const char* base0 = static_cast<const char*>(replicas[0]);
-  const int E = frag_elems(es, es);
+  const int E = store_frag_elems(es);
   const int U = allreduce_unroll(world, E * es);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](const PieceBatch& b) { return launch_allreduce(dtype, dtype, false, world, b, p, st); };
@@ -634,7 +634,7 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   p.flags = flags;
   const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
   const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
-  const int E = frag_elems(is, os);
+  const int E = store_frag_elems(os);
   const int U = share_unroll(wmax, E * is);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](const PieceBatch& b) {

@@ -37,8 +37,8 @@ struct CopyOp {
 
 template <typename S, typename D, int SCALE, bool CHECK, typename View>
 __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) {
-  constexpr int E = frag_elems(int(sizeof(S)), int(sizeof(D)));
-  constexpr int U = kCopyFragsPerThread;
+  constexpr int E = store_frag_elems(int(sizeof(D)));
+  constexpr int U = copy_unroll(E * int(sizeof(S)));
   constexpr int VPB = kBlock * U;
   constexpr int EPT = U * E;
   constexpr int EPB = kBlock * EPT;
@@ -167,7 +167,8 @@ hipError_t launch_any(int src_dtype, int dst_dtype, const L& l, const CopyParams
 }  // namespace
 
 int copy_frag_elems(int src_dtype, int dst_dtype) {
-  return frag_elems(dtype_size(src_dtype), dtype_size(dst_dtype));
+  (void)src_dtype;
+  return store_frag_elems(dtype_size(dst_dtype));
 }
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,

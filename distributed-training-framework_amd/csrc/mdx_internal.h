@@ -32,6 +32,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // (flat) pointers; casting them makes the compiler emit global_load/store
 // instead of flat_load/store (no aperture check, no LDS counter).
 typedef __attribute__((address_space(1))) u32x4 gu32x4;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) u32x2 gu32x2;
 
 // ----------------------------------------------------------------------------
 // Element conversions (IEEE, round to nearest even, NaN -> 0xFFFF for bf16)
@@ -82,41 +84,65 @@ __device__ __forceinline__ T zero_of() {
 }
 
 // ----------------------------------------------------------------------------
-// 16-byte vector loads and stores of E elements
+// Vector loads and stores of one fragment (E elements: 8, 16 or 32 bytes)
 // ----------------------------------------------------------------------------
 
 template <typename T, int E, bool NT>
 __device__ __forceinline__ void vload(T (&dst)[E], const T* p) {
-  static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
-  constexpr int NV = int(E * sizeof(T) / 16);
-  constexpr int PER = int(16 / sizeof(T));
-  const gu32x4* q = (const gu32x4*)(p);
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    u32x4 w;
+  constexpr int BYTES = int(E * sizeof(T));
+  static_assert(BYTES == 8 || BYTES % 16 == 0, "fragment must be 8 bytes or whole 16-byte vectors");
+  if constexpr (BYTES == 8) {
+    const gu32x2* q = (const gu32x2*)(p);
+    u32x2 w;
     if constexpr (NT) {
-      w = __builtin_nontemporal_load(q + k);
+      w = __builtin_nontemporal_load(q);
     } else {
-      w = q[k];
+      w = *q;
     }
-    __builtin_memcpy(&dst[k * PER], &w, 16);
+    __builtin_memcpy(&dst[0], &w, 8);
+  } else {
+    constexpr int NV = BYTES / 16;
+    constexpr int PER = int(16 / sizeof(T));
+    const gu32x4* q = (const gu32x4*)(p);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      u32x4 w;
+      if constexpr (NT) {
+        w = __builtin_nontemporal_load(q + k);
+      } else {
+        w = q[k];
+      }
+      __builtin_memcpy(&dst[k * PER], &w, 16);
+    }
   }
 }
 
 template <typename T, int E, bool NT>
 __device__ __forceinline__ void vstore(T* p, const T (&src)[E]) {
-  static_assert((E * sizeof(T)) % 16 == 0, "fragment must be whole 16-byte vectors");
-  constexpr int NV = int(E * sizeof(T) / 16);
-  constexpr int PER = int(16 / sizeof(T));
-  gu32x4* q = (gu32x4*)(p);
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    u32x4 w;
-    __builtin_memcpy(&w, &src[k * PER], 16);
+  constexpr int BYTES = int(E * sizeof(T));
+  static_assert(BYTES == 8 || BYTES % 16 == 0, "fragment must be 8 bytes or whole 16-byte vectors");
+  if constexpr (BYTES == 8) {
+    gu32x2* q = (gu32x2*)(p);
+    u32x2 w;
+    __builtin_memcpy(&w, &src[0], 8);
     if constexpr (NT) {
-      __builtin_nontemporal_store(w, q + k);
+      __builtin_nontemporal_store(w, q);
     } else {
-      q[k] = w;
+      *q = w;
+    }
+  } else {
+    constexpr int NV = BYTES / 16;
+    constexpr int PER = int(16 / sizeof(T));
+    gu32x4* q = (gu32x4*)(p);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      u32x4 w;
+      __builtin_memcpy(&w, &src[k * PER], 16);
+      if constexpr (NT) {
+        __builtin_nontemporal_store(w, q + k);
+      } else {
+        q[k] = w;
+      }
     }
   }
 }
@@ -181,12 +207,21 @@ struct CopyParams {
   int32_t* found_inf;
 };
 
-// Elements per 16-byte-aligned fragment for a dtype pair, and fragments per
-// lane of the copy kernel (one fragment = one 16-byte vector of the narrower
-// dtype; the scalar path of a misaligned span handles as many elements).
+// Fragments.  A fragment is one 16-byte vector of the widest type a kernel
+// stores, so that every store instruction of a wave writes 64 x 16 = 1 KB of
+// consecutive bytes; a narrower input is then read 8 bytes per lane, a wider
+// one 32 bytes.  (Fragments sized by the narrow type instead store 16 bytes
+// of every 32 per instruction, which measured 6-8% extra HBM writes on the
+// widening kernels.)  Each lane loads at least 16 bytes per input in the copy
+// kernel (U fragments), and about 128 bytes across all inputs in the W-way
+// reductions.
 constexpr int min_size(int a, int b) { return a < b ? a : b; }
-constexpr int frag_elems(int src_size, int dst_size) { return 16 / min_size(src_size, dst_size); }
-constexpr int kCopyFragsPerThread = 1;  // measured on MI355X: 1 beats 2 and 4
+constexpr int max_size(int a, int b) { return a > b ? a : b; }
+constexpr int store_frag_elems(int widest_store_size) { return 16 / widest_store_size; }
+constexpr int copy_unroll(int frag_in_bytes) { return frag_in_bytes >= 16 ? 1 : 16 / frag_in_bytes; }
+// Alignment heads are searched over 16 bytes of the narrowest (2-byte) type,
+// whatever the fragment, so that mixed-dtype runs keep a vector body.
+constexpr int kHeadRange = 8;
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
                        hipStream_t stream);
@@ -225,18 +260,18 @@ struct ReduceParams {
 };
 
 // Fragments per lane and contribution (U) of the W-way reductions: each lane
-// keeps U fragments of all W contributions in flight, about 8 16-byte loads
-// (one fragment per contribution at W = 8).  Measured on MI355X with one-wave
-// workgroups: 16 or 32 loads per lane cost 2-6% of the W = 8 all-reduce's
-// bandwidth, and a workgroup that streams several chunks in a double-buffered
-// loop loses to one short-lived workgroup per chunk.
-constexpr int kReduceVecsPerLane = 8;
+// keeps U fragments of all W contributions in flight, about 128 bytes of
+// loads (one 16-byte fragment per contribution at W = 8).  Measured on MI355X
+// with one-wave workgroups: 256 or 512 bytes per lane cost 2-6% of the W = 8
+// all-reduce's bandwidth, and a workgroup that streams several chunks in a
+// double-buffered loop loses to one short-lived workgroup per chunk.
+constexpr int kReduceLoadBytesPerLane = 128;
 constexpr int clamp_unroll(int u) { return u < 1 ? 1 : (u > 8 ? 8 : u); }
-constexpr int allreduce_unroll(int world, int frag_bytes) {
-  return clamp_unroll(kReduceVecsPerLane / (world * (frag_bytes / 16)));
+constexpr int allreduce_unroll(int world, int frag_in_bytes) {
+  return clamp_unroll(kReduceLoadBytesPerLane / (world * frag_in_bytes));
 }
-constexpr int share_unroll(int wmax, int frag_bytes) {
-  return clamp_unroll(kReduceVecsPerLane / (wmax * (frag_bytes / 16)));
+constexpr int share_unroll(int wmax, int frag_in_bytes) {
+  return clamp_unroll(kReduceLoadBytesPerLane / (wmax * frag_in_bytes));
 }
 
 // Host-side dispatch into the instantiating translation units.

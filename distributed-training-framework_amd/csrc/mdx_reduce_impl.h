@@ -27,7 +27,8 @@
 //
 // Every contribution is read once per step, so every load is non-temporal;
 // each lane keeps U fragments of all W contributions in flight before the
-// first add (U * W = 8 16-byte loads for the all-reduce at W = 8).
+// first add (about 128 bytes per lane: U * W = 8 16-byte loads for the fp32
+// all-reduce at W = 8).
 #pragma once
 
 #include "mdx_internal.h"
@@ -41,8 +42,7 @@ namespace reduce_impl {
 
 template <typename In, typename T, typename G, int W, bool UNPACK, bool PRE, typename View>
 __device__ __forceinline__ void allreduce_body(const View& tab, const ReduceParams& p) {
-  constexpr int E = frag_elems(min_size(int(sizeof(In)), int(sizeof(T))),
-                               UNPACK ? int(sizeof(G)) : int(sizeof(T)));
+  constexpr int E = store_frag_elems(UNPACK ? max_size(int(sizeof(T)), int(sizeof(G))) : int(sizeof(T)));
   constexpr int U = allreduce_unroll(W, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
@@ -258,7 +258,7 @@ enum : int { kPreNone = 0, kPreMul = 1, kPreDiv = 2 };
 
 template <typename In, typename Acc, typename Out, int WMAX, int PRE, bool ACC>
 __device__ __forceinline__ void share_body(const PieceBatch& b, const ReduceParams& p, int s, int c, int nblk) {
-  constexpr int E = frag_elems(int(sizeof(In)), int(sizeof(Out)));
+  constexpr int E = store_frag_elems(int(sizeof(Out)));
   constexpr int U = share_unroll(WMAX, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
