@@ -133,28 +133,39 @@ class DistributedGradScaler:
 
     # -- device flag ----------------------------------------------------------
 
-    def _flag(self, device: torch.device) -> torch.Tensor:
-        """This step's found-inf flag on ``device``, zeroed on first use in a step.
+    def _flag(self, device: torch.device, defer_clear: bool = False) -> tuple[torch.Tensor, bool]:
+        """This step's found-inf flag on ``device`` and whether it still needs clearing.
 
-        Cleared with a fill kernel (not a memset) so that the step can be
-        captured into a HIP graph."""
+        The flag is zeroed on its first use in a step, with a fill kernel (not
+        a memset) so that the step can be captured into a HIP graph; with
+        ``defer_clear`` the caller enqueues that clear itself (``flag.zero_()``)
+        before anything that sets the flag."""
         flag = self._flags.get(device)
+        pending = False
         if flag is None:
             flag = torch.zeros(1, dtype=torch.int32, device=device)
             self._flags[device] = flag
             self._flag_armed.add(device)
+            pending = defer_clear  # already zero; clearing again keeps every step's launch the same
         elif device not in self._flag_armed:
-            flag.zero_()
+            if defer_clear:
+                pending = True
+            else:
+                flag.zero_()
             self._flag_armed.add(device)
-        return flag
+        return flag, pending
 
-    def _begin_fused_unscale(self, device: torch.device, param_ids: frozenset) -> tuple[float, torch.Tensor]:
+    def _begin_fused_unscale(
+        self, device: torch.device, param_ids: frozenset, defer_clear: bool = False
+    ) -> tuple[float, torch.Tensor] | tuple[float, torch.Tensor, bool]:
         """Hand a producer (DDP's unpack) the inverse scale and the device flag.
 
         The producer writes these params' grads already multiplied by
         ``1/scale`` and flags non-finite results; ``unscale_`` then skips them.
         Gradients must not be accumulated on top of unscaled values, so a
-        second synchronised backward before ``step``/``update`` is an error."""
+        second synchronised backward before ``step``/``update`` is an error.
+        With ``defer_clear`` a third value says whether the producer must clear
+        the flag (first producer of the step) before its kernels run."""
         if self._unscaled:
             raise RuntimeError("gradients were already unscaled this step; call update() first")
         if not self._prescaled.isdisjoint(param_ids):
@@ -163,7 +174,10 @@ class DistributedGradScaler:
                 "would accumulate onto already-unscaled ones"
             )
         self._prescaled |= param_ids
-        return 1.0 / self._scale, self._flag(device)
+        flag, pending = self._flag(device, defer_clear)
+        if defer_clear:
+            return 1.0 / self._scale, flag, pending
+        return 1.0 / self._scale, flag
 
     # -- the training-loop surface -----------------------------------------
 
@@ -186,7 +200,7 @@ class DistributedGradScaler:
 
         inv_scale = _native.f32(1.0 / self._scale)
         device = comm.current_device()
-        flag = self._flag(device)
+        flag, _ = self._flag(device)
 
         groups: dict[torch.dtype, list[tuple[int, int, int]]] = {}
         for group in optimizer.param_groups:

@@ -300,6 +300,103 @@ def test_set_to_none_backward_steps(comm_stream):
             assert same_bits(host_bits(p.grad), want["grads"][i]), f"step {step} param {i}"
 
 
+def test_graph_replays_match_eager(rng):
+    """capture_graphs: every replay is bit-exact with the eager launches on the same inputs.
+
+    Eager work and host syncs run between replays; the graph is re-captured when the
+    scale backs off (found-inf at step 2) and when the gradients move (set to None
+    before step 4), and replayed otherwise."""
+    W, rank, init = 4, 1, 2.0**10
+    shapes = [(int(rng.integers(1, 300)),) if i % 3 else (int(rng.integers(1, 40)), 33) for i in range(60)]
+    numels = [int(np.prod(s)) for s in shapes]
+    runs = {}
+    for graphs in (False, True):
+        model = Flat(shapes)
+        scaler = DistributedGradScaler(init_scale=init, growth_interval=1000)
+        ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=0.02, grad_scaler=scaler,
+                  capture_graphs=graphs)
+        runs[graphs] = (model, scaler, ddp)
+    step_rng = np.random.default_rng(77)
+    captured = []
+    for step in range(6):
+        grads = synthetic_grads(step_rng, shapes, W, torch.float32, init)
+        if step == 2:
+            grads[(rank + 1) % W][5] = grads[(rank + 1) % W][5].copy()
+            grads[(rank + 1) % W][5][0] = np.float32(np.inf)
+        results = {}
+        for graphs, (model, scaler, ddp) in runs.items():
+            stage_peers(ddp, grads, [o.F32] * len(shapes), rank, W)
+            keep = [p.grad for p in model.parameters()]  # alive, so new gradients get new addresses
+            for p, g in zip(model.parameters(), grads[rank], strict=True):
+                if step == 4:
+                    p.grad = None
+                if p.grad is None:
+                    p.grad = dev_from(g, p.shape)
+                else:
+                    p.grad.copy_(dev_from(g, p.shape))  # same tensors: the graph replays
+            ddp.finish_gradient_sync()
+
+            class _Opt:
+                param_groups = [{"params": list(model.parameters())}]
+
+            found = scaler.unscale_(_Opt())
+            scaler.update()
+            results[graphs] = (found, [host_bits(p.grad) for p in model.parameters()])
+            if graphs:
+                captured.append(id(ddp._graphs[(0, len(ddp._buckets))][1]))
+            # unrelated eager work and a host sync between replays
+            x = torch.randn(1 << 16, device=DEV)
+            assert torch.isfinite(x.sum()).item()
+        del keep
+        # the step's scale: 2^10 until the backoff at the end of step 2, 2^9 after
+        want = o.ddp_pipeline(grads, [o.F32] * len(shapes), numels, 0.02, rank, 1.0 / (init if step <= 2 else init / 2))
+        assert results[True][0] == results[False][0] == want["found_inf"] == (step == 2)
+        for i in range(len(shapes)):
+            assert same_bits(results[True][1][i], results[False][1][i]), f"step {step} param {i}"
+            assert same_bits(results[True][1][i], want["grads"][i]), f"step {step} param {i} vs oracle"
+    # captured at step 0, re-captured at 3 (scale backed off at the end of step 2) and 4 (new gradients)
+    assert captured[0] == captured[1] == captured[2] != captured[3] != captured[4] == captured[5]
+    assert runs[True][2]._graphs and not runs[False][2]._graphs
+
+
+@pytest.mark.parametrize("cap", [25.0, 0.01])
+def test_graph_launches_during_backward(cap):
+    """capture_graphs with per-bucket launches from the backward hooks: three steps, oracle-exact."""
+    c = tiny_gpt.Config()
+    W, rank = 4, 0
+    ids, tgt = tiny_gpt.batch(c, 8)
+    replica = []
+    for r in range(W):
+        m = tiny_gpt.GPT(c).to(DEV)
+        _, l_r = m(ids.chunk(W)[r].to(DEV), tgt.chunk(W)[r].to(DEV))
+        l_r.backward()
+        replica.append([host_bits(p.grad) for p in m.parameters()])
+    model = tiny_gpt.GPT(c).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture_hook(captured))
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, capture_graphs=True)
+    dts = [o.F32] * len(replica[0])
+    numels = [p.numel() for p in model.parameters()]
+    for step in range(3):
+        stage_peers(ddp, replica, dts, rank, W)
+        for p in model.parameters():
+            if p.grad is not None:
+                p.grad.zero_()  # accumulate into the same tensors: replays after the first step
+        _, l = ddp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
+        l.backward()
+        own = [host_bits(captured[id(p)]) for p in model.parameters()]
+        want = o.ddp_pipeline([own if r == rank else replica[r] for r in range(W)], dts, numels, cap, rank, None)
+        for i, p in enumerate(model.parameters()):
+            assert same_bits(host_bits(p.grad), want["grads"][i]), f"step {step} param {i}"
+    assert len(ddp._graphs) >= 1
+
+
+def test_capture_graphs_argument_is_checked():
+    with pytest.raises(ValueError):
+        DDP(Flat([(4,)]), process_group=ResidentGroup(2, 0, DEV), capture_graphs=True, comm_stream=True)
+
+
 def test_comm_stream_argument_is_checked():
     with pytest.raises(TypeError):
         DDP(Flat([(4,)]), process_group=ResidentGroup(2, 0, DEV), comm_stream="yes")
