@@ -41,7 +41,7 @@ from minidist import workloads as wl  # noqa: E402  (parameter tables only)
 from .gradpath import build_buckets  # noqa: E402
 
 
-def _worker(rank, world, store, cfg, steps, warmup, threads, cap_mb, scale, out_path, layers):
+def _worker(rank, world, store, cfg, steps, warmup, threads, cap_mb, scale, out_path, layers, grads_path=None):
     torch.set_num_threads(threads)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world)
     specs = wl.gpt_specs(**cfg)
@@ -94,18 +94,21 @@ def _worker(rank, world, store, cfg, steps, warmup, threads, cap_mb, scale, out_
         Path(out_path).write_text(
             json.dumps({"step_s": t.tolist(), "numel": numel, "buckets": len(layout)})
         )
+        if grads_path is not None:  # checking runs: rank 0's gradients after the last step
+            torch.save([gr.clone() for gr in grads], grads_path)
     dist.barrier()
     dist.destroy_process_group()
 
 
 def run(world: int, steps: int, warmup: int, threads: int, cfg: dict, cap_mb: float = 25.0,
-        scale: float = 2.0**16, layers: int | None = None) -> dict:
+        scale: float = 2.0**16, layers: int | None = None, grads_path: str | None = None) -> dict:
+    """Time the path; with ``grads_path``, rank 0's final gradients are saved there (torch.save)."""
     with tempfile.TemporaryDirectory() as tmp:
         store = os.path.join(tmp, "store")
         out = os.path.join(tmp, "out.json")
         mp.spawn(
             _worker,
-            args=(world, store, cfg, steps, warmup, threads, cap_mb, scale, out, layers),
+            args=(world, store, cfg, steps, warmup, threads, cap_mb, scale, out, layers, grads_path),
             nprocs=world,
             join=True,
         )
