@@ -25,7 +25,8 @@ dispatch of the timed region.  The CPU baseline
 anything touches the GPU.
 
 The other benchmark configurations are parity cases; ``--workload`` measures
-them too (one JSON line each, same fields, no CPU baseline):
+them too (one JSON line each, same fields; the CPU baseline for cfg0 and cfg2,
+whose replicas fit in host memory):
 
     cfg0  tiny GPT fp32, W = 4, one 13 MiB bucket      (staged bytes 36*N)
     cfg2  GPT-2-medium fp32, W = 4, 25 MB buckets       (staged bytes 36*N)
@@ -57,10 +58,15 @@ CAP_MB = 25.0
 LOSS_SCALE = 2.0**16
 
 
-def cpu_baseline(steps: int, threads: int) -> dict | None:
+# The reference's CPU path is timed beside the DDP workloads it can hold in host memory.
+CPU_BASELINE = {"cfg0": ("tiny", 4), "cfg1": ("gpt2-small", W_CFG1), "cfg2": ("gpt2-medium", 4)}
+
+
+def cpu_baseline(workload: str, steps: int, threads: int) -> dict | None:
     """Time the reference's CPU path (oracle/gloo_path.py) in a child process."""
-    cmd = [sys.executable, "-m", "oracle.gloo_path", "--world", str(W_CFG1), "--steps", str(steps),
-           "--warmup", "1", "--threads", str(threads)]
+    config, world = CPU_BASELINE[workload]
+    cmd = [sys.executable, "-m", "oracle.gloo_path", "--config", config, "--world", str(world), "--steps",
+           str(steps), "--warmup", "1", "--threads", str(threads)]
     res = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
     if res.returncode != 0:
         print(res.stderr[-2000:], file=sys.stderr, flush=True)
@@ -616,13 +622,16 @@ def main() -> int:
         )
         return 2
 
-    # ---- CPU baseline first (headline workload only): nothing has touched the GPU yet
+    # ---- CPU baseline first: nothing has touched the GPU yet
     cpu = None
-    if args.workload == "cfg1" and not args.no_cpu_baseline:
-        cores = max(W_CFG1, min(16, host_cores()))
-        threads = max(1, cores // W_CFG1)
+    if args.workload in CPU_BASELINE and not args.no_cpu_baseline:
+        world = CPU_BASELINE[args.workload][1]
+        cores = max(world, min(16, host_cores()))
+        threads = max(1, cores // world)
+        # about 10 s of CPU work: a GPT-2-medium step takes ~3x a GPT-2-124M one, the tiny GPT ~1%
+        steps = {"cfg0": args.cpu_steps * 10, "cfg1": args.cpu_steps, "cfg2": max(3, args.cpu_steps // 3)}
         t0 = time.perf_counter()
-        cpu = cpu_baseline(args.cpu_steps, threads)
+        cpu = cpu_baseline(args.workload, steps[args.workload], threads)
         print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
 
     if args.workload == "cfg3":
@@ -639,8 +648,8 @@ def main() -> int:
             "unit": "GB/s",
             "cores": cpu["cores"],
             "kind": "port",
-            "sample": f"{cpu['steps']} timed steps (+1 warmup) of the full cfg1 pipeline, reference op chain on "
-                      f"torch CPU + gloo, {W_CFG1} processes x {cpu['threads_per_rank']} threads; "
+            "sample": f"{cpu['steps']} timed steps (+1 warmup) of the full {args.workload} pipeline, reference op "
+                      f"chain on torch CPU + gloo, {cpu['world']} processes x {cpu['threads_per_rank']} threads; "
                       f"median {cpu['median_ms']:.1f} ms/step",
             "ms_per_step": round(cpu["median_ms"], 2),
             "speedup": round(cpu["median_ms"] / out["ms_per_step"], 1),

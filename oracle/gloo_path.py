@@ -16,7 +16,7 @@ fp32 gradients and run, per step, the reference's op sequence:
 Timing: ``perf_counter`` around the step bracketed by barriers, max over
 ranks.  Prints one JSON line.
 
-    python -m oracle.gloo_path --world 8 --steps 3 --warmup 1 --threads 2
+    python -m oracle.gloo_path --config gpt2-small --world 8 --steps 3 --warmup 1 --threads 2
 """
 
 from __future__ import annotations
@@ -127,15 +127,20 @@ def run(world: int, steps: int, warmup: int, threads: int, cfg: dict, cap_mb: fl
     }
 
 
+CONFIGS = {"tiny": wl.TINY_GPT, "gpt2-small": wl.GPT2_SMALL, "gpt2-medium": wl.GPT2_MEDIUM}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="gpt2-small", choices=sorted(CONFIGS))
     ap.add_argument("--world", type=int, default=8)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--threads", type=int, default=2)
     ap.add_argument("--layers", type=int, default=None)
     args = ap.parse_args()
-    print(json.dumps(run(args.world, args.steps, args.warmup, args.threads, wl.GPT2_SMALL, layers=args.layers)))
+    print(json.dumps(run(args.world, args.steps, args.warmup, args.threads, CONFIGS[args.config],
+                         layers=args.layers)))
 
 
 if __name__ == "__main__":
