@@ -184,3 +184,79 @@ def test_second_backward_accumulates_into_shard_grad():
         # is covered by the kernel tests; backward kernels need not be deterministic)
         rel = (p.grad - 2 * f).abs().max().item() / max((2 * f).abs().max().item(), 1.0)
         assert rel <= 1e-6
+
+
+def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1):
+    """FSDP on rank ``rank`` of a ResidentGroup next to a full-batch reference, both SGD.
+
+    Every step the emulated peers get what they would hold: their shard of the
+    current weights (as gathered, in ``param_dtype``) and the local gradients of a
+    replica holding those weights on their chunk of the batch."""
+    c = tiny_gpt.Config(n_layer=2)
+    ids, tgt = tiny_gpt.batch(c, 8, seed=99)
+    ref = tiny_gpt.GPT(c).to(DEV)
+    model = tiny_gpt.GPT(c).to(DEV)
+    names_by_id = {id(p): n for n, p in model.named_parameters()}
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy)
+    opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
+    opt_ref = torch.optim.SGD(ref.parameters(), lr=lr)
+    out = []
+    for _ in range(steps):
+        cur = {n: p.detach().clone() for n, p in ref.named_parameters()}
+        for unit in fsdp._units:
+            flat = torch.cat([cur[names_by_id[id(p)]].reshape(-1) for p in unit.params])
+            flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
+            S, shards = unit.shard_numel, unit.peer_param_shards()
+            for r in range(W):
+                if r != rank:
+                    shards[r].copy_(flat[r * S : (r + 1) * S].to(shards.dtype))
+        replica = []
+        for r in range(W):
+            if r == rank:
+                replica.append({})
+                continue
+            m = tiny_gpt.GPT(c).to(DEV)
+            with torch.no_grad():
+                for n, p in m.named_parameters():
+                    p.copy_(cur[n].to(param_dtype).float())
+            m = m.to(param_dtype)
+            _, l_r = m(ids.chunk(W)[r].to(DEV), tgt.chunk(W)[r].to(DEV))
+            l_r.backward()
+            replica.append({n: p.grad.detach().clone() for n, p in m.named_parameters()})
+        _stage(fsdp, names_by_id, replica, rank, W)
+        _, loss = fsdp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        _, lref = ref(ids.to(DEV), tgt.to(DEV))
+        lref.backward()
+        opt_ref.step()
+        opt_ref.zero_grad(set_to_none=True)
+        out.append((loss.item(), lref.item()))
+    return fsdp, ref, names_by_id, out
+
+
+@pytest.mark.parametrize("W,rank", [(2, 1), (4, 2)])
+def test_sgd_steps_track_full_batch(W, rank):
+    """Reference tests/test_fsdp.py:92-127: after 4 SGD steps this rank's shard equals its slice of
+    the full-batch model's weights (the reference compares with DDP; both equal the full batch)."""
+    fsdp, ref, names_by_id, _ = _sgd_run(W, rank, torch.float32)
+    final = {n: p.detach() for n, p in ref.named_parameters()}
+    for unit in fsdp._units:
+        flat = torch.cat([final[names_by_id[id(p)]].reshape(-1) for p in unit.params])
+        flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
+        S = unit.shard_numel
+        want = flat[rank * S : (rank + 1) * S]
+        rel = (unit.flat_shard.detach() - want).abs().max().item() / max(want.abs().max().item(), 1.0)
+        assert rel <= 1e-5, f"unit {unit.name}: {rel:.3e}"
+
+
+def test_bf16_params_track_fp32_training():
+    """Reference tests/test_fsdp.py:189-211: bf16 gathered parameters with fp32 reduction keep the
+    loss within 0.05 of fp32 training, and the master shard stays fp32."""
+    fsdp, _, _, bf16 = _sgd_run(2, 0, torch.bfloat16)
+    _, _, _, fp32 = _sgd_run(2, 0, torch.float32)
+    for (mine, _), (want, _) in zip(bf16, fp32, strict=True):  # this rank's loss on its chunk, both runs
+        assert abs(mine - want) <= 0.05
+    assert all(u.flat_shard.dtype == torch.float32 for u in fsdp._units)
