@@ -354,3 +354,16 @@ def test_planned_launch_rejects_bad_plans_before_launch():
     assert L.mdx_plan_spans(spans.ctypes.data, 1, 0, 0, junk.ctypes.data, ctypes.byref(size)) == 0
     assert L.mdx_unpack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, None, None) == -1  # unpack needs sources
     assert L.mdx_allreduce_unpack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, None, None) == -1  # wrong kind
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits (code 2) with a message that says so,
+    before anything touches a GPU."""
+    import subprocess
+    import sys
+
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120)
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr or "single" in res.stderr
+    assert res.stdout.strip() == ""
