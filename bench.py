@@ -202,11 +202,41 @@ def bench_ddp(name: str, args) -> dict:
     # around it: the events then come from a separate pass of eager steps.
     ResidentGroup.all_reduce_unpack_planned = timed_all_reduce
 
+    def timed_sum(bufs):
+        """--staged: the W-way sum dispatch, with HIP events like the fused reduction's."""
+        if not timing["on"]:
+            return group.all_reduce_sum(bufs)
+        s = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        group.all_reduce_sum(bufs)
+        e1.record(s)
+        red_events.append((e0, e1))
+
     def step() -> bool:
         ddp.finish_gradient_sync()
         found = scaler.unscale_(opt)
         scaler.update()
         return found
+
+    if args.staged:
+        # The reference's three stages as separate dispatches over the same data: pack (x 1/W) into the
+        # buckets, the W-way sum written back into this rank's buckets (one mdx_allreduce_sum), then
+        # unpack from the buckets into the gradients with the scaler's unscale + found-inf.
+        if cfg["reduce_dtype"] is not None:
+            raise SystemExit("--staged covers the same-dtype workloads (cfg0, cfg1, cfg2)")
+        plan = ddp._plan(0, len(ddp._buckets))
+        bucket_bufs = [b.buffer for b in ddp._buckets]
+
+        def step() -> bool:  # noqa: F811 - the staged variant of the step above
+            plan.refresh()
+            plan.pack(1.0 / W)
+            inv_scale, flag = scaler._begin_fused_unscale(dev, plan.param_ids)
+            timed_sum(bucket_bufs)
+            plan.unpack(inv_scale, flag)
+            found = scaler.unscale_(opt)
+            scaler.update()
+            return found
 
     steps = args.steps if name != "cfg4" else min(args.steps, 20)
     for _ in range(args.warmup):
@@ -248,11 +278,15 @@ def bench_ddp(name: str, args) -> dict:
     red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
     red_avg_ms = sum(red_ms) / len(red_ms)
     red_bytes = N * (W * s_w + s_b + s_g)
-    red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
     kname = ("allreduce_wide_kernel_dev<bf16, float, bf16, 8>" if b0.widening
              else f"allreduce_unpack_kernel_dev<float, float, {W}>")
+    if args.staged:
+        red_bytes = N * (W + 1) * s_b  # W buckets read, the sum written
+        hbm_bytes = N * (s_g + s_b) + red_bytes + N * (s_b + s_g)
+        kname = f"allreduce_kernel<float, float, {W}, false> (mdx_allreduce_sum)"
+    red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
 
-    traffic = measured_traffic(name)
+    traffic = None if args.staged else measured_traffic(name)
 
     return {
         "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",
@@ -280,10 +314,13 @@ def bench_ddp(name: str, args) -> dict:
             "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
             "found_inf": bool(found_any),
             "launch": "hip graph replay (capture_graphs=True)" if args.graphs else "eager dispatches",
+            "pipeline": "staged: pack, W-way sum, unpack (three dispatches)" if args.staged
+                        else "pack + fused W-way sum / unpack / unscale (two dispatches)",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{kname} (mdx_allreduce_unpack_planned, all {len(ddp._buckets)} buckets in one dispatch)",
+            "kernel": kname if args.staged else
+                      f"{kname} (mdx_allreduce_unpack_planned, all {len(ddp._buckets)} buckets in one dispatch)",
             "achieved": round(red_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -603,6 +640,9 @@ def main() -> int:
     ap.add_argument("--overlap-modes", default="compute,serial,overlap",
                     help="cfg1-overlap modes to run (all three for the JSON line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--staged", action="store_true",
+                    help="DDP workloads: time the reference's staged pipeline (pack, W-way sum, unpack as three "
+                         "dispatches) instead of the fused one, for comparison")
     ap.add_argument("--graphs", action="store_true",
                     help="DDP workloads: replay each step's launches from a captured HIP graph (capture_graphs=True)")
     ap.add_argument("--cpu-steps", type=int, default=20)
