@@ -147,9 +147,11 @@ int run_copy(const mdx_span* spans, int n_spans, int sdt, int ddt, const CopyPar
              hipStream_t stream) {
   SpanBatch b;
   memset(&b, 0, sizeof(b));
+  CopyParams p = params;  // a requested flag clear rides on the first dispatch only
   auto flush = [&]() -> int {
     if (b.count == 0) return MDX_OK;
-    const int rc = status(launch_copy(sdt, ddt, b, params, stream));
+    const int rc = status(launch_copy(sdt, ddt, b, p, stream));
+    p.clear = nullptr;
     memset(&b, 0, sizeof(b));
     return rc;
   };
@@ -163,7 +165,11 @@ int run_copy(const mdx_span* spans, int n_spans, int sdt, int ddt, const CopyPar
     b.count = k + 1;
     return b.count == kRunsPerLaunch ? flush() : MDX_OK;
   });
-  return rc != MDX_OK ? rc : flush();
+  if (rc != MDX_OK) return rc;
+  const int frc = flush();
+  if (frc != MDX_OK) return frc;
+  // nothing was launched: the clear still has to happen, in stream order
+  return p.clear != nullptr ? status(launch_clear_flag(p.clear, stream)) : MDX_OK;
 }
 
 // Appends a run to a piece batch; `flush` launches and clears a full batch.
@@ -441,13 +447,13 @@ const char* mdx_strerror(int code) {
 }
 
 int mdx_pack(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, float scale,
-             int divide, void* stream) {
+             int divide, int32_t* clear_flag, void* stream) {
   if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype)) return MDX_EDTYPE;
   int rc = check_spans(spans, n_spans, false);
   if (rc != MDX_OK) return rc;
   int32_t flags = 0;
   if (scale != 1.0f) flags = divide ? kCopyDivide : kCopyScale;
-  CopyParams p{scale, flags, nullptr};
+  CopyParams p{scale, flags, nullptr, clear_flag};
   return run_copy(spans, n_spans, src_dtype, dst_dtype, p, false, static_cast<hipStream_t>(stream));
 }
 
@@ -457,7 +463,7 @@ int mdx_unpack(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype,
   int rc = check_spans(spans, n_spans, true);
   if (rc != MDX_OK) return rc;
   CopyParams p{inv_scale, (inv_scale != 1.0f ? kCopyScale : 0) | (found_inf ? kCopyCheck : 0),
-               found_inf};
+               found_inf, nullptr};
   return run_copy(spans, n_spans, src_dtype, dst_dtype, p, false, static_cast<hipStream_t>(stream));
 }
 
@@ -467,7 +473,7 @@ int mdx_unscale_found_inf(const mdx_span* spans, int n_spans, int dtype, float i
   int rc = check_spans(spans, n_spans, false);
   if (rc != MDX_OK) return rc;
   CopyParams p{inv_scale, (inv_scale != 1.0f ? kCopyScale : 0) | (found_inf ? kCopyCheck : 0),
-               found_inf};
+               found_inf, nullptr};
   return run_copy(spans, n_spans, dtype, dtype, p, true, static_cast<hipStream_t>(stream));
 }
 
@@ -475,7 +481,7 @@ int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stre
   if (numel < 0 || (numel > 0 && (src == nullptr || dst == nullptr))) return MDX_EINVAL;
   if (any_overlap(src, numel * 4, dst, numel * 2)) return MDX_EALIAS;
   mdx_span sp{src, dst, numel};
-  CopyParams p{1.0f, 0, nullptr};
+  CopyParams p{1.0f, 0, nullptr, nullptr};
   return run_copy(&sp, 1, MDX_F32, MDX_BF16, p, false, static_cast<hipStream_t>(stream));
 }
 
@@ -676,15 +682,18 @@ int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int world, int w
                         plan_bytes);
 }
 
-int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream) {
+int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, int32_t* clear_flag,
+                     void* stream) {
   const PlanHeader* h;
   DevTable t;
   const int rc = plan_view(plan, d_plan, kPlanSpans, &h, &t);
   if (rc != MDX_OK) return rc;
-  if (h->count == 0) return MDX_OK;
+  if (h->count == 0) {
+    return clear_flag != nullptr ? status(launch_clear_flag(clear_flag, static_cast<hipStream_t>(stream))) : MDX_OK;
+  }
   int32_t flags = 0;
   if (scale != 1.0f) flags = divide ? kCopyDivide : kCopyScale;
-  CopyParams p{scale, flags, nullptr};
+  CopyParams p{scale, flags, nullptr, clear_flag};
   return status(launch_copy_dev(h->dtype_a, h->dtype_b, t, h->blocks, p, static_cast<hipStream_t>(stream)));
 }
 
@@ -696,7 +705,7 @@ int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_scale, in
   if (rc != MDX_OK) return rc;
   if (h->reserved) return MDX_EINVAL;  // unpack needs a source for every span
   if (h->count == 0) return MDX_OK;
-  CopyParams p{inv_scale, (inv_scale != 1.0f ? kCopyScale : 0) | (found_inf ? kCopyCheck : 0), found_inf};
+  CopyParams p{inv_scale, (inv_scale != 1.0f ? kCopyScale : 0) | (found_inf ? kCopyCheck : 0), found_inf, nullptr};
   return status(launch_copy_dev(h->dtype_a, h->dtype_b, t, h->blocks, p, static_cast<hipStream_t>(stream)));
 }
 

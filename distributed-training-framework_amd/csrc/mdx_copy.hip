@@ -56,6 +56,9 @@ __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) 
   const bool zero_src = (src == nullptr);
   const CopyOp<S, D, SCALE, CHECK> op{p.scale};
   bool bad = false;
+  // The scaler's per-step flag clear rides on the pack: one lane of the first
+  // workgroup (a per-lane store under the lane predicate).
+  if (p.clear != nullptr && blk == 0 && t == 0) *p.clear = 0;
 
   if (h >= 0) {
     const int64_t nvec = (n - h) / E;
@@ -164,7 +167,16 @@ hipError_t launch_any(int src_dtype, int dst_dtype, const L& l, const CopyParams
   return launch_typed<bf16, bf16>(l, p, stream);
 }
 
+__global__ void __launch_bounds__(kBlock) clear_flag_kernel(int32_t* flag) {
+  if (threadIdx.x == 0) *flag = 0;
+}
+
 }  // namespace
+
+hipError_t launch_clear_flag(int32_t* flag, hipStream_t stream) {
+  hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(kBlock), 0, stream, flag);
+  return hipGetLastError();
+}
 
 int copy_frag_elems(int src_dtype, int dst_dtype) {
   (void)src_dtype;

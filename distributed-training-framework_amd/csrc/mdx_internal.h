@@ -205,6 +205,7 @@ struct CopyParams {
   float scale;
   int32_t flags;
   int32_t* found_inf;
+  int32_t* clear;  // set to 0 by the dispatch's first lane (the scaler's per-step flag clear), or NULL
 };
 
 // Fragments.  A fragment is one 16-byte vector of the widest type a kernel
@@ -225,6 +226,7 @@ constexpr int kHeadRange = 8;
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
                        hipStream_t stream);
+hipError_t launch_clear_flag(int32_t* flag, hipStream_t stream);
 int copy_frag_elems(int src_dtype, int dst_dtype);
 
 // ----------------------------------------------------------------------------

@@ -24,12 +24,12 @@ LIB_PATH = Path(__file__).resolve().parent / "libmdx.so"
 MDX_F32 = 0
 MDX_BF16 = 1
 MDX_MAX_WORLD = 16
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
-    "mdx_pack": (_i32, [_vp, _i32, _i32, _i32, _f32, _i32, _vp]),
+    "mdx_pack": (_i32, [_vp, _i32, _i32, _i32, _f32, _i32, _vp, _vp]),
     "mdx_unpack": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _vp]),
     "mdx_unscale_found_inf": (_i32, [_vp, _i32, _i32, _f32, _vp, _vp]),
     "mdx_allreduce_sum": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
@@ -45,7 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_plan_allreduce_unpack_wide": (
         _i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
     ),
-    "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp]),
+    "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp, _vp]),
     "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_strerror": (ctypes.c_char_p, [_i32]),
@@ -153,8 +153,11 @@ def _ptrs(values: list[int]) -> ctypes.Array:
 # ---------------------------------------------------------------------------
 
 
-def pack(spans: np.ndarray, src_dtype: int, dst_dtype: int, scale: float, divide: bool, stream: int) -> None:
-    rc = lib().mdx_pack(_ptr(spans), len(spans), src_dtype, dst_dtype, scale, int(divide), stream)
+def pack(
+    spans: np.ndarray, src_dtype: int, dst_dtype: int, scale: float, divide: bool, stream: int,
+    clear_flag: int | None = None,
+) -> None:
+    rc = lib().mdx_pack(_ptr(spans), len(spans), src_dtype, dst_dtype, scale, int(divide), clear_flag, stream)
     check(rc, "mdx_pack")
 
 
@@ -295,8 +298,9 @@ def plan_allreduce_unpack_wide(
     )
 
 
-def pack_planned(plan: Plan, scale: float, divide: bool, stream: int) -> None:
-    check(lib().mdx_pack_planned(plan.host_ptr, plan.device_ptr, scale, int(divide), stream), "mdx_pack_planned")
+def pack_planned(plan: Plan, scale: float, divide: bool, stream: int, clear_flag: int | None = None) -> None:
+    rc = lib().mdx_pack_planned(plan.host_ptr, plan.device_ptr, scale, int(divide), clear_flag, stream)
+    check(rc, "mdx_pack_planned")
 
 
 def unpack_planned(plan: Plan, inv_scale: float, found_inf: int | None, stream: int) -> None:

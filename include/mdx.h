@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 2
+#define MDX_ABI_VERSION 3
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -87,9 +87,14 @@ typedef struct mdx_piece {
  * `buf[off:off+n].copy_(p.grad.reshape(-1))` then `buf.div_(W)`
  * (minidist/fsdp.py:218-227), with scale = W and divide = 1.
  * dst[i] = rnd_dst(rnd_dst(src[i]) * scale), or ... / scale when divide != 0;
- * the scaling is skipped when scale == 1.  All spans of one call share dtypes. */
+ * the scaling is skipped when scale == 1.  All spans of one call share dtypes.
+ * `clear_flag` (may be NULL): a found-inf flag (int32, device memory) that the
+ * call also sets to 0, ordered on `stream` like the copy -- the scaler's
+ * once-per-step clear (minidist/amp.py:206 `found_inf = zeros(1)`) folded into
+ * the pack that precedes the reduction which sets it, instead of a dispatch of
+ * its own.  It is cleared even when there is nothing to copy. */
 MDX_API int mdx_pack(const mdx_span* spans, int n_spans, int src_dtype, int dst_dtype, float scale,
-             int divide, void* stream);
+                     int divide, int32_t* clear_flag, void* stream);
 
 /* Unpack, with the loss-scaler's unscale + found-inf fused as an epilogue.
  * Replaces _Bucket.scatter_from_buffer (minidist/ddp.py:94-102):
@@ -230,7 +235,8 @@ MDX_API int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int worl
                                            int grad_dtype, float prescale, void* plan, int64_t* plan_bytes);
 
 /* mdx_pack over a plan: one dispatch.  `plan` = host copy, `d_plan` = device copy. */
-MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, void* stream);
+MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, int32_t* clear_flag,
+                             void* stream);
 
 /* mdx_unpack over a plan whose every span has a source: one dispatch. */
 MDX_API int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,

@@ -178,11 +178,12 @@ def test_comm_stream_carries_every_launch(monkeypatch):
     from minidist import _native
 
     seen = []
-    for name in ("pack", "pack_planned", "allreduce_unpack", "allreduce_unpack_planned"):
+    # position of the stream argument in each entry point's Python binding
+    for name, at in (("pack", 5), ("pack_planned", 3), ("allreduce_unpack", 7), ("allreduce_unpack_planned", 3)):
         orig = getattr(_native, name)
 
-        def spy(*a, _orig=orig, _name=name):
-            seen.append((_name, a[-1]))
+        def spy(*a, _orig=orig, _name=name, _at=at):
+            seen.append((_name, a[_at]))
             return _orig(*a)
 
         monkeypatch.setattr(_native, name, spy)

@@ -67,22 +67,22 @@ def test_argument_checks_happen_before_any_launch():
     L = nat.lib()
     P = ctypes.c_void_p
     # dtype
-    assert L.mdx_pack(None, 0, 9, 0, 1.0, 0, None) == -2
+    assert L.mdx_pack(None, 0, 9, 0, 1.0, 0, None, None) == -2
     assert L.mdx_unpack(None, 0, 0, 5, 1.0, None, None) == -2
     assert L.mdx_unscale_found_inf(None, 0, 3, 1.0, None, None) == -2
     # counts and NULLs
-    assert L.mdx_pack(None, -1, 0, 0, 1.0, 0, None) == -1
-    assert L.mdx_pack(None, 3, 0, 0, 1.0, 0, None) == -1
+    assert L.mdx_pack(None, -1, 0, 0, 1.0, 0, None, None) == -1
+    assert L.mdx_pack(None, 3, 0, 0, 1.0, 0, None, None) == -1
     s = _span(0, 0, 10)  # dst NULL with numel > 0
-    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None) == -1
+    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None, None) == -1
     s = _span(0, 4096, 10)  # unpack needs a source
     assert L.mdx_unpack(s.ctypes.data, 1, 0, 0, 1.0, None, None) == -1
     s = _span(0, 4096, -1)
-    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None) == -1
+    assert L.mdx_pack(s.ctypes.data, 1, 0, 0, 1.0, 0, None, None) == -1
     assert L.mdx_cast_f32_bf16(None, None, -1, None) == -1
     assert L.mdx_cast_f32_bf16(P(4096), P(4096 + 8), 16, None) == -4  # overlapping cast
     # zero-length work is a no-op that succeeds without a device
-    assert L.mdx_pack(None, 0, 0, 0, 1.0, 0, None) == 0
+    assert L.mdx_pack(None, 0, 0, 0, 1.0, 0, None, None) == 0
     assert L.mdx_cast_f32_bf16(None, None, 0, None) == 0
     # world / rank
     reps = (ctypes.c_void_p * 2)(4096, 8192)
@@ -347,8 +347,8 @@ def test_plan_allreduce_unpack_builds_and_rejects_overlap():
 def test_planned_launch_rejects_bad_plans_before_launch():
     L = nat.lib()
     junk = np.zeros(64, dtype=np.uint64)
-    assert L.mdx_pack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, 0, None) == -1  # no magic
-    assert L.mdx_pack_planned(None, None, 1.0, 0, None) == -1
+    assert L.mdx_pack_planned(junk.ctypes.data, junk.ctypes.data, 1.0, 0, None, None) == -1  # no magic
+    assert L.mdx_pack_planned(None, None, 1.0, 0, None, None) == -1
     spans = nat.spans_array([(0, 0x40000000, 64)])  # a zero-source span
     size = ctypes.c_int64(junk.nbytes)
     assert L.mdx_plan_spans(spans.ctypes.data, 1, 0, 0, junk.ctypes.data, ctypes.byref(size)) == 0

@@ -616,3 +616,30 @@ def test_golden_widening_replay():
         for i, g in grads:
             assert same_bits(to_host(g), d[f"unscaled_p{i}"]), f"param {i}"
     assert bool(flag.item()) == bool(d["found_inf"])
+
+
+@pytest.mark.parametrize("n_spans", [0, 3, 150])
+@pytest.mark.parametrize("planned", [False, True])
+def test_pack_clears_the_flag(rng, n_spans, planned):
+    """clear_flag: the pack also sets the found-inf flag to 0 in stream order -- with nothing to
+    copy, over several kernel-argument batches, or through a plan -- and copies exactly as without it."""
+    sizes = [int(x) for x in rng.integers(1, 700, n_spans)]
+    srcs = [to_dev(values(rng, n, o.F32)) for n in sizes]
+    dst = empty_dev(sum(sizes) + 1, o.F32)
+    rows, off = [], 0
+    for s, n in zip(srcs, sizes, strict=True):
+        rows.append((s.data_ptr(), dst.data_ptr() + off * 4, n))
+        off += n
+    flag = torch.ones(1, dtype=torch.int32, device=DEV)
+    other = torch.ones(1, dtype=torch.int32, device=DEV)
+    if planned and n_spans:
+        plan = nat.plan_spans(nat.spans_array(rows), 0, 0, DEV)
+        nat.pack_planned(plan, nat.f32(0.25), False, stream(), flag.data_ptr())
+    else:
+        nat.pack(nat.spans_array(rows), 0, 0, nat.f32(0.25), False, stream(), flag.data_ptr())
+    assert flag.item() == 0 and other.item() == 1
+    got, off = to_host(dst), 0
+    for s, n in zip(srcs, sizes, strict=True):
+        assert same_bits(got[off : off + n], o.mul_scalar(to_host(s), o.F32, 0.25))
+        off += n
+    assert same_bits(got[off:], np.full(len(got) - off, SENTINEL_F32, dtype=np.float32))
