@@ -1,0 +1,127 @@
+"""Seeded random DDP pipelines on the GPU, bit for bit against the oracle.
+
+Each case draws its own configuration: gradient dtype (fp32 or bf16, and for
+bf16 optionally fp32 buckets, the widening path), W in [2, 16], the rank,
+20-40 parameters of ragged shapes, a bucket cap between one bucket per
+parameter and a single bucket, gradients that are views at odd element
+offsets of a larger buffer (so that no pointer need be 16-byte aligned),
+parameters without a gradient, special values (+-inf, NaN, subnormals) in
+some peers' gradients, and with or without the fused scaler.  The whole
+pipeline runs through the Python API (DistributedDataParallel over a
+ResidentGroup, DistributedGradScaler) and is compared with
+oracle.ddp_pipeline: every gradient, every bucket, the found-inf decision.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from conftest import first_mismatch, same_bits
+from minidist import DDP, DistributedGradScaler, ResidentGroup
+from oracle import gradpath as o
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+SPECIALS = np.array([np.inf, -np.inf, np.nan, 1e-45, -1e-40, 0.0, -0.0], dtype=np.float32)
+
+
+def host_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().reshape(-1)
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().astype(np.uint16)
+    return t.numpy().copy()
+
+
+def dev_view(a: np.ndarray, shape, offset: int) -> torch.Tensor:
+    """``a`` on the GPU as a view ``offset`` elements into a larger buffer."""
+    n = a.size
+    if a.dtype == np.uint16:
+        buf = torch.zeros(n + offset + 8, dtype=torch.int16, device=DEV)
+        buf[offset : offset + n].copy_(torch.from_numpy(a.view(np.int16).copy()))
+        return buf.view(torch.bfloat16)[offset : offset + n].view(shape)
+    buf = torch.zeros(n + offset + 8, dtype=torch.float32, device=DEV)
+    buf[offset : offset + n].copy_(torch.from_numpy(a.copy()))
+    return buf[offset : offset + n].view(shape)
+
+
+def dev_from(a: np.ndarray) -> torch.Tensor:
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    return torch.from_numpy(a.copy()).to(DEV)
+
+
+class Flat(nn.Module):
+    def __init__(self, shapes, dtype):
+        super().__init__()
+        self.ps = nn.ParameterList([nn.Parameter(torch.zeros(s, dtype=dtype, device=DEV)) for s in shapes])
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_pipeline_matches_oracle(seed):
+    rng = np.random.default_rng(9000 + seed)
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    widening = dtype == torch.bfloat16 and rng.random() < 0.5
+    gdt = o.BF16 if dtype == torch.bfloat16 else o.F32
+    W = int(rng.integers(2, 17))
+    rank = int(rng.integers(0, W))
+    n_params = int(rng.integers(20, 41))
+    shapes = [(int(rng.integers(1, 3000)),) if rng.random() < 0.7 else (int(rng.integers(1, 60)), int(rng.integers(1, 40)))
+              for _ in range(n_params)]
+    numels = [int(np.prod(s)) for s in shapes]
+    total_mb = sum(numels) * (2 if dtype == torch.bfloat16 else 4) / 2**20
+    cap = float(rng.choice([1e-6, total_mb / 7, total_mb / 3, 1e6]))
+    use_scaler = rng.random() < 0.6
+    scale = 2.0 ** int(rng.integers(0, 14)) if use_scaler else 1.0
+
+    grads = []
+    for r in range(W):
+        row = []
+        for n in numels:
+            g = (rng.standard_normal(n) * 1e-3 * scale).astype(np.float32)
+            if rng.random() < 0.05:  # a rare special value in this gradient
+                g[int(rng.integers(0, n))] = SPECIALS[int(rng.integers(0, len(SPECIALS)))]
+            row.append(o.from_f32(g, gdt))
+        grads.append(row)
+    for i in rng.integers(0, n_params, int(rng.integers(0, 3))):  # gradients this rank never received
+        grads[rank][int(i)] = None
+
+    model = Flat(shapes, dtype)
+    scaler = DistributedGradScaler(init_scale=scale) if use_scaler else None
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, grad_scaler=scaler,
+              reduce_dtype=torch.float32 if widening else None)
+    params = list(model.parameters())
+    index = {id(p): i for i, p in enumerate(params)}
+    for b, bucket in enumerate(ddp._buckets):
+        idxs = [index[id(p)] for p in bucket.params]
+        rows = ddp.bucket_replicas(b)
+        wire_dtype, prescaled = ddp.bucket_wire_format(b)
+        wdt = o.BF16 if wire_dtype == torch.bfloat16 else o.F32
+        for r in range(W):
+            if r != rank:
+                packed = o.pack([grads[r][i] for i in idxs], [gdt] * len(idxs), [numels[i] for i in idxs], wdt,
+                                1.0 / W if prescaled else 1.0)
+                rows[r].copy_(dev_from(packed))
+    for p, g in zip(params, grads[rank], strict=True):
+        p.grad = None if g is None else dev_view(g, p.shape, int(rng.integers(0, 9)))
+    ddp.finish_gradient_sync()
+    found = None
+    if scaler is not None:
+
+        class _Opt:
+            param_groups = [{"params": params}]
+
+        found = scaler.unscale_(_Opt())
+
+    want = o.ddp_pipeline(grads, [gdt] * n_params, numels, cap, rank, 1.0 / scale if use_scaler else None,
+                          bucket_dtype=o.F32 if widening else None)
+    case = f"seed {seed}: {dtype} widening={widening} W={W} rank={rank} cap={cap:.3g} scale={scale:g}"
+    for i, p in enumerate(params):
+        got = host_bits(p.grad)
+        assert same_bits(got, want["grads"][i]), f"{case} param {i}: {first_mismatch(got, want['grads'][i])}"
+    for b, bucket in enumerate(ddp._buckets):
+        assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"{case} bucket {b}"
+    if scaler is not None:
+        assert found == want["found_inf"], case
