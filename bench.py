@@ -312,6 +312,9 @@ def bench_ddp(name: str, args) -> dict:
             "hbm_bytes_per_step": hbm_bytes,
             "hbm_gbs": round(hbm_bytes / (ms_per_step * 1e-3) / 1e9, 2),
             "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            # a full 25 MiB bucket's share of the measured step (one bucket alone would sit in the
+            # 256 MB Infinity Cache, so it is not timed on its own)
+            "us_per_25MiB_bucket": round(ms_per_step * 1e3 * (25 * 2**20 // b0.buffer.element_size()) / N, 2),
             "found_inf": bool(found_any),
             "launch": "hip graph replay (capture_graphs=True)" if args.graphs else "eager dispatches",
             "pipeline": "staged: pack, W-way sum, unpack (three dispatches)" if args.staged
