@@ -203,20 +203,23 @@ def test_cfg0_tiny_gpt_every_element_vs_oracle(rank):
 # ---------------------------------------------------------------------------
 
 
-def _cfg1(rank: int, seed: int):
+def _cfg1(rank: int, seed: int, **ddp_options):
     specs = wl.gpt_specs(**wl.GPT2_SMALL)
     W, S = 8, 2.0**16
     model = wl.SpecModule(specs, DEV)
     scaler = DistributedGradScaler(init_scale=S)
-    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=25.0, grad_scaler=scaler)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=25.0, grad_scaler=scaler,
+              **ddp_options)
     gen = torch.Generator(device=DEV).manual_seed(seed)
     _stage_gpu(ddp, W, rank, gen, 1e-3 * S)
     return model, scaler, ddp, W, S
 
 
-@pytest.mark.parametrize("rank", [0, 6])
-def test_cfg1_gpt2_small_full_size(rank):
-    model, scaler, ddp, W, S = _cfg1(rank, 1234 + rank)
+@pytest.mark.parametrize("rank,options", [(0, {}), (6, {}), (3, {"comm_stream": True}), (5, {"capture_graphs": True})])
+def test_cfg1_gpt2_small_full_size(rank, options):
+    """Full size, the default launch path and, on other ranks, the dedicated communication
+    stream and the graph-captured launch."""
+    model, scaler, ddp, W, S = _cfg1(rank, 1234 + rank, **options)
     assert len(ddp._buckets) == 18 and sum(p.numel() for p in model.parameters()) == 124_439_808
     rng = np.random.default_rng(rank)
     before = _sample_before(ddp, rng)
