@@ -15,6 +15,9 @@ large configurations use three checks that do not depend on size:
 
 Inputs follow the configurations' recipes (seeded ``randn`` times the stated
 scales); the large ones are generated on the GPU.
+
+The last section takes the path to its size limits with the same checks: a
+bucket and an FSDP unit whose element offsets pass 2^31 (4-16 GB buffers).
 """
 
 from __future__ import annotations
@@ -404,3 +407,125 @@ def test_cfg4_llama7b_bf16_widening_full_size():
     assert found is False
     _oracle_sample(ddp, W, rank, 1.0 / S, before)
     _check_chain(ddp, W, rank, 1.0 / S, own)
+
+
+# ---------------------------------------------------------------------------
+# Maximum sizes: element offsets past 2^31 in a bucket and in an FSDP unit
+# ---------------------------------------------------------------------------
+
+
+class _BigAndSmall(torch.nn.Module):
+    """Registered small first, so the reverse-order bucket holds the big gradient at offset 0
+    and the small one at offset n_big (past 2^31)."""
+
+    def __init__(self, n_big: int, n_small: int, dtype: torch.dtype):
+        super().__init__()
+        self.small = torch.nn.Parameter(torch.zeros(n_small, dtype=dtype, device=DEV))
+        self.big = torch.nn.Parameter(torch.zeros(n_big, dtype=dtype, device=DEV))
+
+
+@pytest.mark.parametrize("widening", [False, True])
+def test_bucket_offsets_beyond_2_31_elements(widening):
+    """One bucket of 2^31 + 4104 elements (bf16 grads; bf16 or fp32 bucket), W = 2, fused unscale.
+    The big gradient is cut into runs on the host; the small one starts 2^31 + 5 elements in."""
+    n_big, n_small = 2**31 + 5, 4099
+    W, rank, S = 2, 1, 2.0**10
+    model = _BigAndSmall(n_big, n_small, torch.bfloat16)
+    scaler = DistributedGradScaler(init_scale=S)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=1e6, grad_scaler=scaler,
+              reduce_dtype=torch.float32 if widening else None)
+    assert len(ddp._buckets) == 1 and ddp._buckets[0].widening == widening
+    where = _bucket_map(ddp)
+    assert where[id(model.big)] == (0, 0) and where[id(model.small)] == (0, n_big)
+    gen = torch.Generator(device=DEV).manual_seed(31)
+    _stage_gpu(ddp, W, rank, gen, 1e-3 * S)
+    before = _sample_before(ddp, np.random.default_rng(12), per_param=256)
+    # and the big gradient's elements on either side of 2^31
+    idx, _ = before[id(model.big)]
+    idx = np.unique(np.concatenate([idx, np.arange(2**31 - 3, 2**31 + 3)]))
+    before[id(model.big)] = (idx, bits(model.big.grad[torch.from_numpy(idx).to(DEV)]))
+    own = _snapshot(ddp)
+    ddp.finish_gradient_sync()
+    assert scaler.unscale_(_Opt(model.parameters())) is False
+    _oracle_sample(ddp, W, rank, 1.0 / S, before)
+    _check_chain(ddp, W, rank, 1.0 / S, own)
+
+
+class _Shape:
+    def __init__(self, n: int):
+        self.shape = (n,)
+
+
+class _BigUnitRoot(torch.nn.Module):
+    def __init__(self, numels, seed):
+        super().__init__()
+        self.block = _Block([_Shape(n) for n in numels])
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        with torch.no_grad():
+            for p in self.block.parameters():
+                p.copy_(torch.randn(p.shape, device=DEV, generator=g) * 0.02)
+
+
+@pytest.mark.parametrize("rank", [6, 7])
+def test_fsdp_shard_offsets_beyond_2_31_elements(rank):
+    """One FSDP unit of 2,550,150,955 elements at W = 8 (S = 318,768,870): rank 6's shard crosses
+    element 2^31 and the big parameter's end, rank 7's starts past 2^31 and ends in the padding.
+    Gather cast and reduce-scatter share vs the torch op chain on every element and the oracle on a
+    sample."""
+    numels = [2**31 + 1001, 3 * 2**27 + 12345, 777]
+    W = 8
+    m = _BigUnitRoot(numels, seed=7)
+    master_full = torch.cat([p.detach().reshape(-1) for p in m.block.parameters()])
+    policy = MixedPrecisionPolicy(param_dtype=torch.bfloat16, reduce_dtype=torch.float32)
+    f = FSDP(m, unit_types=(_Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy)
+    unit = f._units[0]
+    T = sum(numels)
+    S, P = unit.shard_numel, unit.padded_numel
+    assert (unit.total_numel, S, P) == (T, -(-T // W), W * -(-T // W))
+    lo = rank * S
+    assert (lo < 2**31 < lo + S) if rank == 6 else (lo > 2**31 and lo + S > T)
+    rng = np.random.default_rng(rank)
+    sample = np.unique(np.concatenate([np.arange(4), np.arange(S - 4, S), rng.integers(0, S, 4096),
+                                       np.arange(-3, 3) + (2**31 - lo), np.arange(-3, 3) + (numels[0] - lo),
+                                       np.arange(-3, 3) + (T - lo)]))
+    sample = sample[(sample >= 0) & (sample < S)]
+    ts = torch.from_numpy(sample).to(DEV)
+
+    # gather cast: this rank's slot == RNE bf16 of the fp32 master shard
+    want_shard = torch.zeros(S, device=DEV)
+    n_real = max(0, min(S, T - lo))
+    want_shard[:n_real].copy_(master_full[lo : lo + n_real])
+    del master_full
+    assert same_gpu(unit.flat_shard, want_shard)
+    unit.unshard()
+    slot = unit._full[lo : lo + S]
+    assert same_gpu(slot, want_shard.to(torch.bfloat16))
+    got_cast = bits(slot[ts])
+    want_cast = o.fsdp_gather_cast(bits(want_shard[ts]), o.BF16)
+    assert same_bits(got_cast, want_cast), first_mismatch(got_cast, want_cast)
+    del want_shard
+
+    # reduce-scatter share: 8 full-size bf16 contributions summed in fp32 into the shard
+    gen = torch.Generator(device=DEV).manual_seed(200 + rank)
+    peers = unit.peer_grad_contributions()
+    for r in range(W):
+        if r != rank:
+            peers[r].copy_((torch.randn(P, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16))
+    own_full = torch.zeros(P, dtype=torch.bfloat16, device=DEV)
+    own_full[:T].copy_((torch.randn(T, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16))
+    off = 0
+    for p in unit.params:
+        p.grad = own_full[off : off + p.numel()].view(p.shape).clone()
+        off += p.numel()
+    unit.reduce_scatter_grads()
+    slices = [own_full[lo : lo + S] if r == rank else peers[r, lo : lo + S] for r in range(W)]
+    acc = None
+    for x in slices:  # fsdp.py:218-233 on this rank's slice: widen, div_(W), rank-ordered SUM
+        part = x.to(torch.float32).div_(W)
+        acc = part if acc is None else acc.add_(part)
+    got = unit.flat_shard.grad
+    assert same_gpu(got, acc)
+    parts = [o.div_scalar(o.convert(bits(x[ts]), o.BF16, o.F32), o.F32, W) for x in slices]
+    want = o.allreduce_sum(parts, o.F32)
+    assert same_bits(bits(got[ts]), want), first_mismatch(bits(got[ts]), want)
+    assert all(p.grad is None for p in unit.params)
