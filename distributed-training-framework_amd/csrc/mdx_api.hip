@@ -18,7 +18,7 @@
 namespace mdx {
 namespace {
 
-inline bool valid_dtype(int d) { return d == MDX_F32 || d == MDX_BF16; }
+inline bool valid_dtype(int d) { return d == MDX_F32 || d == MDX_BF16 || d == MDX_F16; }
 
 inline int status(hipError_t e) { return e == hipSuccess ? MDX_OK : int(e); }
 
@@ -334,7 +334,7 @@ struct FusedArgs {
 };
 
 // `dtype` is the contributions' dtype, `out_dtype` the bucket's (equal, or
-// bf16 -> fp32 for the widening variant).
+// bf16 / fp16 -> fp32 for the widening variant).
 int check_fused(const void* const* replicas, int world, int dtype, int out_dtype, const mdx_grad_run* runs,
                 int n_runs, void* out, int grad_dtype, FusedArgs* f) {
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype) || !valid_dtype(grad_dtype)) return MDX_EDTYPE;
@@ -382,8 +382,10 @@ int check_fused(const void* const* replicas, int world, int dtype, int out_dtype
   return MDX_OK;
 }
 
-// The widening variant exists for bf16 contributions into fp32 buckets.
-bool wide_dtypes(int dtype, int out_dtype) { return dtype == MDX_BF16 && out_dtype == MDX_F32; }
+// The widening variant exists for bf16 or fp16 contributions into fp32 buckets.
+bool wide_dtypes(int dtype, int out_dtype) {
+  return (dtype == MDX_BF16 || dtype == MDX_F16) && out_dtype == MDX_F32;
+}
 
 // Replays the fused runs as (piece, grad) runs.
 template <typename Emit>
@@ -436,7 +438,7 @@ const char* mdx_strerror(int code) {
   switch (code) {
     case MDX_OK: return "success";
     case MDX_EINVAL: return "mdx: invalid argument (NULL pointer, negative count or size, bad plan)";
-    case MDX_EDTYPE: return "mdx: unsupported dtype code (expected MDX_F32 or MDX_BF16)";
+    case MDX_EDTYPE: return "mdx: unsupported dtype code or combination (MDX_F32, MDX_BF16, MDX_F16)";
     case MDX_EWORLD: return "mdx: world size outside [1, MDX_MAX_WORLD] or rank outside [0, world)";
     case MDX_EALIAS: return "mdx: output overlaps an input it must not overlap";
     case MDX_ESIZE: return "mdx: plan buffer missing or too small (required size returned)";
@@ -575,7 +577,7 @@ int mdx_allreduce_unpack_wide(const void* const* replicas, int world, int wire_d
   memset(&b, 0, sizeof(b));
   auto flush = [&]() -> int {
     if (b.count == 0) return MDX_OK;
-    const int r = status(launch_allreduce_wide(grad_dtype, world, b, f.p, st));
+    const int r = status(launch_allreduce_wide(wire_dtype, grad_dtype, world, b, f.p, st));
     memset(&b, 0, sizeof(b));
     return r;
   };
@@ -728,7 +730,7 @@ int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv
   p.found_inf = found_inf;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (h->reduce_dtype != h->dtype_a) {
-    return status(launch_allreduce_wide_dev(h->dtype_b, h->world, t, h->blocks, p, st));
+    return status(launch_allreduce_wide_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p, st));
   }
   return status(launch_allreduce_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p, st));
 }

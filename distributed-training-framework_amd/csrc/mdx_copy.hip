@@ -159,12 +159,18 @@ hipError_t launch_typed(const L& l, const CopyParams& p, hipStream_t stream) {
   return check ? l.template go<S, D, kScaleNone, true>(p, stream) : l.template go<S, D, kScaleNone, false>(p, stream);
 }
 
+template <typename S, typename L>
+hipError_t launch_to(int dst_dtype, const L& l, const CopyParams& p, hipStream_t stream) {
+  if (dst_dtype == MDX_F32) return launch_typed<S, float>(l, p, stream);
+  if (dst_dtype == MDX_BF16) return launch_typed<S, bf16>(l, p, stream);
+  return launch_typed<S, f16>(l, p, stream);
+}
+
 template <typename L>
 hipError_t launch_any(int src_dtype, int dst_dtype, const L& l, const CopyParams& p, hipStream_t stream) {
-  if (src_dtype == MDX_F32 && dst_dtype == MDX_F32) return launch_typed<float, float>(l, p, stream);
-  if (src_dtype == MDX_F32 && dst_dtype == MDX_BF16) return launch_typed<float, bf16>(l, p, stream);
-  if (src_dtype == MDX_BF16 && dst_dtype == MDX_F32) return launch_typed<bf16, float>(l, p, stream);
-  return launch_typed<bf16, bf16>(l, p, stream);
+  if (src_dtype == MDX_F32) return launch_to<float>(dst_dtype, l, p, stream);
+  if (src_dtype == MDX_BF16) return launch_to<bf16>(dst_dtype, l, p, stream);
+  return launch_to<f16>(dst_dtype, l, p, stream);
 }
 
 __global__ void __launch_bounds__(kBlock) clear_flag_kernel(int32_t* flag) {

@@ -21,8 +21,12 @@ constexpr int kBlock = 64;  // one wave64 per workgroup (measured: beats 128, 25
 constexpr int kRunsPerLaunch = 48;        // runs per dispatch (kernarg budget)
 constexpr int64_t kMaxRunElems = int64_t(1) << 26;
 
-// bf16 storage type: raw bits, so that conversions are exact and explicit.
+// bf16 and fp16 storage types: raw bits, so that conversions are exact and
+// explicit.
 struct bf16 {
+  uint16_t u;
+};
+struct f16 {
   uint16_t u;
 };
 
@@ -36,11 +40,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(1))) u32x2 gu32x2;
 
 // ----------------------------------------------------------------------------
-// Element conversions (IEEE, round to nearest even, NaN -> 0xFFFF for bf16)
+// Element conversions (IEEE, round to nearest even; NaN -> 0xFFFF for bf16,
+// sign | 0x7E00 | mantissa >> 13 for fp16, as torch's CPU conversions)
 // ----------------------------------------------------------------------------
 
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(bf16 x) { return __uint_as_float(uint32_t(x.u) << 16); }
+// fp16 -> fp32 is exact (v_cvt_f32_f16; fp16 subnormals are kept).
+__device__ __forceinline__ float to_f32(f16 x) { return float(__builtin_bit_cast(_Float16, x.u)); }
 
 template <typename T>
 __device__ __forceinline__ T from_f32(float x);
@@ -62,6 +69,20 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float x) {
   return r;
 }
 
+// fp32 -> fp16: v_cvt_f16_f32 in the default mode (round to nearest even,
+// fp16 subnormals kept, overflow to +-inf); NaNs are rebuilt as torch does.
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float x) {
+  const uint32_t u = __float_as_uint(x);
+  f16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.u = uint16_t(((u >> 16) & 0x8000u) | 0x7e00u | ((u >> 13) & 0x3ffu));
+  } else {
+    r.u = __builtin_bit_cast(uint16_t, _Float16(x));
+  }
+  return r;
+}
+
 // `dst.copy_(src)` for one element: identity within a dtype (NaN payloads
 // untouched), one rounding across dtypes.
 template <typename S, typename D>
@@ -75,6 +96,7 @@ struct Cvt<T, T> {
 
 __device__ __forceinline__ bool is_finite(float x) { return __builtin_isfinite(x); }
 __device__ __forceinline__ bool is_finite(bf16 x) { return (x.u & 0x7f80u) != 0x7f80u; }
+__device__ __forceinline__ bool is_finite(f16 x) { return (x.u & 0x7c00u) != 0x7c00u; }
 
 template <typename T>
 __device__ __forceinline__ T zero_of() {
@@ -282,9 +304,9 @@ hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, c
 hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, const PieceBatch& b,
                         const ReduceParams& p, hipStream_t stream);
 int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world);
-// Widening fused all-reduce + unpack: bf16 contributions, fp32 bucket.
-hipError_t launch_allreduce_wide(int grad_dtype, int world, const PieceBatch& b, const ReduceParams& p,
-                                 hipStream_t stream);
+// Widening fused all-reduce + unpack: bf16 or fp16 contributions, fp32 bucket.
+hipError_t launch_allreduce_wide(int wire_dtype, int grad_dtype, int world, const PieceBatch& b,
+                                 const ReduceParams& p, hipStream_t stream);
 
 // ----------------------------------------------------------------------------
 // Work-table views.  A kernel body reads its runs through one of two views:
@@ -369,9 +391,9 @@ hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int 
                            hipStream_t stream);
 hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
                                 const ReduceParams& p, hipStream_t stream);
-hipError_t launch_allreduce_wide_dev(int grad_dtype, int world, const DevTable& t, int blocks,
+hipError_t launch_allreduce_wide_dev(int wire_dtype, int grad_dtype, int world, const DevTable& t, int blocks,
                                      const ReduceParams& p, hipStream_t stream);
 
-inline int dtype_size(int dt) { return dt == MDX_BF16 ? 2 : 4; }
+inline int dtype_size(int dt) { return dt == MDX_F32 ? 4 : 2; }
 
 }  // namespace mdx

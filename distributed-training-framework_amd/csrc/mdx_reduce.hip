@@ -7,25 +7,55 @@ hipError_t launch_allreduce_f32(int grad_dtype, bool unpack, int world, const Pi
                                 const ReduceParams& p, hipStream_t stream);
 hipError_t launch_allreduce_bf16(int grad_dtype, bool unpack, int world, const PieceBatch& b,
                                  const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_f16(int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                                const ReduceParams& p, hipStream_t stream);
 hipError_t launch_allreduce_dev_f32(int grad_dtype, int world, const DevTable& t, int blocks,
-                                   const ReduceParams& p, hipStream_t stream);
-hipError_t launch_allreduce_dev_bf16(int grad_dtype, int world, const DevTable& t, int blocks,
                                     const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_dev_bf16(int grad_dtype, int world, const DevTable& t, int blocks,
+                                     const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_dev_f16(int grad_dtype, int world, const DevTable& t, int blocks,
+                                    const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_wide_bf16(int grad_dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                                      hipStream_t stream);
+hipError_t launch_allreduce_wide_f16(int grad_dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                                     hipStream_t stream);
+hipError_t launch_allreduce_wide_dev_bf16(int grad_dtype, int world, const DevTable& t, int blocks,
+                                          const ReduceParams& p, hipStream_t stream);
+hipError_t launch_allreduce_wide_dev_f16(int grad_dtype, int world, const DevTable& t, int blocks,
+                                         const ReduceParams& p, hipStream_t stream);
 hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
                              hipStream_t stream);
-hipError_t launch_share_generic(int in_dtype, int acc_dtype, int out_dtype, const PieceBatch& b,
-                                const ReduceParams& p, hipStream_t stream);
+hipError_t launch_share_generic_f32(int acc_dtype, int out_dtype, const PieceBatch& b, const ReduceParams& p,
+                                    hipStream_t stream);
+hipError_t launch_share_generic_bf16(int acc_dtype, int out_dtype, const PieceBatch& b, const ReduceParams& p,
+                                     hipStream_t stream);
+hipError_t launch_share_generic_f16(int acc_dtype, int out_dtype, const PieceBatch& b, const ReduceParams& p,
+                                    hipStream_t stream);
 
 hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, const PieceBatch& b,
                             const ReduceParams& p, hipStream_t stream) {
   if (dtype == MDX_BF16) return launch_allreduce_bf16(grad_dtype, unpack, world, b, p, stream);
+  if (dtype == MDX_F16) return launch_allreduce_f16(grad_dtype, unpack, world, b, p, stream);
   return launch_allreduce_f32(grad_dtype, unpack, world, b, p, stream);
 }
 
 hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
                                 const ReduceParams& p, hipStream_t stream) {
   if (dtype == MDX_BF16) return launch_allreduce_dev_bf16(grad_dtype, world, t, blocks, p, stream);
+  if (dtype == MDX_F16) return launch_allreduce_dev_f16(grad_dtype, world, t, blocks, p, stream);
   return launch_allreduce_dev_f32(grad_dtype, world, t, blocks, p, stream);
+}
+
+hipError_t launch_allreduce_wide(int wire_dtype, int grad_dtype, int world, const PieceBatch& b,
+                                 const ReduceParams& p, hipStream_t stream) {
+  if (wire_dtype == MDX_F16) return launch_allreduce_wide_f16(grad_dtype, world, b, p, stream);
+  return launch_allreduce_wide_bf16(grad_dtype, world, b, p, stream);
+}
+
+hipError_t launch_allreduce_wide_dev(int wire_dtype, int grad_dtype, int world, const DevTable& t, int blocks,
+                                     const ReduceParams& p, hipStream_t stream) {
+  if (wire_dtype == MDX_F16) return launch_allreduce_wide_dev_f16(grad_dtype, world, t, blocks, p, stream);
+  return launch_allreduce_wide_dev_bf16(grad_dtype, world, t, blocks, p, stream);
 }
 
 static bool fast_triple(int in_dtype, int acc_dtype, int out_dtype) {
@@ -40,7 +70,9 @@ int share_wmax(int in_dtype, int acc_dtype, int out_dtype, int world) {
 hipError_t launch_share(int in_dtype, int acc_dtype, int out_dtype, int wmax, const PieceBatch& b,
                         const ReduceParams& p, hipStream_t stream) {
   if (fast_triple(in_dtype, acc_dtype, out_dtype)) return launch_share_fast(in_dtype, wmax, b, p, stream);
-  return launch_share_generic(in_dtype, acc_dtype, out_dtype, b, p, stream);
+  if (in_dtype == MDX_BF16) return launch_share_generic_bf16(acc_dtype, out_dtype, b, p, stream);
+  if (in_dtype == MDX_F16) return launch_share_generic_f16(acc_dtype, out_dtype, b, p, stream);
+  return launch_share_generic_f32(acc_dtype, out_dtype, b, p, stream);
 }
 
 }  // namespace mdx

@@ -13,7 +13,7 @@
 //
 // allreduce_wide_kernel<In, T, G, W> (+ _dev): the same fused all-reduce +
 // unpack for contributions that travel in a narrower dtype In than the bucket
-// dtype T (bf16 gradients summed into fp32 buckets).  Each contribution is
+// dtype T (bf16 or fp16 gradients summed into fp32 buckets).  Each contribution is
 // widened and pre-scaled at the receiver, x_r = rnd_T(cvt_T(c_r[p]) * pre),
 // which is exactly the value the sender's pack (`copy_` into a T bucket, then
 // `mul_(1/W)`) would have put on the wire; the rank-ordered sum, the write of
@@ -250,6 +250,42 @@ hipError_t launch_allreduce_wide_dev(int world, const DevTable& t, int blocks, c
   return by_world(world, DevWide<In, T, G>{t, blocks}, p, stream);
 }
 
+// Per-dtype instantiation sets, one call each from the instantiating
+// translation units: T is the bucket dtype (plain SUM and fused unpack into
+// any gradient dtype); In is the wire dtype of the widening variant.
+template <typename T>
+hipError_t launch_allreduce_for(int grad_dtype, bool unpack, int world, const PieceBatch& b,
+                                const ReduceParams& p, hipStream_t stream) {
+  if (!unpack) return launch_allreduce<T, T, false>(world, b, p, stream);
+  if (grad_dtype == MDX_F32) return launch_allreduce<T, float, true>(world, b, p, stream);
+  if (grad_dtype == MDX_BF16) return launch_allreduce<T, bf16, true>(world, b, p, stream);
+  return launch_allreduce<T, f16, true>(world, b, p, stream);
+}
+
+template <typename T>
+hipError_t launch_allreduce_dev_for(int grad_dtype, int world, const DevTable& t, int blocks,
+                                    const ReduceParams& p, hipStream_t stream) {
+  if (grad_dtype == MDX_F32) return launch_allreduce_unpack_dev<T, float>(world, t, blocks, p, stream);
+  if (grad_dtype == MDX_BF16) return launch_allreduce_unpack_dev<T, bf16>(world, t, blocks, p, stream);
+  return launch_allreduce_unpack_dev<T, f16>(world, t, blocks, p, stream);
+}
+
+template <typename In>
+hipError_t launch_wide_for(int grad_dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                           hipStream_t stream) {
+  if (grad_dtype == MDX_F32) return launch_allreduce_wide<In, float, float>(world, b, p, stream);
+  if (grad_dtype == MDX_BF16) return launch_allreduce_wide<In, float, bf16>(world, b, p, stream);
+  return launch_allreduce_wide<In, float, f16>(world, b, p, stream);
+}
+
+template <typename In>
+hipError_t launch_wide_dev_for(int grad_dtype, int world, const DevTable& t, int blocks, const ReduceParams& p,
+                               hipStream_t stream) {
+  if (grad_dtype == MDX_F32) return launch_allreduce_wide_dev<In, float, float>(world, t, blocks, p, stream);
+  if (grad_dtype == MDX_BF16) return launch_allreduce_wide_dev<In, float, bf16>(world, t, blocks, p, stream);
+  return launch_allreduce_wide_dev<In, float, f16>(world, t, blocks, p, stream);
+}
+
 // ---------------------------------------------------------------------------
 // reduce-scatter share
 // ---------------------------------------------------------------------------
@@ -388,6 +424,27 @@ hipError_t launch_share_w(const PieceBatch& b, const ReduceParams& p, hipStream_
   const int blocks = b.first_block[b.count];
   hipLaunchKernelGGL((share_kernel<In, Acc, Out, WMAX>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
   return hipGetLastError();
+}
+
+// Every (Acc, Out) pair for contributions of type In at the widest class
+// (runtime W <= 16), except (fp32, fp32), which has width-specialised kernels.
+template <typename In, typename Acc>
+hipError_t share16_out(int out_dtype, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  if (out_dtype == MDX_BF16) return launch_share_w<In, Acc, bf16, 16>(b, p, stream);
+  if (out_dtype == MDX_F16) return launch_share_w<In, Acc, f16, 16>(b, p, stream);
+  if constexpr (sizeof(Acc) == 4) {
+    return hipErrorInvalidValue;  // (fp32, fp32) goes to the width-specialised kernels
+  } else {
+    return launch_share_w<In, Acc, float, 16>(b, p, stream);
+  }
+}
+
+template <typename In>
+hipError_t launch_share_generic_for(int acc_dtype, int out_dtype, const PieceBatch& b, const ReduceParams& p,
+                                    hipStream_t stream) {
+  if (acc_dtype == MDX_F32) return share16_out<In, float>(out_dtype, b, p, stream);
+  if (acc_dtype == MDX_BF16) return share16_out<In, bf16>(out_dtype, b, p, stream);
+  return share16_out<In, f16>(out_dtype, b, p, stream);
 }
 
 }  // namespace reduce_impl

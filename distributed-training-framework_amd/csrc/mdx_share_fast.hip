@@ -1,5 +1,5 @@
-// Instantiates the reduce-scatter share for FSDP's usual dtypes (bf16 or fp32
-// gradients, fp32 reduction, fp32 shard) at every width class.
+// Instantiates the reduce-scatter share for FSDP's usual dtypes (fp32, bf16 or
+// fp16 gradients, fp32 reduction, fp32 shard) at every width class.
 #include "mdx_reduce_impl.h"
 
 namespace mdx {
@@ -18,6 +18,7 @@ static hipError_t by_width(int wmax, const PieceBatch& b, const ReduceParams& p,
 hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
                              hipStream_t stream) {
   if (in_dtype == MDX_BF16) return by_width<bf16>(wmax, b, p, stream);
+  if (in_dtype == MDX_F16) return by_width<f16>(wmax, b, p, stream);
   return by_width<float>(wmax, b, p, stream);
 }
 

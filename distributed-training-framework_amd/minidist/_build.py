@@ -26,10 +26,14 @@ SOURCES = [
     "mdx_copy.hip",
     "mdx_reduce.hip",
     "mdx_allreduce_f32.hip",
-    "mdx_allreduce_wide.hip",
     "mdx_allreduce_bf16.hip",
+    "mdx_allreduce_f16.hip",
+    "mdx_allreduce_wide.hip",
+    "mdx_allreduce_wide_f16.hip",
     "mdx_share_fast.hip",
     "mdx_share_generic.hip",
+    "mdx_share_generic_bf16.hip",
+    "mdx_share_generic_f16.hip",
 ]
 HEADERS = ["mdx_internal.h", "mdx_reduce_impl.h"]
 

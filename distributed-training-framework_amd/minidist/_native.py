@@ -23,8 +23,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libmdx.so"
 
 MDX_F32 = 0
 MDX_BF16 = 1
+MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -112,7 +113,9 @@ def dtype_code(dtype: torch.dtype) -> int:
         return MDX_F32
     if dtype == torch.bfloat16:
         return MDX_BF16
-    raise TypeError(f"minidist kernels handle float32 and bfloat16, not {dtype}")
+    if dtype == torch.float16:
+        return MDX_F16
+    raise TypeError(f"minidist kernels handle float32, bfloat16 and float16, not {dtype}")
 
 
 def require_device_tensor(t: torch.Tensor, what: str) -> None:

@@ -399,8 +399,8 @@ class ResidentGroup:
     ):
         """:meth:`all_reduce_unpack` for contributions narrower than the bucket.
 
-        ``wire`` is this rank's row of bf16 contributions (a symmetric buffer);
-        every replica's element is widened to fp32 and multiplied by
+        ``wire`` is this rank's row of bf16 or fp16 contributions (a symmetric
+        buffer); every replica's element is widened to fp32 and multiplied by
         ``prescale`` where it is read, the W values are summed in rank order
         into ``bucket`` (fp32, same element offsets as ``wire``) and unpacked
         into the gradients of ``runs``."""
@@ -433,8 +433,8 @@ class ResidentGroup:
     ) -> "_native.Plan":
         """Device plan of a widening fused all-reduce + unpack.
 
-        ``wire`` is this rank's row of bf16 contributions (a symmetric
-        buffer); every replica's element is widened to fp32 and multiplied by
+        ``wire`` is this rank's row of bf16 or fp16 contributions (a
+        symmetric buffer); every replica's element is widened to fp32 and multiplied by
         ``prescale`` where it is read, the W values are summed in rank order
         into ``bucket`` (fp32, same element offsets as ``wire``) and unpacked
         into the gradients of ``runs``."""

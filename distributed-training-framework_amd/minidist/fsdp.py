@@ -6,7 +6,7 @@ minidist/fsdp.py (``MixedPrecisionPolicy`` :72-105, ``_FSDPUnit`` :108-244,
 run as gfx950 kernels:
 
 * ``unshard`` (:172-182): the fp32 master shard is cast to ``param_dtype``
-  (bf16 round-to-nearest-even) *straight into this rank's slot* of the gather
+  (bf16 or fp16, round-to-nearest-even) *straight into this rank's slot* of the gather
   buffer, so the all-gather needs no separate input; with a real process
   group the all-gather then runs in place, with a
   :class:`~minidist.comm.ResidentGroup` the peers' resident shards are copied
@@ -24,6 +24,7 @@ run as gfx950 kernels:
 
 from __future__ import annotations
 
+import weakref
 from collections.abc import Iterator, Sequence
 from contextlib import contextmanager
 
@@ -385,6 +386,7 @@ class FullyShardedDataParallel(nn.Module):
             for p in unit.params:
                 if p.requires_grad:
                     unit._hook_handles.append(p.register_post_accumulate_grad_hook(self._make_grad_ready(unit)))
+        weakref.finalize(self, _remove_param_hooks, [u._hook_handles for u in self._units])
 
     def _make_pre_forward(self, unit: _FSDPUnit):
         def hook(module, args):
@@ -408,8 +410,16 @@ class FullyShardedDataParallel(nn.Module):
         return hook
 
     def _make_grad_ready(self, unit: _FSDPUnit):
+        # Weak references: the cycle collector does not see a parameter's
+        # post-accumulate-grad hooks, so a hook holding the wrapper or the unit
+        # (which holds the parameter) would keep every shard, gather buffer and
+        # resident peer buffer alive after the caller drops the wrapper.
+        owner_ref, unit_ref = weakref.ref(self), weakref.ref(unit)
+
         def hook(param):
-            unit.on_param_grad_ready(sync=self.require_backward_grad_sync)
+            owner, u = owner_ref(), unit_ref()
+            if owner is not None and u is not None:
+                u.on_param_grad_ready(sync=owner.require_backward_grad_sync)
 
         return hook
 
@@ -486,6 +496,13 @@ class FullyShardedDataParallel(nn.Module):
             return super().__getattr__(name)
         except AttributeError:
             return getattr(self.module, name)
+
+
+def _remove_param_hooks(handle_lists: list) -> None:
+    for handles in handle_lists:
+        for h in handles:
+            h.remove()
+        handles.clear()
 
 
 FSDP = FullyShardedDataParallel

@@ -20,7 +20,10 @@
  *   - Arithmetic is IEEE fp32 with round-to-nearest-even, denormals kept and
  *     no contraction, in the same op order as the ATen chain it replaces, so
  *     results are bit-identical to the reference for a fixed summation order.
- *     bf16 results are rounded to nearest even; every NaN becomes 0xFFFF.
+ *     bf16 and fp16 results are rounded to nearest even (overflow gives
+ *     +-inf).  Every NaN stored as bf16 becomes 0xFFFF; a NaN stored as fp16
+ *     keeps its sign and the top mantissa bits, quieted: sign | 0x7E00 |
+ *     (fp32 mantissa >> 13) -- torch's CPU conversions in both cases.
  *   - found_inf, when not NULL, points to one int32 on the device that the
  *     caller zeroes; a kernel stores 1 into it if it produced any inf or NaN,
  *     and never stores 0.
@@ -36,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 3
+#define MDX_ABI_VERSION 4
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -46,14 +49,16 @@ extern "C" {
 #define MDX_API
 #endif
 
-/* Element types (torch.float32, torch.bfloat16). */
-enum { MDX_F32 = 0, MDX_BF16 = 1 };
+/* Element types (torch.float32, torch.bfloat16, torch.float16).  Every entry
+ * point takes any of them wherever it takes a dtype code, in any combination,
+ * except where stated. */
+enum { MDX_F32 = 0, MDX_BF16 = 1, MDX_F16 = 2 };
 
 /* Status codes (negative; positive values are hipError_t). */
 enum {
   MDX_OK = 0,
   MDX_EINVAL = -1,    /* NULL pointer, negative count or size            */
-  MDX_EDTYPE = -2,    /* dtype code not in {MDX_F32, MDX_BF16}            */
+  MDX_EDTYPE = -2,    /* dtype code not in {MDX_F32, MDX_BF16, MDX_F16}   */
   MDX_EWORLD = -3,    /* world outside [1, MDX_MAX_WORLD] or rank >= world */
   MDX_EALIAS = -4,    /* an output overlaps an input it must not overlap  */
   MDX_ESIZE = -5,     /* plan buffer missing or too small                 */
@@ -152,18 +157,18 @@ MDX_API int mdx_allreduce_unpack(const void* const* replicas, int world, int dty
                                  const mdx_grad_run* runs, int n_runs, void* out, int grad_dtype,
                                  float inv_scale, int32_t* found_inf, void* stream);
 
-/* mdx_allreduce_unpack for contributions narrower than the bucket: bf16
- * contributions (wire_dtype = MDX_BF16) summed into an fp32 bucket
- * (reduce_dtype = MDX_F32; other pairs return MDX_EDTYPE).  Each contribution
+/* mdx_allreduce_unpack for contributions narrower than the bucket: bf16 or
+ * fp16 contributions (wire_dtype = MDX_BF16 or MDX_F16) summed into an fp32
+ * bucket (reduce_dtype = MDX_F32; other pairs return MDX_EDTYPE).  Each contribution
  * is widened and pre-scaled where it is received,
  *   x_r = rnd_f32(f32(rep[r][o+j]) * prescale),
  * then acc = ((x_0 + x_1) + ...) in fp32, out[o+j] = acc (fp32, when out !=
  * NULL) and the unpack / unscale / found-inf epilogue of mdx_allreduce_unpack.
  * With prescale = fp32(1/W) this is bit-identical to the reference chain for a
- * bucket of fp32 holding bf16 gradients: _Bucket.gather_into_buffer's
+ * bucket of fp32 holding bf16 (fp16) gradients: _Bucket.gather_into_buffer's
  * `flat.copy_(p.grad)` (widening) + `buffer.mul_(1/W)` (minidist/ddp.py:
  * 85-91), comm.all_reduce (minidist/comm.py:223-234), scatter_from_buffer's
- * `p.grad.copy_(reduced)` (ddp.py:100-101, fp32 -> bf16 RNE) and unscale_
+ * `p.grad.copy_(reduced)` (ddp.py:100-101, fp32 -> bf16 / fp16 RNE) and unscale_
  * (minidist/amp.py:212-213) -- while the contributions travel at half the
  * bytes.  The fp32 accumulation is FSDP's reduce_dtype arithmetic
  * (minidist/fsdp.py:218-229) applied to DDP buckets.  `out` must not overlap
@@ -193,7 +198,8 @@ MDX_API int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void
 /* fp32 -> bf16 round-to-nearest-even cast (NaN -> 0xFFFF), written straight
  * into this rank's slot of the FSDP gather buffer.
  * Replaces `src = flat_shard.to(param_dtype)` in _FSDPUnit.unshard
- * (minidist/fsdp.py:178-180). */
+ * (minidist/fsdp.py:178-180) for param_dtype = bf16; every other dtype pair
+ * of that cast is an mdx_pack of one span with scale 1. */
 MDX_API int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stream);
 
 /* ---------------------------------------------------------------------------

@@ -9,14 +9,18 @@ It restates, element by element and in numpy, the arithmetic the reference
 performs with ATen ops.  Every function cites the reference lines it follows
 (paths relative to the reference repository root).  Conventions:
 
-* fp32 arrays are ``np.float32``; bf16 arrays are ``np.uint16`` bit patterns.
-* ATen evaluates bf16 arithmetic in an fp32 "opmath" type and rounds the
-  result back to bf16 once per op; Python scalars passed to ``mul_`` are first
+* fp32 arrays are ``np.float32``; bf16 arrays are ``np.uint16`` bit patterns;
+  fp16 arrays are ``np.float16`` (only ever converted, never computed in).
+* ATen evaluates bf16 and fp16 arithmetic in an fp32 "opmath" type and rounds
+  the result back once per op; Python scalars passed to ``mul_`` are first
   rounded to fp32.  Both facts were probed against torch 2.10 CPU and are what
   the helpers below implement.
 * The fp32 -> bf16 conversion is IEEE round-to-nearest-even; every NaN maps to
   ``0xFFFF`` (torch 2.10's vectorised CPU conversion, the one the reference's
   gloo path runs).
+* The fp32 -> fp16 conversion is IEEE round-to-nearest-even with fp16
+  subnormals and overflow to +-inf; a NaN keeps its sign and the top ten
+  mantissa bits, with the quiet bit set (torch 2.10 CPU).
 
 Pins (each function is checked by ``tests/test_oracle.py`` against something
 other than itself):
@@ -27,6 +31,11 @@ function                   pinned by
 bf16_from_f32              torch CPU ``.to(bfloat16)`` over a structured sweep
                            of every (sign, exponent, high mantissa) pattern x
                            the rounding-relevant low halves; hand-built ties
+f16_from_f32               torch CPU ``.to(float16)`` and numpy's
+                           ``astype(float16)`` (non-NaN) over a structured
+                           sweep of every (sign, exponent, top 14 mantissa
+                           bits) x low bits; hand-built ties, subnormals and
+                           overflow; the golden fixture
 build_buckets              brute-force enumeration on tiny configs, the
                            layout invariants of tests/test_ddp.py:103-121 and
                            the closed-form cfg1/cfg2 bucket counts
@@ -55,7 +64,8 @@ import numpy as np
 
 F32 = "f32"
 BF16 = "bf16"
-_ITEMSIZE = {F32: 4, BF16: 2}
+F16 = "f16"
+_ITEMSIZE = {F32: 4, BF16: 2, F16: 2}
 
 BF16_NAN = np.uint16(0xFFFF)
 
@@ -90,12 +100,54 @@ def f32_from_bf16(b: np.ndarray) -> np.ndarray:
     )
 
 
+def f16_from_f32(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16, round to nearest even, in integer arithmetic.
+
+    Follows ``Tensor.to(torch.float16)`` / fp16 ``copy_`` (the casts at
+    minidist/fsdp.py:180 with ``param_dtype=torch.float16`` and
+    minidist/ddp.py:90,101 for fp16 gradients).  Normal results rebias the
+    exponent (127 -> 15) and round at mantissa bit 13; results below 2^-14
+    are the significand (implicit bit included) shifted right by
+    126 - exponent with the same ties-to-even rule; from 65520 up
+    everything rounds to +-inf; a NaN becomes sign | 0x7E00 | mantissa >> 13.
+    """
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
+    sign = (u >> 16) & 0x8000
+    a = u & 0x7FFFFFFF
+    r = a - 0x38000000  # exponent 127 -> 15
+    normal = (r + 0xFFF + ((r >> 13) & 1)) >> 13
+    e = a >> 23
+    m = (a & 0x7FFFFF) | 0x800000
+    shift = np.clip(126 - e, 14, 25)
+    q = m >> shift
+    rem = m & ((1 << shift) - 1)
+    half = 1 << (shift - 1)
+    sub = q + ((rem > half) | ((rem == half) & ((q & 1) == 1)))
+    out = np.where(a >= 0x38800000, normal, sub)
+    out = np.where(a >= 0x477FF000, 0x7C00, out)
+    out = np.where(a > 0x7F800000, 0x7E00 | ((a >> 13) & 0x3FF), out)
+    return (sign | out).astype(np.uint16).view(np.float16)
+
+
+def f32_from_f16(h: np.ndarray) -> np.ndarray:
+    """fp16 -> fp32 (exact widening; numpy's conversion, subnormals included)."""
+    return np.ascontiguousarray(h, dtype=np.float16).astype(np.float32)
+
+
 def to_f32(a: np.ndarray, dtype: str) -> np.ndarray:
-    return f32_from_bf16(a) if dtype == BF16 else np.asarray(a, dtype=np.float32)
+    if dtype == BF16:
+        return f32_from_bf16(a)
+    if dtype == F16:
+        return f32_from_f16(a)
+    return np.asarray(a, dtype=np.float32)
 
 
 def from_f32(a: np.ndarray, dtype: str) -> np.ndarray:
-    return bf16_from_f32(a) if dtype == BF16 else np.asarray(a, dtype=np.float32)
+    if dtype == BF16:
+        return bf16_from_f32(a)
+    if dtype == F16:
+        return f16_from_f32(a)
+    return np.asarray(a, dtype=np.float32)
 
 
 def convert(a: np.ndarray, src: str, dst: str) -> np.ndarray:
@@ -106,7 +158,7 @@ def convert(a: np.ndarray, src: str, dst: str) -> np.ndarray:
 
 
 def zeros(n: int, dtype: str) -> np.ndarray:
-    return np.zeros(n, dtype=np.uint16 if dtype == BF16 else np.float32)
+    return np.zeros(n, dtype={BF16: np.uint16, F16: np.float16}.get(dtype, np.float32))
 
 
 def mul_scalar(a: np.ndarray, dtype: str, scale: float) -> np.ndarray:
@@ -339,7 +391,7 @@ def fsdp_gather_cast(flat_shard_f32: np.ndarray, param_dtype: str) -> np.ndarray
     """``flat_shard.to(param_dtype)`` before the all-gather (fsdp.py:178-180)."""
     if param_dtype == F32:
         return np.array(flat_shard_f32, dtype=np.float32, copy=True)
-    return bf16_from_f32(flat_shard_f32)
+    return from_f32(flat_shard_f32, param_dtype)
 
 
 def fsdp_flatten(

@@ -49,6 +49,11 @@ def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
         if not np.array_equal(na, nb):
             return False
         return np.array_equal(a[~na], b[~nb])
+    if a.dtype == np.float16:
+        na, nb = np.isnan(a), np.isnan(b)
+        if not np.array_equal(na, nb):
+            return False
+        return np.array_equal(a.view(np.uint16)[~na], b.view(np.uint16)[~nb])
     return np.array_equal(a, b)
 
 
@@ -57,8 +62,9 @@ def first_mismatch(a: np.ndarray, b: np.ndarray) -> str:
     b = np.asarray(b).reshape(-1)
     if a.shape != b.shape:
         return f"shape {a.shape} vs {b.shape}"
-    ua = a.view(np.uint32) if a.dtype == np.float32 else a
-    ub = b.view(np.uint32) if b.dtype == np.float32 else b
+    bits = {np.dtype(np.float32): np.uint32, np.dtype(np.float16): np.uint16}
+    ua = a.view(bits[a.dtype]) if a.dtype in bits else a
+    ub = b.view(bits[b.dtype]) if b.dtype in bits else b
     idx = np.nonzero(ua != ub)[0]
     if idx.size == 0:
         return "no mismatch"

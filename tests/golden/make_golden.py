@@ -7,12 +7,14 @@ inputs.  This is independent of the numpy oracle in oracle/gradpath.py, which
 the CPU tests check against these files.  The reference package itself is not
 imported; each chain below cites the lines it replays.
 
-  python tests/golden/make_golden.py
+  python tests/golden/make_golden.py          # writes the fixtures that are missing
+  python tests/golden/make_golden.py --force  # rewrites every fixture
 """
 
 from __future__ import annotations
 
 import json
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -27,12 +29,20 @@ FSDP_NUMELS = [7, 12, 5, 33, 64, 3]
 def _bits(t: torch.Tensor) -> np.ndarray:
     if t.dtype == torch.bfloat16:
         return t.view(torch.int16).numpy().astype(np.uint16)
-    return t.numpy().copy()
+    return t.numpy().copy()  # fp32 -> float32, fp16 -> float16
 
 
 def _specials(g: torch.Generator, n: int) -> torch.Tensor:
     pool = torch.tensor(
         [0.0, -0.0, 1e-40, -1e-42, 3.0e38, -3.0e38, 1.0, 2.0**-126, 7.5e-39, 65504.0], dtype=torch.float32
+    )
+    return pool[torch.randint(0, len(pool), (n,), generator=g)]
+
+
+def _specials_f16(g: torch.Generator, n: int) -> torch.Tensor:
+    """fp16's own edge values: subnormals, the largest finite value, the smallest normal."""
+    pool = torch.tensor(
+        [0.0, -0.0, 6e-8, -1.2e-7, 60000.0, -65504.0, 1.0, 2.0**-14, 3.0e-5, 65504.0], dtype=torch.float32
     )
     return pool[torch.randint(0, len(pool), (n,), generator=g)]
 
@@ -57,6 +67,29 @@ def bf16_cast() -> dict:
     u = np.concatenate([np.array(words, dtype=np.uint32), rand.numpy().astype(np.uint32)])
     x = torch.from_numpy(u.view(np.float32).copy())
     return {"x_bits": u, "y_bits": _bits(x.to(torch.bfloat16))}
+
+
+# ---------------------------------------------------------------------------
+# fp16 cast (fsdp.py:178-180 `flat_shard.to(param_dtype)` with param_dtype=float16)
+# ---------------------------------------------------------------------------
+
+
+def f16_cast() -> dict:
+    g = torch.Generator().manual_seed(17)
+    words = [
+        0x3F800000, 0x3F801000, 0x3F803000, 0x3F801001, 0x3F800FFF,  # 1.0; ties at mantissa bit 12
+        0x477FE000, 0x477FEFFF, 0x477FF000, 0x477FFFFF, 0x47800000,  # 65504 .. the overflow threshold
+        0x38800000, 0x387FF000, 0x387FE000, 0x387FFFFF,  # 2^-14 and just below (subnormal -> normal)
+        0x33800000, 0x33000000, 0x33000001, 0x32FFFFFF, 0x33C00000, 0x34200000,  # 2^-24, 2^-25 ties
+        0x00000001, 0x80000000, 0x7F800000, 0xFF800000, 0x7F7FFFFF,
+        0x7FC00000, 0xFFC12345, 0x7F800001, 0x7FA00000,  # NaNs: quiet, payload, signalling
+    ]
+    rand = torch.randint(0, 2**32, (4000,), generator=g, dtype=torch.int64)
+    # exponents that land in fp16's range, low bits at rounding boundaries
+    rand[:2000] = ((rand[:2000] & 0x807FFFFF) | (torch.randint(100, 145, (2000,), generator=g) << 23)) & ~0x3F
+    u = np.concatenate([np.array(words, dtype=np.uint32), rand.numpy().astype(np.uint32)])
+    x = torch.from_numpy(u.view(np.float32).copy())
+    return {"x_bits": u, "y_bits": x.to(torch.float16).view(torch.int16).numpy().view(np.uint16)}
 
 
 # ---------------------------------------------------------------------------
@@ -95,7 +128,10 @@ def ddp_case(
             t = torch.randn(n, generator=g) * 1e-2 * scale
             k = max(1, n // 8)
             idx = torch.randint(0, n, (k,), generator=g)
-            t[idx] = _specials(g, k) * (1.0 if dtype == torch.float32 else 1e-30)
+            if dtype == torch.float16:
+                t[idx] = _specials_f16(g, k)
+            else:
+                t[idx] = _specials(g, k) * (1.0 if dtype == torch.float32 else 1e-30)
             row.append(t.to(dtype))
         grads.append(row)
     grads[rank][4] = None  # this rank's param 4 got no gradient (zero-filled, then cloned)
@@ -162,7 +198,9 @@ def ddp_case(
 # ---------------------------------------------------------------------------
 
 
-def fsdp_case(W: int, grad_dtype: torch.dtype, reduce_dtype: torch.dtype, seed: int) -> dict:
+def fsdp_case(W: int, grad_dtype: torch.dtype, reduce_dtype: torch.dtype, seed: int,
+              cast_dtype: torch.dtype = torch.bfloat16) -> dict:
+    """``cast_dtype`` is the gather dtype (MixedPrecisionPolicy.param_dtype)."""
     g = torch.Generator().manual_seed(seed)
     total = sum(FSDP_NUMELS)
     S = (total + W - 1) // W  # fsdp.py:135
@@ -171,8 +209,10 @@ def fsdp_case(W: int, grad_dtype: torch.dtype, reduce_dtype: torch.dtype, seed: 
     master_flat[:total] = torch.randn(total, generator=g) * 0.02
     out = {"W": W, "S": S, "P": P, "numels": np.array(FSDP_NUMELS), "grad_dtype": str(grad_dtype),
            "reduce_dtype": str(reduce_dtype), "master_flat": master_flat.numpy().copy()}
+    if cast_dtype != torch.bfloat16:
+        out["cast_dtype"] = str(cast_dtype)
     for r in range(W):
-        out[f"gather_cast_r{r}"] = _bits(master_flat[r * S : (r + 1) * S].clone().to(torch.bfloat16))
+        out[f"gather_cast_r{r}"] = _bits(master_flat[r * S : (r + 1) * S].clone().to(cast_dtype))
     grads = []
     for r in range(W):
         row = []
@@ -207,29 +247,35 @@ def fsdp_case(W: int, grad_dtype: torch.dtype, reduce_dtype: torch.dtype, seed: 
     return out
 
 
+FIXTURES = {
+    "bf16_cast.npz": bf16_cast,
+    "f16_cast.npz": f16_cast,
+    "ddp_f32_w4.npz": lambda: ddp_case(torch.float32, W=4, rank=1, cap_mb=0.001, scale=2.0**16, seed=5,
+                                       inject_inf=False),
+    "ddp_f32_w3_inf.npz": lambda: ddp_case(torch.float32, W=3, rank=2, cap_mb=0.002, scale=2.0**10, seed=6,
+                                           inject_inf=True),
+    "ddp_bf16_w8.npz": lambda: ddp_case(torch.bfloat16, W=8, rank=5, cap_mb=0.0005, scale=2.0**12, seed=7,
+                                        inject_inf=False),
+    "ddp_bf16_f32bucket_w8.npz": lambda: ddp_case(torch.bfloat16, W=8, rank=3, cap_mb=0.0005, scale=2.0**12,
+                                                  seed=13, inject_inf=True, bucket_dtype=torch.float32),
+    "ddp_f16_w4_inf.npz": lambda: ddp_case(torch.float16, W=4, rank=2, cap_mb=0.0005, scale=2.0**10, seed=14,
+                                           inject_inf=True),
+    "ddp_f16_f32bucket_w8.npz": lambda: ddp_case(torch.float16, W=8, rank=6, cap_mb=0.0005, scale=2.0**10,
+                                                 seed=15, inject_inf=False, bucket_dtype=torch.float32),
+    "fsdp_bf16_w4.npz": lambda: fsdp_case(4, torch.bfloat16, torch.float32, seed=8),
+    "fsdp_bf16_w3.npz": lambda: fsdp_case(3, torch.bfloat16, torch.float32, seed=9),
+    "fsdp_f32_w2.npz": lambda: fsdp_case(2, torch.float32, torch.float32, seed=10),
+    "fsdp_bf16red_w4.npz": lambda: fsdp_case(4, torch.bfloat16, torch.bfloat16, seed=12),
+    "fsdp_f16_w4.npz": lambda: fsdp_case(4, torch.float16, torch.float32, seed=16, cast_dtype=torch.float16),
+    "fsdp_f16red_w3.npz": lambda: fsdp_case(3, torch.float16, torch.float16, seed=18, cast_dtype=torch.float16),
+}
+
+
 def main() -> None:
-    np.savez_compressed(HERE / "bf16_cast.npz", **bf16_cast())
-    np.savez_compressed(
-        HERE / "ddp_f32_w4.npz",
-        **ddp_case(torch.float32, W=4, rank=1, cap_mb=0.001, scale=2.0**16, seed=5, inject_inf=False),
-    )
-    np.savez_compressed(
-        HERE / "ddp_f32_w3_inf.npz",
-        **ddp_case(torch.float32, W=3, rank=2, cap_mb=0.002, scale=2.0**10, seed=6, inject_inf=True),
-    )
-    np.savez_compressed(
-        HERE / "ddp_bf16_w8.npz",
-        **ddp_case(torch.bfloat16, W=8, rank=5, cap_mb=0.0005, scale=2.0**12, seed=7, inject_inf=False),
-    )
-    np.savez_compressed(
-        HERE / "ddp_bf16_f32bucket_w8.npz",
-        **ddp_case(torch.bfloat16, W=8, rank=3, cap_mb=0.0005, scale=2.0**12, seed=13, inject_inf=True,
-                   bucket_dtype=torch.float32),
-    )
-    np.savez_compressed(HERE / "fsdp_bf16_w4.npz", **fsdp_case(4, torch.bfloat16, torch.float32, seed=8))
-    np.savez_compressed(HERE / "fsdp_bf16_w3.npz", **fsdp_case(3, torch.bfloat16, torch.float32, seed=9))
-    np.savez_compressed(HERE / "fsdp_f32_w2.npz", **fsdp_case(2, torch.float32, torch.float32, seed=10))
-    np.savez_compressed(HERE / "fsdp_bf16red_w4.npz", **fsdp_case(4, torch.bfloat16, torch.bfloat16, seed=12))
+    force = "--force" in sys.argv[1:]
+    for name, make in FIXTURES.items():
+        if force or not (HERE / name).exists():
+            np.savez_compressed(HERE / name, **make())
     # Scaler known answers from the reference's tests/test_amp.py.
     kat = {
         "overflow_skips": {"init_scale": 1024.0, "found": [True], "scale_after": 512.0, "num_skipped": 1,

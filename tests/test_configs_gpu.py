@@ -22,6 +22,8 @@ bucket and an FSDP unit whose element offsets pass 2^31 (4-16 GB buffers).
 
 from __future__ import annotations
 
+import gc
+
 import numpy as np
 import pytest
 import torch
@@ -39,6 +41,10 @@ DEV = torch.device("cuda", 0)
 def _release_memory():
     yield
     torch.cuda.synchronize()
+    # A wrapper and its module reference each other through the gradient hooks, so the
+    # multi-GB buffers of these configurations are freed by the cycle collector, not by
+    # reference counting.
+    gc.collect()
     torch.cuda.empty_cache()
 
 

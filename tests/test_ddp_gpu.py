@@ -38,7 +38,7 @@ def dev_from(a: np.ndarray, shape) -> torch.Tensor:
 
 
 def odt(dtype: torch.dtype) -> str:
-    return o.BF16 if dtype == torch.bfloat16 else o.F32
+    return {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(dtype, o.F32)
 
 
 class Flat(nn.Module):
@@ -78,7 +78,7 @@ def synthetic_grads(rng, shapes, W, dtype, scale, none_at=()):
     return out
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("W,rank", [(2, 1), (4, 0), (8, 5), (3, 2)])
 @pytest.mark.parametrize("cap", [1e-6, 0.01, 25.0, 1e6])
 def test_finish_gradient_sync_bitwise(rng, dtype, W, rank, cap):
@@ -540,27 +540,29 @@ def test_fused_unscale_in_ddp_unpack(rng, inject):
 
 
 # ---------------------------------------------------------------------------
-# reduce_dtype: bf16 gradients accumulated in fp32 buckets (the Llama-7B configuration, cfg4, at small scale)
+# reduce_dtype: bf16 / fp16 gradients accumulated in fp32 buckets (the Llama-7B configuration, cfg4, at
+# small scale)
 # ---------------------------------------------------------------------------
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("W,rank", [(2, 1), (8, 5), (3, 0)])
 @pytest.mark.parametrize("cap", [1e-6, 0.01, 25.0])
 @pytest.mark.parametrize("inject", [False, True])
-def test_reduce_dtype_widening_bitwise(rng, W, rank, cap, inject):
+def test_reduce_dtype_widening_bitwise(rng, dtype, W, rank, cap, inject):
     """Widening buckets == the reference chain with an fp32 bucket (copy_, mul_(1/W), SUM, copy_, unscale)."""
     shapes = [(33,), (64, 8), (5,), (130,), (1,), (7, 9), (256, 4), (3,)]
-    S = 2.0**12
-    model = Flat(shapes, torch.bfloat16)
+    S = 2.0**12 if dtype == torch.bfloat16 else 2.0**10
+    model = Flat(shapes, dtype)
     scaler = DistributedGradScaler(init_scale=S)
     ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, grad_scaler=scaler,
               reduce_dtype=torch.float32)
     assert all(b.widening and b.buffer is None for b in ddp._buckets)
-    grads = synthetic_grads(rng, shapes, W, torch.bfloat16, S)
+    grads = synthetic_grads(rng, shapes, W, dtype, S)
     grads[rank][2] = None
-    if inject:
-        grads[(rank + 1) % W][5][7] = np.uint16(0x7F80)  # +inf in a peer's bf16 gradient
-    dts = [o.BF16] * len(shapes)
+    if inject:  # +inf in a peer's 16-bit gradient
+        grads[(rank + 1) % W][5][7] = np.uint16(0x7F80) if dtype == torch.bfloat16 else np.float16(np.inf)
+    dts = [odt(dtype)] * len(shapes)
     stage_peers(ddp, grads, dts, rank, W)
     for p, g in zip(model.parameters(), grads[rank], strict=True):
         p.grad = None if g is None else dev_from(g, p.shape)
@@ -569,11 +571,11 @@ def test_reduce_dtype_widening_bitwise(rng, W, rank, cap, inject):
     found = scaler.unscale_(opt)
     want = o.ddp_pipeline(grads, dts, [int(np.prod(s)) for s in shapes], cap, rank, 1.0 / S, bucket_dtype=o.F32)
     for i, p in enumerate(model.parameters()):
-        assert p.grad.dtype == torch.bfloat16
+        assert p.grad.dtype == dtype
         got = host_bits(p.grad)
         assert same_bits(got, want["grads"][i]), f"param {i}: " + first_mismatch(got, want["grads"][i])
     for b, bucket in enumerate(ddp._buckets):
-        assert bucket.buffer.dtype == torch.float32 and bucket.wire.dtype == torch.bfloat16
+        assert bucket.buffer.dtype == torch.float32 and bucket.wire.dtype == dtype
         assert same_bits(host_bits(bucket.buffer), want["reduced"][b])
     assert found == want["found_inf"] == inject
     scaler.update()

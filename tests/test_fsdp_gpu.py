@@ -59,7 +59,7 @@ def _capture(store):
 
 
 @pytest.mark.parametrize("W", [2, 4, 3])
-@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_shard_grads_match_oracle_and_full_batch(W, param_dtype):
     c = tiny_gpt.Config(n_layer=3)
     ids, tgt = tiny_gpt.batch(c, 12 if W == 3 else 8, seed=1234)
@@ -86,7 +86,7 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype):
     _, loss = fsdp(ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV))
     loss.backward()
 
-    gdt = o.BF16 if param_dtype == torch.bfloat16 else o.F32
+    gdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(param_dtype, o.F32)
     for unit in fsdp._units:
         assert not unit.is_unsharded and unit._full.untyped_storage().nbytes() == 0
         assert all(p.grad is None for p in unit.params)
@@ -260,3 +260,29 @@ def test_bf16_params_track_fp32_training():
     for (mine, _), (want, _) in zip(bf16, fp32, strict=True):  # this rank's loss on its chunk, both runs
         assert abs(mine - want) <= 0.05
     assert all(u.flat_shard.dtype == torch.float32 for u in fsdp._units)
+
+
+def test_dropped_fsdp_frees_its_buffers():
+    """The gradient hooks hold the wrapper and its units weakly: dropping the wrapper and the
+    module frees the shards, the gather buffers and the resident peer buffers."""
+    import gc
+    import weakref
+
+    c = tiny_gpt.Config(n_layer=2, n_embd=256)
+    torch.cuda.synchronize()
+    gc.collect()
+    base = torch.cuda.memory_allocated(DEV)
+    model = tiny_gpt.GPT(c).to(DEV)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(4, 1, DEV),
+                mixed_precision=MixedPrecisionPolicy(param_dtype=torch.bfloat16))
+    ids, tgt = tiny_gpt.batch(c, 4, seed=3)
+    logits, loss = fsdp(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    refs = [weakref.ref(fsdp), weakref.ref(fsdp._units[0]), weakref.ref(fsdp._units[0].flat_shard)]
+    assert torch.cuda.memory_allocated(DEV) > base
+    # (an output kept alive would hold its autograd graph, and the graph the module hooks)
+    del fsdp, model, loss, logits
+    gc.collect()
+    assert all(r() is None for r in refs)
+    assert torch.cuda.memory_allocated(DEV) == base
+

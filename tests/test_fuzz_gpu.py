@@ -1,7 +1,7 @@
 """Seeded random DDP pipelines on the GPU, bit for bit against the oracle.
 
-Each case draws its own configuration: gradient dtype (fp32 or bf16, and for
-bf16 optionally fp32 buckets, the widening path), W in [2, 16], the rank,
+Each case draws its own configuration: gradient dtype (fp32, bf16 or fp16,
+and for the 16-bit ones optionally fp32 buckets, the widening path), W in [2, 16], the rank,
 20-40 parameters of ragged shapes, a bucket cap between one bucket per
 parameter and a single bucket, gradients that are views at odd element
 offsets of a larger buffer (so that no pointer need be 16-byte aligned),
@@ -42,7 +42,7 @@ def dev_view(a: np.ndarray, shape, offset: int) -> torch.Tensor:
         buf = torch.zeros(n + offset + 8, dtype=torch.int16, device=DEV)
         buf[offset : offset + n].copy_(torch.from_numpy(a.view(np.int16).copy()))
         return buf.view(torch.bfloat16)[offset : offset + n].view(shape)
-    buf = torch.zeros(n + offset + 8, dtype=torch.float32, device=DEV)
+    buf = torch.zeros(n + offset + 8, dtype=torch.float16 if a.dtype == np.float16 else torch.float32, device=DEV)
     buf[offset : offset + n].copy_(torch.from_numpy(a.copy()))
     return buf[offset : offset + n].view(shape)
 
@@ -62,19 +62,19 @@ class Flat(nn.Module):
 @pytest.mark.parametrize("seed", range(24))
 def test_random_pipeline_matches_oracle(seed):
     rng = np.random.default_rng(9000 + seed)
-    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
-    widening = dtype == torch.bfloat16 and rng.random() < 0.5
-    gdt = o.BF16 if dtype == torch.bfloat16 else o.F32
+    dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    widening = dtype != torch.float32 and rng.random() < 0.5
+    gdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(dtype, o.F32)
     W = int(rng.integers(2, 17))
     rank = int(rng.integers(0, W))
     n_params = int(rng.integers(20, 41))
     shapes = [(int(rng.integers(1, 3000)),) if rng.random() < 0.7 else (int(rng.integers(1, 60)), int(rng.integers(1, 40)))
               for _ in range(n_params)]
     numels = [int(np.prod(s)) for s in shapes]
-    total_mb = sum(numels) * (2 if dtype == torch.bfloat16 else 4) / 2**20
+    total_mb = sum(numels) * (4 if dtype == torch.float32 else 2) / 2**20
     cap = float(rng.choice([1e-6, total_mb / 7, total_mb / 3, 1e6]))
     use_scaler = rng.random() < 0.6
-    scale = 2.0 ** int(rng.integers(0, 14)) if use_scaler else 1.0
+    scale = 2.0 ** int(rng.integers(0, 14 if dtype != torch.float16 else 10)) if use_scaler else 1.0
 
     grads = []
     for r in range(W):
@@ -98,7 +98,7 @@ def test_random_pipeline_matches_oracle(seed):
         idxs = [index[id(p)] for p in bucket.params]
         rows = ddp.bucket_replicas(b)
         wire_dtype, prescaled = ddp.bucket_wire_format(b)
-        wdt = o.BF16 if wire_dtype == torch.bfloat16 else o.F32
+        wdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(wire_dtype, o.F32)
         for r in range(W):
             if r != rank:
                 packed = o.pack([grads[r][i] for i in idxs], [gdt] * len(idxs), [numels[i] for i in idxs], wdt,

@@ -108,6 +108,16 @@ def test_argument_checks_happen_before_any_launch():
     assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 2, 0, 0, 1, P(1 << 20), 0, 0, 1.0, None, None) == -3
     assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 0, 0, 7, 1, P(1 << 20), 0, 0, 1.0, None, None) == -2
     assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 0, 0, 0, 1, P(8192), 0, 0, 1.0, None, None) == -4
+    # fp16 (MDX_F16 = 2) is an element type of every entry point; widening is only bf16 / fp16 -> fp32
+    assert nat.MDX_F16 == 2
+    assert L.mdx_pack(None, 0, 2, 0, 1.0, 0, None, None) == 0
+    assert L.mdx_unscale_found_inf(None, 0, 2, 1.0, None, None) == 0
+    assert L.mdx_allreduce_unpack(reps, 2, 2, None, 0, None, 2, 1.0, None, None) == 0
+    assert L.mdx_allreduce_unpack_wide(reps, 2, 2, runs.ctypes.data, 1, None, 2, 2, 0.5, 1.0, None, None) == -2
+    assert L.mdx_allreduce_unpack_wide(reps, 2, 0, runs.ctypes.data, 1, None, 0, 2, 0.5, 1.0, None, None) == -2
+    # dtypes 2 pass the dtype check; the out-of-range rank is what is rejected (nothing launches)
+    assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 2, 2, 2, 1, P(1 << 20), 2, 0, 1.0, None,
+                                      None) == -3
 
 
 # ---------------------------------------------------------------------------
@@ -126,6 +136,36 @@ def test_comm_stats_formulas_match_reference():
     assert comm.get_world_size(grp) == 4 and comm.get_rank(grp) == 1
     assert comm.get_world_size(None) == 1 and comm.get_rank(None) == 0
     assert comm.all_reduce(torch.zeros(3), group=None) is None  # world 1 short-circuit
+
+
+def test_dropped_ddp_frees_its_module_and_removes_its_hooks():
+    """A parameter's post-accumulate-grad hooks are not visited by the cycle collector, so a
+    wrapper reachable from them would keep its module, buckets and resident arenas alive for
+    good.  Dropping the wrapper frees it at once and takes its hooks off a module that lives on."""
+    import gc
+    import weakref
+
+    from minidist import DDP, DistributedGradScaler
+
+    class Flat(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ps = torch.nn.ParameterList([torch.nn.Parameter(torch.zeros(100)) for _ in range(3)])
+
+    def make():
+        m = Flat()
+        d = DDP(m, process_group=comm.ResidentGroup(2, 1, "cpu"), bucket_cap_mb=1e-6,
+                grad_scaler=DistributedGradScaler())
+        return weakref.ref(m.ps[0]), weakref.ref(d)
+
+    wp, wd = make()
+    assert wd() is None and wp() is None  # no cycle at all: reference counting frees both
+    m = Flat()
+    d = DDP(m, process_group=comm.ResidentGroup(2, 1, "cpu"))
+    assert all(len(p._post_accumulate_grad_hooks) == 1 for p in m.parameters())
+    del d
+    gc.collect()
+    assert all(not p._post_accumulate_grad_hooks for p in m.parameters())
 
 
 def test_resident_group_validates_its_shape():

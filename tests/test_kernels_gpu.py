@@ -24,16 +24,21 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 SENTINEL_F32 = np.float32(-7.25)
 SENTINEL_BF16 = np.uint16(0x4242)
+SENTINEL = {o.F32: SENTINEL_F32, o.BF16: SENTINEL_BF16, o.F16: np.float16(-3.5)}
+CODE = {o.F32: nat.MDX_F32, o.BF16: nat.MDX_BF16, o.F16: nat.MDX_F16}
+DTYPES = [o.F32, o.BF16, o.F16]
 
 
 def code(dt: str) -> int:
-    return nat.MDX_BF16 if dt == o.BF16 else nat.MDX_F32
+    return CODE[dt]
 
 
 def to_dev(a: np.ndarray) -> torch.Tensor:
     a = np.ascontiguousarray(a)
     if a.dtype == np.uint16:
         return torch.from_numpy(a.view(np.int16).copy()).to(DEV).view(torch.bfloat16)
+    if a.dtype == np.float16:
+        return torch.from_numpy(a.copy()).to(DEV)
     return torch.from_numpy(a.astype(np.float32)).to(DEV)
 
 
@@ -47,6 +52,8 @@ def to_host(t: torch.Tensor) -> np.ndarray:
 def empty_dev(n: int, dt: str) -> torch.Tensor:
     if dt == o.BF16:
         return torch.full((n,), int(SENTINEL_BF16.view(np.int16)), dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    if dt == o.F16:
+        return torch.full((n,), float(SENTINEL[o.F16]), dtype=torch.float16, device=DEV)
     return torch.full((n,), float(SENTINEL_F32), dtype=torch.float32, device=DEV)
 
 
@@ -57,14 +64,19 @@ def stream() -> int:
 def values(rng, n: int, dt: str, specials: bool = True, scale: float = 1.0) -> np.ndarray:
     x = (rng.standard_normal(n) * scale).astype(np.float32)
     if specials and n:
-        pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-40, 3.4e38, -3.39e38, 1.2e-38], np.float32)
+        if dt == o.F16:  # fp16's own edges: subnormals, the largest finite value, the smallest normal
+            pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 6e-8, -1e-5, 65504.0, -60000.0, 6.1035e-5],
+                            np.float32)
+        else:
+            pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-40, 3.4e38, -3.39e38, 1.2e-38],
+                            np.float32)
         idx = rng.integers(0, n, max(1, n // 50))
         x[idx] = pool[rng.integers(0, len(pool), idx.size)]
     return o.from_f32(x, dt)
 
 
 def esize(dt: str) -> int:
-    return 2 if dt == o.BF16 else 4
+    return o.itemsize(dt)
 
 
 # ---------------------------------------------------------------------------
@@ -99,13 +111,14 @@ def _span_case(rng, sdt, ddt, null_every=0, n_spans=None):
     return srcs, dst, rows, rows_host
 
 
-@pytest.mark.parametrize("sdt,ddt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.BF16, o.F32)])
+@pytest.mark.parametrize("sdt", DTYPES)
+@pytest.mark.parametrize("ddt", DTYPES)
 @pytest.mark.parametrize("scale,divide", [(1.0, False), (1.0 / 8, False), (1.0 / 3, False), (3.0, True), (8.0, True)])
 def test_pack_matches_oracle(rng, sdt, ddt, scale, divide):
     srcs, dst, rows, rows_host = _span_case(rng, sdt, ddt, null_every=5)
     nat.pack(nat.spans_array(rows), code(sdt), code(ddt), nat.f32(scale), divide, stream())
     got = to_host(dst)
-    want = np.full(got.shape, SENTINEL_BF16 if ddt == o.BF16 else SENTINEL_F32, dtype=got.dtype)
+    want = np.full(got.shape, SENTINEL[ddt], dtype=got.dtype)
     for host, off, n in rows_host:
         v = o.zeros(n, ddt) if host is None else o.convert(host, sdt, ddt)
         if scale != 1.0:
@@ -114,7 +127,11 @@ def test_pack_matches_oracle(rng, sdt, ddt, scale, divide):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("bdt,gdt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16)])
+@pytest.mark.parametrize(
+    "bdt,gdt",
+    [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.F16, o.F16), (o.F32, o.F16), (o.F16, o.F32),
+     (o.BF16, o.F16)],
+)
 @pytest.mark.parametrize("inv_scale", [1.0, 2.0**-16, 1.0 / 3])
 def test_unpack_unscale_found_inf_matches_oracle(rng, bdt, gdt, inv_scale):
     n_total = sum(SIZES) + 64
@@ -141,7 +158,7 @@ def test_unpack_unscale_found_inf_matches_oracle(rng, bdt, gdt, inv_scale):
         got = to_host(g)
         assert same_bits(got[shift : shift + len(src)], v), first_mismatch(got[shift : shift + len(src)], v)
         sent = got[:shift].tolist() + got[shift + len(src) :].tolist()
-        assert all(s == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32) for s in sent)
+        assert all(s == SENTINEL[gdt] for s in sent)
     assert bool(flag.item()) == any_bad
 
 
@@ -164,11 +181,19 @@ def test_unpack_flags_only_when_nonfinite(rng):
     ob = empty_dev(64, o.BF16)
     nat.unpack(nat.spans_array([(t.data_ptr(), ob.data_ptr(), 64)]), 0, 1, 1.0, flag.data_ptr(), stream())
     assert flag.item() == 1
+    # fp32 value finite, fp16 result overflows (65520 rounds to inf): counts; 65519 does not
+    flag.zero_()
+    oh = empty_dev(64, o.F16)
+    for v, want in ((65519.0, 0), (65520.0, 1)):
+        t = to_dev(np.full(64, v, np.float32))
+        nat.unpack(nat.spans_array([(t.data_ptr(), oh.data_ptr(), 64)]), 0, nat.MDX_F16, 1.0, flag.data_ptr(),
+                   stream())
+        assert flag.item() == want, v
 
 
-@pytest.mark.parametrize("dt", [o.F32, o.BF16])
+@pytest.mark.parametrize("dt", DTYPES)
 def test_unscale_in_place_matches_oracle(rng, dt):
-    hosts = [values(rng, n, dt, scale=2.0**16) for n in SIZES]
+    hosts = [values(rng, n, dt, scale=2.0**10 if dt == o.F16 else 2.0**16) for n in SIZES]
     devs = [to_dev(h) for h in hosts]
     rows = [(t.data_ptr(), t.data_ptr(), t.numel()) for t in devs]
     flag = torch.zeros(1, dtype=torch.int32, device=DEV)
@@ -184,7 +209,7 @@ def test_unscale_in_place_matches_oracle(rng, dt):
 # ---------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dt", [o.F32, o.BF16])
+@pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("W", [1, 2, 3, 4, 5, 8, 16])
 def test_allreduce_sum_matches_oracle(rng, dt, W):
     runs = [(3, 1), (17, 4096), (5000, 3), (70000, 12345)]  # (offset, numel), increasing
@@ -196,7 +221,7 @@ def test_allreduce_sum_matches_oracle(rng, dt, W):
         [r.data_ptr() for r in reps], code(dt), [a for a, _ in runs], [n for _, n in runs], out.data_ptr(), stream()
     )
     got = to_host(out)
-    want = np.full(extent, SENTINEL_BF16 if dt == o.BF16 else SENTINEL_F32, dtype=got.dtype)
+    want = np.full(extent, SENTINEL[dt], dtype=got.dtype)
     for a, n in runs:
         want[a : a + n] = o.allreduce_sum([h[a : a + n] for h in reps_host], dt)
     assert same_bits(got, want), first_mismatch(got, want)
@@ -226,7 +251,11 @@ def test_allreduce_full_bucket_exact_sum_property(rng):
     assert np.array_equal(to_host(out), want)
 
 
-@pytest.mark.parametrize("bdt,gdt", [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.BF16, o.F32)])
+@pytest.mark.parametrize(
+    "bdt,gdt",
+    [(o.F32, o.F32), (o.BF16, o.BF16), (o.F32, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F32, o.F16),
+     (o.F16, o.F32), (o.BF16, o.F16), (o.F16, o.BF16)],
+)
 @pytest.mark.parametrize("W", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("inv_scale,write_out", [(1.0, True), (2.0**-16, True), (1.0 / 3, False)])
 def test_allreduce_unpack_matches_oracle(rng, bdt, gdt, W, inv_scale, write_out):
@@ -263,7 +292,7 @@ def test_allreduce_unpack_matches_oracle(rng, bdt, gdt, W, inv_scale, write_out)
         got = to_host(g)
         assert same_bits(got[s : s + n], v), first_mismatch(got[s : s + n], v)
         sent = np.concatenate([got[:s], got[s + n :]])
-        assert np.all(sent == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32))
+        assert np.all(sent == SENTINEL[gdt])
     got_out = to_host(reps[rank])
     assert same_bits(got_out, want_out if write_out else before), first_mismatch(got_out, want_out)
     for r in range(W):
@@ -286,7 +315,9 @@ def test_allreduce_unpack_rejects_grad_overlapping_a_replica():
 
 @pytest.mark.parametrize(
     "idt,rdt,sdt",
-    [(o.BF16, o.F32, o.F32), (o.F32, o.F32, o.F32), (o.BF16, o.BF16, o.F32), (o.BF16, o.F32, o.BF16), (o.F32, o.BF16, o.BF16)],
+    [(o.BF16, o.F32, o.F32), (o.F32, o.F32, o.F32), (o.BF16, o.BF16, o.F32), (o.BF16, o.F32, o.BF16),
+     (o.F32, o.BF16, o.BF16), (o.F16, o.F32, o.F32), (o.F16, o.F16, o.F32), (o.F16, o.F32, o.F16),
+     (o.F16, o.F16, o.F16), (o.F32, o.F16, o.F32), (o.BF16, o.F16, o.BF16), (o.F16, o.BF16, o.F32)],
 )
 @pytest.mark.parametrize("W,rank", [(1, 0), (2, 1), (3, 2), (4, 0), (8, 5)])
 @pytest.mark.parametrize("accumulate", [False, True])
@@ -354,23 +385,58 @@ def test_cast_matches_golden_and_ties():
         assert np.array_equal(to_host(dst), want), first_mismatch(to_host(dst), want)
 
 
+def _cast_f16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 through the pack entry point (one span, scale 1): the gather cast for
+    param_dtype = float16.  Returns the fp16 bit patterns."""
+    src = to_dev(np.ascontiguousarray(x))
+    dst = empty_dev(x.size, o.F16)
+    nat.pack(nat.spans_array([(src.data_ptr(), dst.data_ptr(), x.size)]), nat.MDX_F32, nat.MDX_F16, 1.0, False,
+             stream())
+    return to_host(dst).view(np.uint16)
+
+
+def test_cast_f16_structured_sweep():
+    """Every (sign, exponent, top-14 mantissa) pattern x low bits deciding ties from bit 9 up,
+    NaN bits included, against the oracle's integer restatement."""
+    hi = np.arange(1 << 23, dtype=np.uint32) << np.uint32(9)
+    lows = np.array([0x000, 0x001, 0x0FF, 0x100, 0x101, 0x1FF], dtype=np.uint32)
+    x = (hi[:, None] | lows[None, :]).reshape(-1).view(np.float32)
+    got = _cast_f16(x)
+    want = o.f16_from_f32(x).view(np.uint16)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_cast_f16_matches_golden():
+    d = load_golden("f16_cast.npz")
+    got = _cast_f16(d["x_bits"].view(np.float32))
+    assert np.array_equal(got, d["y_bits"]), first_mismatch(got, d["y_bits"])
+
+
 # ---------------------------------------------------------------------------
 # Golden replays through the raw ABI
 # ---------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz"])
+TORCH = {o.F32: torch.float32, o.BF16: torch.bfloat16, o.F16: torch.float16}
+
+
+def _golden_dtype(name) -> str:
+    name = str(name)
+    return o.BF16 if "bfloat16" in name else (o.F16 if "float16" in name else o.F32)
+
+
+@pytest.mark.parametrize("name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz", "ddp_f16_w4_inf.npz"])
 def test_golden_ddp_replay(name):
     d = load_golden(name)
     W, rank = int(d["W"]), int(d["rank"])
     numels = [int(n) for n in d["numels"]]
-    dt = o.BF16 if "bfloat16" in str(d["dtype"]) else o.F32
+    dt = _golden_dtype(d["dtype"])
     layout = json.loads(str(d["layout"]))
     scale = float(d["scale"])
     flag = torch.zeros(1, dtype=torch.int32, device=DEV)
     for b, idxs in enumerate(layout):
         bn = sum(numels[i] for i in idxs)
-        reps = [torch.zeros(bn + 8, dtype=torch.float32 if dt == o.F32 else torch.bfloat16, device=DEV) for _ in range(W)]
+        reps = [torch.zeros(bn + 8, dtype=TORCH[dt], device=DEV) for _ in range(W)]
         keep = []
         for r in range(W):
             rows, off = [], 0
@@ -454,7 +520,10 @@ def test_pack_and_unpack_planned_match_direct(rng):
     assert bool(flag.item()) == bad
 
 
-@pytest.mark.parametrize("W,bdt,gdt", [(8, o.F32, o.F32), (4, o.F32, o.BF16), (3, o.BF16, o.BF16)])
+@pytest.mark.parametrize(
+    "W,bdt,gdt",
+    [(8, o.F32, o.F32), (4, o.F32, o.BF16), (3, o.BF16, o.BF16), (4, o.F16, o.F16), (8, o.F32, o.F16)],
+)
 def test_allreduce_unpack_planned_matches_oracle(rng, W, bdt, gdt):
     numels = [int(x) for x in rng.integers(1, 5000, 120)]
     offs, off = [], 0
@@ -484,9 +553,9 @@ def test_allreduce_unpack_planned_matches_oracle(rng, W, bdt, gdt):
 # ---------------------------------------------------------------------------
 
 
-def _wide_want(reps_host, a, n, W, gdt, inv_scale):
-    """The reference chain for an fp32 bucket of bf16 gradients: copy_ (widen), mul_(1/W), SUM, copy_, mul_."""
-    xs = [o.mul_scalar(o.convert(h[a : a + n], o.BF16, o.F32), o.F32, 1.0 / W) for h in reps_host]
+def _wide_want(reps_host, a, n, W, gdt, inv_scale, wdt=o.BF16):
+    """The reference chain for an fp32 bucket of 16-bit gradients: copy_ (widen), mul_(1/W), SUM, copy_, mul_."""
+    xs = [o.mul_scalar(o.convert(h[a : a + n], wdt, o.F32), o.F32, 1.0 / W) for h in reps_host]
     acc = o.allreduce_sum(xs, o.F32)
     v = o.convert(acc, o.F32, gdt)
     if inv_scale != 1.0:
@@ -494,17 +563,18 @@ def _wide_want(reps_host, a, n, W, gdt, inv_scale):
     return acc, v
 
 
-@pytest.mark.parametrize("gdt", [o.BF16, o.F32])
+@pytest.mark.parametrize("wdt,gdt", [(o.BF16, o.BF16), (o.BF16, o.F32), (o.F16, o.F16), (o.F16, o.F32),
+                                     (o.BF16, o.F16)])
 @pytest.mark.parametrize("W", [1, 2, 3, 8, 16])
 @pytest.mark.parametrize("inv_scale,write_out", [(1.0, True), (2.0**-12, True), (1.0 / 3, False)])
-def test_allreduce_unpack_wide_matches_oracle(rng, gdt, W, inv_scale, write_out):
+def test_allreduce_unpack_wide_matches_oracle(rng, wdt, gdt, W, inv_scale, write_out):
     numels = [1, 7, 64, 4096, 3, 12345, 256, 5, 8, 9]
     offs, off = [], 3
     for n in numels:
         offs.append(off)
         off += n + int(rng.integers(0, 3))
     extent = off + 4
-    reps_host = [values(rng, extent, o.BF16, scale=1e3) for _ in range(W)]
+    reps_host = [values(rng, extent, wdt, scale=1e3) for _ in range(W)]
     reps = [to_dev(h) for h in reps_host]
     out = empty_dev(extent, o.F32)
     out_before = to_host(out)
@@ -515,19 +585,19 @@ def test_allreduce_unpack_wide_matches_oracle(rng, gdt, W, inv_scale, write_out)
     )
     flag = torch.zeros(1, dtype=torch.int32, device=DEV)
     nat.allreduce_unpack_wide(
-        [r.data_ptr() for r in reps], nat.MDX_BF16, runs, out.data_ptr() if write_out else None, nat.MDX_F32,
+        [r.data_ptr() for r in reps], code(wdt), runs, out.data_ptr() if write_out else None, nat.MDX_F32,
         code(gdt), nat.f32(1.0 / W), nat.f32(inv_scale), flag.data_ptr(), stream(),
     )
     any_bad = False
     want_out = out_before.copy()
     for a, n, g, s in zip(offs, numels, grads, shifts, strict=True):
-        acc, v = _wide_want(reps_host, a, n, W, gdt, inv_scale)
+        acc, v = _wide_want(reps_host, a, n, W, gdt, inv_scale, wdt)
         want_out[a : a + n] = acc
         any_bad |= bool((~o.isfinite(v, gdt)).any())
         got = to_host(g)
         assert same_bits(got[s : s + n], v), first_mismatch(got[s : s + n], v)
         sent = np.concatenate([got[:s], got[s + n :]])
-        assert np.all(sent == (SENTINEL_BF16 if gdt == o.BF16 else SENTINEL_F32))
+        assert np.all(sent == SENTINEL[gdt])
     got_out = to_host(out)
     assert same_bits(got_out, want_out if write_out else out_before), first_mismatch(got_out, want_out)
     for r in range(W):
@@ -535,20 +605,21 @@ def test_allreduce_unpack_wide_matches_oracle(rng, gdt, W, inv_scale, write_out)
     assert bool(flag.item()) == any_bad
 
 
-@pytest.mark.parametrize("W,gdt", [(8, o.BF16), (4, o.F32), (5, o.BF16)])
-def test_allreduce_unpack_wide_planned_matches_oracle(rng, W, gdt):
+@pytest.mark.parametrize("W,wdt,gdt", [(8, o.BF16, o.BF16), (4, o.BF16, o.F32), (5, o.BF16, o.BF16),
+                                       (8, o.F16, o.F16), (3, o.F16, o.F32)])
+def test_allreduce_unpack_wide_planned_matches_oracle(rng, W, wdt, gdt):
     numels = [int(x) for x in rng.integers(1, 5000, 120)]
     offs, off = [], 0
     for n in numels:
         offs.append(off)
         off += n + int(rng.integers(0, 3))
-    reps_host = [values(rng, off, o.BF16, scale=1e3) for _ in range(W)]
+    reps_host = [values(rng, off, wdt, scale=1e3) for _ in range(W)]
     reps = [to_dev(h) for h in reps_host]
     out = empty_dev(off, o.F32)
     grads = [empty_dev(n, gdt) for n in numels]
     runs = nat.grad_runs_array([(a, n, g.data_ptr()) for a, n, g in zip(offs, numels, grads, strict=True)])
     plan = nat.plan_allreduce_unpack_wide(
-        [r.data_ptr() for r in reps], nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_F32, code(gdt),
+        [r.data_ptr() for r in reps], code(wdt), runs, out.data_ptr(), nat.MDX_F32, code(gdt),
         nat.f32(1.0 / W), DEV,
     )
     flag = torch.zeros(1, dtype=torch.int32, device=DEV)
@@ -557,7 +628,7 @@ def test_allreduce_unpack_wide_planned_matches_oracle(rng, W, gdt):
         got_out = to_host(out)
         bad = False
         for a, n, g in zip(offs, numels, grads, strict=True):
-            acc, v = _wide_want(reps_host, a, n, W, gdt, 2.0**-10)
+            acc, v = _wide_want(reps_host, a, n, W, gdt, 2.0**-10, wdt)
             bad |= bool((~o.isfinite(v, gdt)).any())
             assert same_bits(got_out[a : a + n], acc)
             assert same_bits(to_host(g), v)
@@ -570,18 +641,22 @@ def test_allreduce_unpack_wide_rejects_bad_dtypes_and_overlap():
     g = torch.zeros(16, dtype=torch.bfloat16, device=DEV)
     runs = nat.grad_runs_array([(0, 16, g.data_ptr())])
     ptrs = [r.data_ptr() for r in reps]
-    with pytest.raises(RuntimeError, match="dtype"):  # only bf16 -> fp32 widens
+    with pytest.raises(RuntimeError, match="dtype"):  # only bf16 / fp16 -> fp32 widens
         nat.allreduce_unpack_wide(ptrs, nat.MDX_F32, runs, out.data_ptr(), nat.MDX_F32, 1, 0.5, 1.0, None, stream())
     with pytest.raises(RuntimeError, match="dtype"):
         nat.allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_BF16, 1, 0.5, 1.0, None, stream())
+    with pytest.raises(RuntimeError, match="dtype"):
+        nat.allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_F16, 1, 0.5, 1.0, None, stream())
     with pytest.raises(RuntimeError, match="overlaps"):  # the fp32 bucket may not alias a bf16 row
         nat.allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, reps[0].data_ptr(), nat.MDX_F32, 1, 0.5, 1.0, None,
                                   stream())
 
 
-def test_golden_widening_replay():
-    """The fixture replays torch's chain for an fp32 bucket of bf16 grads; the wide kernel must match it."""
-    d = load_golden("ddp_bf16_f32bucket_w8.npz")
+@pytest.mark.parametrize("name", ["ddp_bf16_f32bucket_w8.npz", "ddp_f16_f32bucket_w8.npz"])
+def test_golden_widening_replay(name):
+    """The fixture replays torch's chain for an fp32 bucket of 16-bit grads; the wide kernel must match it."""
+    d = load_golden(name)
+    wdt = _golden_dtype(d["dtype"])
     W, rank = int(d["W"]), int(d["rank"])
     numels = [int(n) for n in d["numels"]]
     layout = json.loads(str(d["layout"]))
@@ -589,7 +664,7 @@ def test_golden_widening_replay():
     flag = torch.zeros(1, dtype=torch.int32, device=DEV)
     for b, idxs in enumerate(layout):
         bn = sum(numels[i] for i in idxs)
-        reps = [torch.zeros(bn + 8, dtype=torch.bfloat16, device=DEV) for _ in range(W)]
+        reps = [torch.zeros(bn + 8, dtype=TORCH[wdt], device=DEV) for _ in range(W)]
         keep = []
         for r in range(W):
             rows, off = [], 0
@@ -599,17 +674,17 @@ def test_golden_widening_replay():
                 keep.append(t)
                 rows.append((0 if t is None else t.data_ptr(), reps[r].data_ptr() + off * 2, numels[i]))
                 off += numels[i]
-            nat.pack(nat.spans_array(rows), nat.MDX_BF16, nat.MDX_BF16, 1.0, False, stream())
+            nat.pack(nat.spans_array(rows), code(wdt), code(wdt), 1.0, False, stream())
         out = empty_dev(bn, o.F32)
         grads, rows, off = [], [], 0
         for i in idxs:
-            g = empty_dev(numels[i], o.BF16)
+            g = empty_dev(numels[i], wdt)
             grads.append((i, g))
             rows.append((off, numels[i], g.data_ptr()))
             off += numels[i]
         nat.allreduce_unpack_wide(
-            [x.data_ptr() for x in reps], nat.MDX_BF16, nat.grad_runs_array(rows), out.data_ptr(), nat.MDX_F32,
-            nat.MDX_BF16, nat.f32(1.0 / W), nat.f32(1.0 / scale), flag.data_ptr(), stream(),
+            [x.data_ptr() for x in reps], code(wdt), nat.grad_runs_array(rows), out.data_ptr(), nat.MDX_F32,
+            code(wdt), nat.f32(1.0 / W), nat.f32(1.0 / scale), flag.data_ptr(), stream(),
         )
         got = to_host(out)
         assert same_bits(got, d[f"reduced_b{b}"]), f"bucket {b}: " + first_mismatch(got, d[f"reduced_b{b}"])

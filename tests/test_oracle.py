@@ -18,6 +18,9 @@ from conftest import GOLDEN, first_mismatch, load_golden, same_bits
 from oracle import gradpath as o
 
 
+TORCH_DTYPE = {o.F32: torch.float32, o.BF16: torch.bfloat16, o.F16: torch.float16}
+
+
 def _torch_bits(t: torch.Tensor) -> np.ndarray:
     if t.dtype == torch.bfloat16:
         return t.view(torch.int16).numpy().astype(np.uint16)
@@ -27,7 +30,14 @@ def _torch_bits(t: torch.Tensor) -> np.ndarray:
 def _from_bits(a: np.ndarray, dtype: str) -> torch.Tensor:
     if dtype == o.BF16:
         return torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16)
+    if dtype == o.F16:
+        return torch.from_numpy(np.asarray(a, dtype=np.float16).copy())
     return torch.from_numpy(np.asarray(a, dtype=np.float32).copy())
+
+
+def _golden_dtype(name) -> str:
+    name = str(name)
+    return o.BF16 if "bfloat16" in name else (o.F16 if "float16" in name else o.F32)
 
 
 # ---------------------------------------------------------------------------
@@ -67,6 +77,90 @@ def test_bf16_widening_is_exact_roundtrip():
 
 
 # ---------------------------------------------------------------------------
+# fp16 conversion
+# ---------------------------------------------------------------------------
+
+
+def _f16_cases() -> tuple[np.ndarray, np.ndarray]:
+    """Hand-built fp32 inputs with their fp16 answers, worked out from the format:
+    ties at mantissa bit 12 (normal) or at the subnormal quantum, the overflow
+    threshold 65520, the smallest subnormal, signed zero, inf and NaN."""
+    cases = [
+        (0x3F800000, 0x3C00),  # 1.0
+        (0x3F801000, 0x3C00),  # 1 + half ulp: tie -> even (0x3C00)
+        (0x3F803000, 0x3C02),  # 1 + 1.5 ulp: tie -> even (0x3C02)
+        (0x3F801001, 0x3C01),  # just above the tie rounds up
+        (0x3F800FFF, 0x3C00),  # just below the tie rounds down
+        (0x477FE000, 0x7BFF),  # 65504, the largest finite fp16
+        (0x477FEFFF, 0x7BFF),  # just below 65520 stays finite
+        (0x477FF000, 0x7C00),  # 65520: tie between 65504 and 2^16 -> even = inf
+        (0x7F7FFFFF, 0x7C00),  # FLT_MAX -> inf
+        (0x38800000, 0x0400),  # 2^-14, smallest normal
+        (0x387FC000, 0x03FF),  # 2^-14 - 2^-24: the largest subnormal, exact
+        (0x387FD000, 0x03FF),  # 2^-14 - 3 * 2^-26: below the tie rounds down
+        (0x387FE000, 0x0400),  # 2^-14 - 2^-25: tie between 0x3FF and 0x400 -> even (0x400)
+        (0x387FF000, 0x0400),  # 2^-14 - 2^-26: above the tie rounds up
+        (0x33800000, 0x0001),  # 2^-24, the smallest subnormal
+        (0x33000000, 0x0000),  # 2^-25: tie between 0 and 2^-24 -> even (0)
+        (0x33000001, 0x0001),  # just above 2^-25 rounds up
+        (0x33C00000, 0x0002),  # 1.5 * 2^-24: tie -> even (2)
+        (0x34200000, 0x0002),  # 2.5 * 2^-24: tie -> even (2)
+        (0x00000001, 0x0000),  # fp32 subnormal -> +0
+        (0x80000000, 0x8000),  # -0
+        (0xC0000000, 0xC000),  # -2
+        (0x7F800000, 0x7C00),  # +inf
+        (0xFF800000, 0xFC00),  # -inf
+        (0x7FC00000, 0x7E00),  # qNaN
+        (0xFFC12345, 0xFE09),  # negative NaN: sign and top mantissa bits kept, quieted
+        (0x7F800001, 0x7E00),  # sNaN with a low payload: quieted, payload bits below 13 dropped
+    ]
+    x = np.array([c[0] for c in cases], dtype=np.uint32).view(np.float32)
+    y = np.array([c[1] for c in cases], dtype=np.uint16)
+    return x, y
+
+
+def test_f16_hand_built_ties_and_specials():
+    x, want = _f16_cases()
+    got = o.f16_from_f32(x).view(np.uint16)
+    assert np.array_equal(got, want), first_mismatch(got, want)
+    t = x.copy()
+    assert np.array_equal(_torch_bits(torch.from_numpy(t).to(torch.float16)).view(np.uint16), want)
+
+
+def test_f16_matches_golden_fixture():
+    d = load_golden("f16_cast.npz")
+    got = o.f16_from_f32(d["x_bits"].view(np.float32)).view(np.uint16)
+    assert np.array_equal(got, d["y_bits"]), first_mismatch(got, d["y_bits"])
+
+
+def test_f16_structured_sweep_matches_torch_and_numpy():
+    """Every (sign, exponent, top-14 mantissa) pattern x low bits that decide ties at
+    any position from mantissa bit 9 up (normal results tie at bit 12, subnormal
+    ones at bits 13-23)."""
+    hi = np.arange(1 << 23, dtype=np.uint32) << np.uint32(9)
+    lows = np.array([0x000, 0x001, 0x0FF, 0x100, 0x101, 0x1FF], dtype=np.uint32)
+    for part in np.array_split(hi, 8):
+        u = (part[:, None] | lows[None, :]).reshape(-1)
+        x = u.view(np.float32)
+        got = o.f16_from_f32(x).view(np.uint16)
+        want = _torch_bits(torch.from_numpy(x.copy()).to(torch.float16)).view(np.uint16)
+        assert np.array_equal(got, want), first_mismatch(got, want)
+        nan = np.isnan(x)
+        with np.errstate(over="ignore"):
+            lib = x[~nan].astype(np.float16).view(np.uint16)
+        assert np.array_equal(got[~nan], lib)
+
+
+def test_f16_widening_is_exact_roundtrip():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    f = o.f32_from_f16(h)
+    nan = np.isnan(f)
+    assert np.array_equal(o.f16_from_f32(f).view(np.uint16)[~nan], h.view(np.uint16)[~nan])
+    # torch widens alike; it also quiets signalling NaNs, whose payloads no test compares
+    assert same_bits(f, _torch_bits(torch.from_numpy(h.copy()).float()))
+
+
+# ---------------------------------------------------------------------------
 # Scalar ops vs torch CPU (the ATen ops the reference calls)
 # ---------------------------------------------------------------------------
 
@@ -79,7 +173,7 @@ def _random_with_specials(rng, n: int) -> np.ndarray:
     return x
 
 
-@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16, o.F16])
 @pytest.mark.parametrize("scale", [1.0 / 8, 1.0 / 3, 1.0 / 7, 2.0**-16, 1e-3])
 def test_mul_scalar_matches_torch(rng, dtype, scale):
     x = o.from_f32(_random_with_specials(rng, 20000), dtype)
@@ -88,7 +182,7 @@ def test_mul_scalar_matches_torch(rng, dtype, scale):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16, o.F16])
 @pytest.mark.parametrize("w", [2, 3, 5, 8])
 def test_div_scalar_matches_torch(rng, dtype, w):
     x = o.from_f32(_random_with_specials(rng, 20000), dtype)
@@ -97,23 +191,23 @@ def test_div_scalar_matches_torch(rng, dtype, w):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("src,dst", [(o.F32, o.BF16), (o.BF16, o.F32), (o.F32, o.F32), (o.BF16, o.BF16)])
+@pytest.mark.parametrize("src", [o.F32, o.BF16, o.F16])
+@pytest.mark.parametrize("dst", [o.F32, o.BF16, o.F16])
 def test_convert_matches_torch_copy(rng, src, dst):
     x = o.from_f32(_random_with_specials(rng, 20000), src)
     got = o.convert(x, src, dst)
-    tdt = torch.bfloat16 if dst == o.BF16 else torch.float32
-    want = _torch_bits(torch.empty(x.size, dtype=tdt).copy_(_from_bits(x, src)))
+    want = _torch_bits(torch.empty(x.size, dtype=TORCH_DTYPE[dst]).copy_(_from_bits(x, src)))
     assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("dtype", [o.F32, o.BF16])
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16, o.F16])
 @pytest.mark.parametrize("W", [2, 3, 8, 16])
 def test_allreduce_sum_matches_torch_sequential_add(rng, dtype, W):
     contribs = [o.from_f32(_random_with_specials(rng, 5000), dtype) for _ in range(W)]
     got = o.allreduce_sum(contribs, dtype)
     acc = _from_bits(contribs[0], dtype).clone()
     for c in contribs[1:]:
-        acc = acc + _from_bits(c, dtype) if dtype == o.BF16 else acc.add_(_from_bits(c, dtype))
+        acc = acc.add_(_from_bits(c, dtype)) if dtype == o.F32 else acc + _from_bits(c, dtype)
     assert same_bits(got, _torch_bits(acc)), first_mismatch(got, _torch_bits(acc))
 
 
@@ -147,6 +241,22 @@ def test_found_inf_sees_bf16_overflow_of_a_finite_fp32_value():
     b = o.convert(big, o.F32, o.BF16)
     _, found = o.unscale_found_inf([b], [o.BF16], 1.0)
     assert found
+
+
+def test_unscale_found_inf_f16_matches_torch(rng):
+    """fp16 gradients (the loss scaler's own format, amp.py:1-30): unscale + isfinite."""
+    grads = [o.from_f32((rng.standard_normal(n) * 3000).astype(np.float32), o.F16) for n in (40, 1000)]
+    grads[1][7] = np.float16(np.inf)
+    grads.append(o.from_f32(np.array([70000.0, 1.0], np.float32), o.F16))  # overflows to inf when cast
+    got, found = o.unscale_found_inf(grads, [o.F16] * 3, 1.0 / 1024)
+    f = torch.zeros(1)
+    for g, want in zip(grads, got, strict=True):
+        t = torch.from_numpy(g.copy()).mul_(1.0 / 1024)
+        f += (~torch.isfinite(t)).any().to(f.dtype)
+        assert same_bits(want, t.numpy())
+    assert found and bool(f.item() > 0)
+    _, clean = o.unscale_found_inf(grads[:1], [o.F16], 1.0 / 1024)
+    assert not clean
 
 
 # ---------------------------------------------------------------------------
@@ -220,18 +330,20 @@ def test_cfg_bucket_counts():
 def _golden_ddp_inputs(d):
     W, rank = int(d["W"]), int(d["rank"])
     numels = [int(n) for n in d["numels"]]
-    dt = o.BF16 if "bfloat16" in str(d["dtype"]) else o.F32
+    dt = _golden_dtype(d["dtype"])
     grads = [[d.get(f"grad_r{r}_p{i}") for i in range(len(numels))] for r in range(W)]
     return W, rank, numels, dt, grads
 
 
-@pytest.mark.parametrize(
-    "name", ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz", "ddp_bf16_f32bucket_w8.npz"]
-)
+DDP_GOLDEN = ["ddp_f32_w4.npz", "ddp_f32_w3_inf.npz", "ddp_bf16_w8.npz", "ddp_bf16_f32bucket_w8.npz",
+              "ddp_f16_w4_inf.npz", "ddp_f16_f32bucket_w8.npz"]
+
+
+@pytest.mark.parametrize("name", DDP_GOLDEN)
 def test_ddp_pipeline_matches_golden(name):
     d = load_golden(name)
     W, rank, numels, dt, grads = _golden_ddp_inputs(d)
-    bdt = o.BF16 if "bfloat16" in str(d["bucket_dtype"]) else o.F32
+    bdt = _golden_dtype(d["bucket_dtype"])
     res = o.ddp_pipeline(
         grads, [dt] * len(numels), numels, float(d["cap_mb"]), rank, 1.0 / float(d["scale"]), bucket_dtype=bdt
     )
@@ -313,15 +425,18 @@ def test_fsdp_layout_closed_form_and_invariants():
     assert len(units) == 3 + 1
 
 
-@pytest.mark.parametrize(
-    "name", ["fsdp_bf16_w4.npz", "fsdp_bf16_w3.npz", "fsdp_f32_w2.npz", "fsdp_bf16red_w4.npz"]
-)
+FSDP_GOLDEN = ["fsdp_bf16_w4.npz", "fsdp_bf16_w3.npz", "fsdp_f32_w2.npz", "fsdp_bf16red_w4.npz",
+               "fsdp_f16_w4.npz", "fsdp_f16red_w3.npz"]
+
+
+@pytest.mark.parametrize("name", FSDP_GOLDEN)
 def test_fsdp_reduce_scatter_and_cast_match_golden(name):
     d = load_golden(name)
     W = int(d["W"])
     numels = [int(n) for n in d["numels"]]
-    gdt = o.BF16 if "bfloat16" in str(d["grad_dtype"]) else o.F32
-    rdt = o.BF16 if "bfloat16" in str(d["reduce_dtype"]) else o.F32
+    gdt = _golden_dtype(d["grad_dtype"])
+    rdt = _golden_dtype(d["reduce_dtype"])
+    cdt = _golden_dtype(d["cast_dtype"]) if "cast_dtype" in d else o.BF16
     grads = [[d.get(f"grad_r{r}_p{i}") for i in range(len(numels))] for r in range(W)]
     S = int(d["S"])
     for rank in range(W):
@@ -329,8 +444,8 @@ def test_fsdp_reduce_scatter_and_cast_match_golden(name):
         assert same_bits(got, d[f"shard_grad_r{rank}"]), first_mismatch(got, d[f"shard_grad_r{rank}"])
         acc = o.fsdp_reduce_scatter_share(grads, gdt, numels, rank, rdt, o.F32, existing=d[f"prev_r{rank}"])
         assert same_bits(acc, d[f"shard_grad_acc_r{rank}"])
-        cast = o.fsdp_gather_cast(d["master_flat"][rank * S : (rank + 1) * S], o.BF16)
-        assert np.array_equal(cast, d[f"gather_cast_r{rank}"])
+        cast = o.fsdp_gather_cast(d["master_flat"][rank * S : (rank + 1) * S], cdt)
+        assert same_bits(cast, d[f"gather_cast_r{rank}"])
 
 
 def test_fsdp_world1_is_plain_flatten(rng):

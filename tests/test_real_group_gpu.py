@@ -130,10 +130,10 @@ class Flat(nn.Module):
 
 
 def odt(dtype: torch.dtype) -> str:
-    return o.BF16 if dtype == torch.bfloat16 else o.F32
+    return {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(dtype, o.F32)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("W,rank,cap", [(2, 1, 25.0), (4, 2, 0.01), (8, 5, 1e-6), (3, 0, 0.004)])
 @pytest.mark.parametrize("inject", [False, True])
 def test_ddp_real_group_path(fake_dist, rng, dtype, W, rank, cap, inject):
@@ -151,7 +151,8 @@ def test_ddp_real_group_path(fake_dist, rng, dtype, W, rank, cap, inject):
     if inject:
         r_inf = (rank + 1) % W
         grads[r_inf][3] = grads[r_inf][3].copy()
-        grads[r_inf][3][0] = np.float32(np.inf) if dtype == torch.float32 else np.uint16(0x7F80)
+        grads[r_inf][3][0] = {torch.float32: np.float32(np.inf), torch.bfloat16: np.uint16(0x7F80),
+                              torch.float16: np.float16(np.inf)}[dtype]
     ddp.allocate_buckets()
     index = {id(p): i for i, p in enumerate(model.parameters())}
     for bucket in ddp._buckets:
