@@ -252,14 +252,60 @@ def test_sgd_steps_track_full_batch(W, rank):
         assert rel <= 1e-5, f"unit {unit.name}: {rel:.3e}"
 
 
-def test_bf16_params_track_fp32_training():
+@pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float16])
+def test_low_precision_params_track_fp32_training(param_dtype):
     """Reference tests/test_fsdp.py:189-211: bf16 gathered parameters with fp32 reduction keep the
-    loss within 0.05 of fp32 training, and the master shard stays fp32."""
-    fsdp, _, _, bf16 = _sgd_run(2, 0, torch.bfloat16)
+    loss within 0.05 of fp32 training, and the master shard stays fp32; likewise fp16, the
+    reference trainer's --fsdp-param-dtype fp16."""
+    fsdp, _, _, low = _sgd_run(2, 0, param_dtype)
     _, _, _, fp32 = _sgd_run(2, 0, torch.float32)
-    for (mine, _), (want, _) in zip(bf16, fp32, strict=True):  # this rank's loss on its chunk, both runs
+    for (mine, _), (want, _) in zip(low, fp32, strict=True):  # this rank's loss on its chunk, both runs
         assert abs(mine - want) <= 0.05
     assert all(u.flat_shard.dtype == torch.float32 for u in fsdp._units)
+
+
+@pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("W,rank", [(2, 1), (4, 3)])
+def test_keep_low_precision_shard(param_dtype, W, rank):
+    """MixedPrecisionPolicy(keep_low_precision_shard=True) (fsdp.py:138-140): the master shard is
+    kept in param_dtype, unshard gathers it without a cast, and reduce_scatter_grads rounds the
+    fp32 reduction to param_dtype (fsdp.py:233) and accumulates in it (fsdp.py:237)."""
+    odt = o.BF16 if param_dtype == torch.bfloat16 else o.F16
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c).to(DEV)
+    init = {n: p.detach().clone() for n, p in model.named_parameters()}
+    names = {id(p): n for n, p in model.named_parameters()}
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32, keep_low_precision_shard=True)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy)
+    rng = np.random.default_rng(21 + W)
+    for unit in fsdp._units:
+        assert unit.flat_shard.dtype == param_dtype
+        S, P = unit.shard_numel, unit.padded_numel
+        flat = np.zeros(P, np.float32)
+        flat[: unit.total_numel] = np.concatenate([init[names[id(p)]].cpu().numpy().reshape(-1) for p in unit.params])
+        want_shard = o.from_f32(flat[rank * S : (rank + 1) * S], odt)
+        assert same_bits(host_bits(unit.flat_shard), want_shard)
+        unit.unshard()
+        assert same_bits(host_bits(unit._full[rank * S : (rank + 1) * S]), want_shard)
+        existing = None
+        for _ in range(2):  # set, then accumulate in param_dtype
+            grads = [[o.from_f32((rng.standard_normal(n) * 1e-3).astype(np.float32), odt) for n in unit.numels]
+                     for _ in range(W)]
+            peers = unit.peer_grad_contributions()
+            for r in range(W):
+                if r != rank:
+                    peers[r].copy_(torch.from_numpy(o.fsdp_flatten(grads[r], odt, unit.numels, P, odt).view(
+                        np.int16 if odt == o.BF16 else np.float16).copy()).to(DEV).view(param_dtype))
+            for p, g in zip(unit.params, grads[rank], strict=True):
+                t = torch.from_numpy(g.view(np.int16) if odt == o.BF16 else g.copy())
+                p.grad = t.to(DEV).view(param_dtype).view(p.shape)
+            unit.reduce_scatter_grads()
+            want = o.fsdp_reduce_scatter_share(grads, odt, unit.numels, rank, o.F32, odt, existing=existing)
+            got = host_bits(unit.flat_shard.grad)
+            assert unit.flat_shard.grad.dtype == param_dtype
+            assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
+            existing = want
+        unit.reshard()
 
 
 def test_dropped_fsdp_frees_its_buffers():
