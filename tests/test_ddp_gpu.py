@@ -596,3 +596,54 @@ def test_reduce_dtype_on_matching_params_is_the_plain_path(rng):
     want = o.ddp_pipeline(grads, [o.F32] * 3, [int(np.prod(s)) for s in shapes], 0.01, rank, None)
     for i, p in enumerate(model.parameters()):
         assert same_bits(host_bits(p.grad), want["grads"][i])
+
+
+class MixedFlat(nn.Module):
+    """Parameters whose dtypes cycle through fp32, bf16 and fp16 (a partially cast model)."""
+
+    DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+    def __init__(self, shapes, offset=0):
+        super().__init__()
+        self.ps = nn.ParameterList([
+            nn.Parameter(torch.zeros(s, dtype=self.DTYPES[(i + offset) % 3], device=DEV)) for i, s in enumerate(shapes)
+        ])
+
+
+@pytest.mark.parametrize("W,rank", [(2, 0), (4, 3), (8, 5)])
+@pytest.mark.parametrize("cap", [1e-6, 0.004, 1e6])
+@pytest.mark.parametrize("offset", [0, 1, 2])
+def test_mixed_dtype_buckets_bitwise(rng, W, rank, cap, offset):
+    """A bucket takes its first parameter's dtype (ddp.py:83-84); every other gradient is cast into it on
+    pack (`copy_`, ddp.py:90) and back on unpack (ddp.py:100-101), then unscaled in its own dtype."""
+    shapes = [(33,), (64, 8), (5,), (130,), (1,), (7, 9), (256, 4), (3,), (500,), (2, 2)]
+    S = 2.0**8
+    model = MixedFlat(shapes, offset)
+    dtypes = [p.dtype for p in model.parameters()]
+    scaler = DistributedGradScaler(init_scale=S)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, grad_scaler=scaler)
+    grads = []
+    for r in range(W):
+        grads.append([o.from_f32((rng.standard_normal(int(np.prod(s))) * 1e-2 * S).astype(np.float32), odt(d))
+                      for s, d in zip(shapes, dtypes, strict=True)])
+    dts = [odt(d) for d in dtypes]
+    stage_peers(ddp, grads, dts, rank, W)
+    for p, g in zip(model.parameters(), grads[rank], strict=True):
+        p.grad = dev_from(g, p.shape)
+    ddp.finish_gradient_sync()
+
+    class _Opt:
+        param_groups = [{"params": list(model.parameters())}]
+
+    found = scaler.unscale_(_Opt())
+    want = o.ddp_pipeline(grads, dts, [int(np.prod(s)) for s in shapes], cap, rank, 1.0 / S)
+    if cap == 1e6:
+        assert len({b.dtype for b in ddp._buckets}) == 1 and len(ddp._buckets) == 1
+    for i, p in enumerate(model.parameters()):
+        assert p.grad.dtype == dtypes[i]
+        got = host_bits(p.grad)
+        assert same_bits(got, want["grads"][i]), f"param {i} ({dtypes[i]}): " + first_mismatch(got, want["grads"][i])
+    for b, bucket in enumerate(ddp._buckets):
+        assert bucket.buffer.dtype == bucket.params[0].dtype
+        assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"bucket {b}"
+    assert found == want["found_inf"]
