@@ -224,7 +224,7 @@ class DistributedGradScaler:
             and comm.is_distributed()
             and comm.get_world_size(self.process_group) > 1
         ):
-            dist.all_reduce(flag, op=dist.ReduceOp.MAX, group=self.process_group)
+            comm.dist_all_reduce(flag, op=dist.ReduceOp.MAX, group=self.process_group)
 
         self._found_inf_this_step = bool(flag.item() > 0)
         self._unscaled = True

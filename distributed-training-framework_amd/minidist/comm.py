@@ -6,7 +6,9 @@ collective wrappers :223-277), so callers and the accounting formulas are
 unchanged.  What changes is what sits under the collective hook:
 
 * With a real ``torch.distributed`` group the wrappers forward to
-  ``dist.*`` exactly as the reference does (RCCL on ROCm devices).
+  ``dist.*`` exactly as the reference does (RCCL on ROCm devices).  A gloo
+  group moves host memory: a device tensor handed to one of its collectives
+  is staged through the host with synchronous copies (``dist_*`` below).
 * With a :class:`ResidentGroup` -- W data-parallel replicas emulated on ONE
   GPU -- the peers' contributions are already resident in this GPU's HBM
   (symmetric buffers, one row per replica) and the reduction arithmetic runs
@@ -518,8 +520,72 @@ def _nbytes(t: torch.Tensor) -> int:
     return t.numel() * t.element_size()
 
 
-_all_gather_single = getattr(dist, "all_gather_single", None) or dist.all_gather_into_tensor
-_reduce_scatter_single = getattr(dist, "reduce_scatter_single", None) or dist.reduce_scatter_tensor
+# --------------------------------------------------------------------------
+# torch.distributed calls of this package.  RCCL (and NCCL) collectives take
+# device tensors as they are.  gloo moves host memory: a device tensor is
+# copied to the host (a synchronous copy, which also waits for the kernels
+# that produced it), the collective runs there synchronously, and the result
+# is copied back in the current stream's order.  The Work returned for
+# async_op is then already complete.
+# --------------------------------------------------------------------------
+
+
+class _CompletedWork:
+    def wait(self, timeout=None) -> bool:
+        return True
+
+    def is_completed(self) -> bool:
+        return True
+
+
+def _via_host(tensor: torch.Tensor, group) -> bool:
+    return tensor.is_cuda and dist.get_backend(group) == "gloo"
+
+
+def dist_all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op: bool = False):
+    if _via_host(tensor, group):
+        host = tensor.cpu()
+        dist.all_reduce(host, op=op, group=group)
+        tensor.copy_(host)
+        return _CompletedWork() if async_op else None
+    return dist.all_reduce(tensor, op=op, group=group, async_op=async_op)
+
+
+def dist_broadcast(tensor: torch.Tensor, src: int, group=None, async_op: bool = False):
+    if _via_host(tensor, group):
+        host = tensor.cpu()
+        dist.broadcast(host, src=src, group=group)
+        tensor.copy_(host)
+        return _CompletedWork() if async_op else None
+    return dist.broadcast(tensor, src=src, group=group, async_op=async_op)
+
+
+def dist_all_gather_into_tensor(output: torch.Tensor, input_: torch.Tensor, group=None, async_op: bool = False):
+    if _via_host(output, group):
+        host_out = torch.empty(output.shape, dtype=output.dtype)
+        dist.all_gather_into_tensor(host_out, input_.cpu(), group=group)
+        output.copy_(host_out)
+        return _CompletedWork() if async_op else None
+    return _all_gather_single(output, input_, group=group, async_op=async_op)
+
+
+def dist_reduce_scatter_tensor(
+    output: torch.Tensor, input_: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op: bool = False
+):
+    if _via_host(output, group):
+        host_out = torch.empty(output.shape, dtype=output.dtype)
+        dist.reduce_scatter_tensor(host_out, input_.cpu(), op=op, group=group)
+        output.copy_(host_out)
+        return _CompletedWork() if async_op else None
+    return _reduce_scatter_single(output, input_, op=op, group=group, async_op=async_op)
+
+
+def _all_gather_single(*args, **kwargs):
+    return (getattr(dist, "all_gather_single", None) or dist.all_gather_into_tensor)(*args, **kwargs)
+
+
+def _reduce_scatter_single(*args, **kwargs):
+    return (getattr(dist, "reduce_scatter_single", None) or dist.reduce_scatter_tensor)(*args, **kwargs)
 
 
 def all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op: bool = False):
@@ -531,7 +597,7 @@ def all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op:
         if op != dist.ReduceOp.SUM:
             raise NotImplementedError("ResidentGroup all_reduce implements SUM")
         return group.all_reduce_sum([tensor], async_op=async_op)
-    return dist.all_reduce(tensor, op=op, group=group, async_op=async_op)
+    return dist_all_reduce(tensor, op=op, group=group, async_op=async_op)
 
 
 def all_reduce_coalesced(tensors: Sequence[torch.Tensor], group=None, async_op: bool = False):
@@ -550,7 +616,7 @@ def all_reduce_coalesced(tensors: Sequence[torch.Tensor], group=None, async_op: 
         return group.all_reduce_sum(list(tensors), async_op=async_op)
     work = None
     for t in tensors:
-        work = dist.all_reduce(t, group=group, async_op=async_op)
+        work = dist_all_reduce(t, group=group, async_op=async_op)
     return work
 
 
@@ -563,7 +629,7 @@ def all_gather_into_tensor(output: torch.Tensor, input_: torch.Tensor, group=Non
     comm_stats.add("all_gather", payload, int((world - 1) / world * payload))
     if isinstance(group, ResidentGroup):
         return group.all_gather_into(output, input_, async_op=async_op)
-    return _all_gather_single(output, input_, group=group, async_op=async_op)
+    return dist_all_gather_into_tensor(output, input_, group=group, async_op=async_op)
 
 
 def reduce_scatter_tensor(
@@ -579,7 +645,7 @@ def reduce_scatter_tensor(
         if op != dist.ReduceOp.SUM:
             raise NotImplementedError("ResidentGroup reduce_scatter implements SUM")
         return group.reduce_scatter_sum(output, input_, async_op=async_op)
-    return _reduce_scatter_single(output, input_, op=op, group=group, async_op=async_op)
+    return dist_reduce_scatter_tensor(output, input_, op=op, group=group, async_op=async_op)
 
 
 def broadcast(tensor: torch.Tensor, src: int, group=None, async_op: bool = False):
@@ -588,4 +654,4 @@ def broadcast(tensor: torch.Tensor, src: int, group=None, async_op: bool = False
     comm_stats.add("broadcast", _nbytes(tensor), _nbytes(tensor))
     if isinstance(group, ResidentGroup):
         return None  # peers are staged by the caller; nothing to send
-    return dist.broadcast(tensor, src=src, group=group, async_op=async_op)
+    return dist_broadcast(tensor, src=src, group=group, async_op=async_op)

@@ -195,7 +195,7 @@ class _FSDPUnit:
                 _copy_spans(rows, self._full.dtype, self._full.dtype, self.device)
             else:
                 own = self._full[self.rank * S : (self.rank + 1) * S]
-                dist.all_gather_into_tensor(self._full, own, group=self.group)
+                comm.dist_all_gather_into_tensor(self._full, own, group=self.group)
         self._unsharded = True
 
     def reshard(self) -> None:
@@ -284,7 +284,7 @@ class _FSDPUnit:
                 float(self.world), True, stream,
             )
             red = torch.empty(self.shard_numel, dtype=reduce_dtype, device=self.device)
-            dist.reduce_scatter_tensor(red, buf, group=self.group)
+            comm.dist_reduce_scatter_tensor(red, buf, group=self.group)
             _native.reduce_scatter_share(
                 _native.pieces_array([(red.data_ptr(), 0, self.shard_numel)]), [0], 0,
                 _native.dtype_code(reduce_dtype), _native.dtype_code(reduce_dtype), False,
@@ -348,9 +348,9 @@ class FullyShardedDataParallel(nn.Module):
         src = 0 if self.process_group is None else dist.get_global_rank(self.process_group, 0)
         with torch.no_grad():
             for p in self.module.parameters():
-                dist.broadcast(p.data, src=src, group=self.process_group)
+                comm.dist_broadcast(p.data, src=src, group=self.process_group)
             for b in self.module.buffers():
-                dist.broadcast(b.data, src=src, group=self.process_group)
+                comm.dist_broadcast(b.data, src=src, group=self.process_group)
 
     def _build_units(self, root, unit_types, reshard_after_forward, reshard_root, device) -> list[_FSDPUnit]:
         """Pre-order claim of unit modules, then a root unit for leftovers (fsdp.py:315-357)."""

@@ -1,0 +1,197 @@
+"""DDP and FSDP over a real torch.distributed process group: two processes on the one GPU.
+
+Both ranks run on ``cuda:0`` and meet in a gloo group (FileStore rendezvous).
+gloo moves host memory, so minidist stages every device tensor it hands to a
+gloo collective through the host (``comm.dist_*``); everything else is the
+product path as it runs over RCCL:
+
+* DDP: the construction-time broadcast from rank 0, the gradient hooks, pack
+  (kernel) -> ``comm.all_reduce`` -> ``Work.wait`` -> unpack + fused unscale and
+  found-inf (kernel), and the scaler's MAX exchange of the flag
+  (minidist/amp.py:216-217), over two steps, the second with an overflow on
+  rank 1 only.
+* FSDP: the broadcast, the cast of the master shard into this rank's slot and
+  the in-place all-gather, and pack (kernel) -> ``reduce_scatter_tensor`` ->
+  shard epilogue (kernel).
+
+With W = 2 the backend's sum is a + b, which IEEE makes independent of order,
+so each rank's results are checked bit for bit against the oracle fed with
+both ranks' local gradients.  Those are captured by hooks registered before
+the wrapper's own, which therefore run first.
+"""
+
+from __future__ import annotations
+
+import os
+from datetime import timedelta
+
+import numpy as np
+import pytest
+import torch
+import torch.distributed as dist
+import torch.multiprocessing as mp
+
+import tiny_gpt
+from conftest import first_mismatch, same_bits
+from minidist import DDP, FSDP, DistributedGradScaler, MixedPrecisionPolicy
+from oracle import gradpath as o
+
+pytestmark = pytest.mark.gpu
+W = 2
+SCALE = 2.0**10
+CAP_MB = 0.01
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().reshape(-1).cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy().copy()
+
+
+def _worker(rank: int, kind: str, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    # a collective that one rank never joins fails after a minute instead of hanging
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=W,
+                            timeout=timedelta(seconds=60))
+    try:
+        if kind == "ddp":
+            _ddp_rank(rank, out_dir)
+        else:
+            _fsdp_rank(rank, DTYPES[kind.split("-")[1]], out_dir)
+    finally:
+        dist.destroy_process_group()
+
+
+def _ddp_rank(rank: int, out_dir: str) -> None:
+    dev = torch.device("cuda", 0)
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c, seed=rank).to(dev)  # different on each rank until DDP broadcasts rank 0's
+    params = list(model.parameters())
+    local: dict[int, torch.Tensor] = {}
+    state = {"inject": False}
+
+    def capture(p):
+        if state["inject"] and rank == 1 and p is params[3]:
+            p.grad.view(-1)[5] = float("inf")  # this rank's backward overflowed
+        local[id(p)] = p.grad.detach().clone()
+
+    for p in params:
+        p.register_post_accumulate_grad_hook(capture)
+    scaler = DistributedGradScaler(init_scale=SCALE)
+    ddp = DDP(model, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+    out = {f"init_{i}": _bits(p) for i, p in enumerate(params)}
+
+    class _Opt:
+        param_groups = [{"params": params}]
+
+    ids, tgt = tiny_gpt.batch(c, 8, seed=5)
+    for step in range(2):
+        state["inject"] = step == 1
+        for p in params:
+            p.grad = None
+        _, loss = ddp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+        scaler.scale_loss(loss).backward()
+        out[f"found_{step}"] = np.array(scaler.unscale_(_Opt()))
+        scaler.update()
+        for i, p in enumerate(params):
+            out[f"local_{step}_{i}"] = _bits(local[id(p)])
+            out[f"final_{step}_{i}"] = _bits(p.grad)
+    out["scale_after"] = np.array(scaler.scale)
+    np.savez(os.path.join(out_dir, f"ddp_r{rank}.npz"), **out)
+
+
+def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str) -> None:
+    dev = torch.device("cuda", 0)
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c, seed=rank).to(dev)
+    params = list(model.parameters())
+    index = {id(p): i for i, p in enumerate(params)}
+    local: dict[int, torch.Tensor] = {}
+
+    def capture(p):
+        local[id(p)] = p.grad.detach().clone()
+
+    for p in params:
+        p.register_post_accumulate_grad_hook(capture)
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), mixed_precision=policy)
+    out = {}
+    for u, unit in enumerate(fsdp._units):
+        out[f"unit_{u}_params"] = np.array([index[id(p)] for p in unit.params])
+        out[f"master_{u}"] = _bits(unit.flat_shard)
+    with fsdp.summon_full_params():
+        for u, unit in enumerate(fsdp._units):
+            out[f"full_{u}"] = _bits(unit._full)
+    ids, tgt = tiny_gpt.batch(c, 8, seed=6)
+    _, loss = fsdp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+    loss.backward()
+    for i, p in enumerate(params):
+        out[f"local_{i}"] = _bits(local[id(p)])
+    for u, unit in enumerate(fsdp._units):
+        out[f"shard_grad_{u}"] = _bits(unit.flat_shard.grad)
+    out["units"] = np.array(len(fsdp._units))
+    np.savez(os.path.join(out_dir, f"fsdp_r{rank}.npz"), **out)
+
+
+def _run(kind: str, tmp_path) -> list[dict]:
+    store = str(tmp_path / "store")
+    print(f"spawning 2 ranks on cuda:0 ({kind})", flush=True)
+    mp.spawn(_worker, args=(kind, store, str(tmp_path)), nprocs=W, join=True)
+    prefix = "ddp" if kind == "ddp" else "fsdp"
+    res = []
+    for r in range(W):
+        with np.load(tmp_path / f"{prefix}_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    return res
+
+
+def _rank0_init(c: tiny_gpt.Config) -> list[np.ndarray]:
+    return [p.detach().reshape(-1).numpy().copy() for p in tiny_gpt.GPT(c, seed=0).parameters()]
+
+
+def test_ddp_two_processes_bitwise(tmp_path):
+    res = _run("ddp", tmp_path)
+    c = tiny_gpt.Config(n_layer=2)
+    init0 = _rank0_init(c)
+    n = len(init0)
+    for r in range(W):  # the broadcast gave every rank rank 0's parameters
+        for i in range(n):
+            assert np.array_equal(res[r][f"init_{i}"], init0[i]), f"rank {r} param {i}"
+    numels = [a.size for a in init0]
+    for step in range(2):
+        grads = [[res[r][f"local_{step}_{i}"] for i in range(n)] for r in range(W)]
+        for rank in range(W):
+            want = o.ddp_pipeline(grads, [o.F32] * n, numels, CAP_MB, rank, 1.0 / SCALE)
+            for i in range(n):
+                got = res[rank][f"final_{step}_{i}"]
+                assert same_bits(got, want["grads"][i]), f"step {step} rank {rank} param {i}: " + first_mismatch(
+                    got, want["grads"][i])
+            # the MAX exchange makes the decision unanimous: only rank 1 overflowed in step 1
+            assert bool(res[rank][f"found_{step}"]) == want["found_inf"] == (step == 1)
+    assert all(float(res[r]["scale_after"]) == SCALE / 2 for r in range(W))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_fsdp_two_processes_bitwise(tmp_path, dtype):
+    res = _run(f"fsdp-{dtype}", tmp_path)
+    c = tiny_gpt.Config(n_layer=2)
+    init0 = _rank0_init(c)
+    pdt = o.BF16 if dtype == "bf16" else o.F32
+    n_units = int(res[0]["units"])
+    assert n_units == c.n_layer + 1
+    for u in range(n_units):
+        idx = [int(i) for i in res[0][f"unit_{u}_params"]]
+        numels = [init0[i].size for i in idx]
+        _, S, P = o.fsdp_layout(numels, W)
+        flat = np.zeros(P, np.float32)
+        flat[: sum(numels)] = np.concatenate([init0[i] for i in idx])
+        grads = [[res[r][f"local_{i}"] for i in idx] for r in range(W)]
+        gathered = o.fsdp_gather_cast(flat, pdt)
+        for rank in range(W):
+            assert np.array_equal(res[rank][f"master_{u}"], flat[rank * S : (rank + 1) * S])
+            assert same_bits(res[rank][f"full_{u}"], gathered), f"unit {u} rank {rank}: all-gather"
+            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, o.F32)
+            got = res[rank][f"shard_grad_{u}"]
+            assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)

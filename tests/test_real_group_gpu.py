@@ -107,6 +107,7 @@ def fake_dist(monkeypatch):
     monkeypatch.setattr(comm, "is_distributed", lambda: True)
     monkeypatch.setattr(dist, "get_world_size", lambda group=None: group_of(group).world)
     monkeypatch.setattr(dist, "get_rank", lambda group=None: group_of(group).rank)
+    monkeypatch.setattr(dist, "get_backend", lambda group=None: "nccl")  # device tensors go straight in
     monkeypatch.setattr(dist, "all_reduce", all_reduce)
     monkeypatch.setattr(dist, "reduce_scatter_tensor", reduce_scatter_tensor)
     monkeypatch.setattr(dist, "all_gather_into_tensor", all_gather_into_tensor)
