@@ -40,7 +40,7 @@ pytestmark = pytest.mark.gpu
 W = 2
 SCALE = 2.0**10
 CAP_MB = 0.01
-DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16}
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def _bits(t: torch.Tensor) -> np.ndarray:
@@ -56,15 +56,15 @@ def _worker(rank: int, kind: str, store: str, out_dir: str) -> None:
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=W,
                             timeout=timedelta(seconds=60))
     try:
-        if kind == "ddp":
-            _ddp_rank(rank, out_dir)
+        if kind.startswith("ddp"):
+            _ddp_rank(rank, out_dir, comm_stream=kind == "ddp-stream")
         else:
             _fsdp_rank(rank, DTYPES[kind.split("-")[1]], out_dir)
     finally:
         dist.destroy_process_group()
 
 
-def _ddp_rank(rank: int, out_dir: str) -> None:
+def _ddp_rank(rank: int, out_dir: str, comm_stream: bool) -> None:
     dev = torch.device("cuda", 0)
     c = tiny_gpt.Config(n_layer=2)
     model = tiny_gpt.GPT(c, seed=rank).to(dev)  # different on each rank until DDP broadcasts rank 0's
@@ -80,7 +80,7 @@ def _ddp_rank(rank: int, out_dir: str) -> None:
     for p in params:
         p.register_post_accumulate_grad_hook(capture)
     scaler = DistributedGradScaler(init_scale=SCALE)
-    ddp = DDP(model, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+    ddp = DDP(model, bucket_cap_mb=CAP_MB, grad_scaler=scaler, comm_stream=comm_stream)
     out = {f"init_{i}": _bits(p) for i, p in enumerate(params)}
 
     class _Opt:
@@ -139,7 +139,7 @@ def _run(kind: str, tmp_path) -> list[dict]:
     store = str(tmp_path / "store")
     print(f"spawning 2 ranks on cuda:0 ({kind})", flush=True)
     mp.spawn(_worker, args=(kind, store, str(tmp_path)), nprocs=W, join=True)
-    prefix = "ddp" if kind == "ddp" else "fsdp"
+    prefix = "ddp" if kind.startswith("ddp") else "fsdp"
     res = []
     for r in range(W):
         with np.load(tmp_path / f"{prefix}_r{r}.npz", allow_pickle=False) as d:
@@ -151,8 +151,9 @@ def _rank0_init(c: tiny_gpt.Config) -> list[np.ndarray]:
     return [p.detach().reshape(-1).numpy().copy() for p in tiny_gpt.GPT(c, seed=0).parameters()]
 
 
-def test_ddp_two_processes_bitwise(tmp_path):
-    res = _run("ddp", tmp_path)
+@pytest.mark.parametrize("comm_stream", [False, True])
+def test_ddp_two_processes_bitwise(tmp_path, comm_stream):
+    res = _run("ddp-stream" if comm_stream else "ddp", tmp_path)
     c = tiny_gpt.Config(n_layer=2)
     init0 = _rank0_init(c)
     n = len(init0)
@@ -173,12 +174,12 @@ def test_ddp_two_processes_bitwise(tmp_path):
     assert all(float(res[r]["scale_after"]) == SCALE / 2 for r in range(W))
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_fsdp_two_processes_bitwise(tmp_path, dtype):
     res = _run(f"fsdp-{dtype}", tmp_path)
     c = tiny_gpt.Config(n_layer=2)
     init0 = _rank0_init(c)
-    pdt = o.BF16 if dtype == "bf16" else o.F32
+    pdt = {"f32": o.F32, "bf16": o.BF16, "f16": o.F16}[dtype]
     n_units = int(res[0]["units"])
     assert n_units == c.n_layer + 1
     for u in range(n_units):
