@@ -58,6 +58,8 @@ def _worker(rank: int, kind: str, store: str, out_dir: str) -> None:
     try:
         if kind.startswith("ddp"):
             _ddp_rank(rank, out_dir, comm_stream=kind == "ddp-stream")
+        elif kind == "fsdp-vs-ddp":
+            _fsdp_vs_ddp_rank(rank, out_dir)
         else:
             _fsdp_rank(rank, DTYPES[kind.split("-")[1]], out_dir)
     finally:
@@ -135,6 +137,59 @@ def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str) -> None:
     np.savez(os.path.join(out_dir, f"fsdp_r{rank}.npz"), **out)
 
 
+def _train(model, rank: int, steps: int = 4, lr: float = 1e-2):
+    """SGD on this rank's chunk of seeded batches (the reference's tests/test_fsdp.py:50-62 loop)."""
+    c = tiny_gpt.Config(n_layer=2)
+    dev = torch.device("cuda", 0)
+    opt = torch.optim.SGD(model.parameters(), lr=lr)
+    losses = []
+    for step in range(steps):
+        ids, tgt = tiny_gpt.batch(c, 8, seed=100 + step)
+        opt.zero_grad(set_to_none=True)
+        _, loss = model(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    return losses
+
+
+def _fsdp_vs_ddp_rank(rank: int, out_dir: str) -> None:
+    """The reference's tests/test_fsdp.py:65-130 over a real group: DDP and FSDP (resharding after
+    forward, and not) from the same initial weights, their gradients after one backward and their
+    weights after four SGD steps."""
+    dev = torch.device("cuda", 0)
+    c = tiny_gpt.Config(n_layer=2)
+    ids, tgt = tiny_gpt.batch(c, 8, seed=99)
+    out = {}
+    ddp = DDP(tiny_gpt.GPT(c, seed=0).to(dev))
+    _, loss = ddp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+    loss.backward()
+    names = [n for n, _ in ddp.module.named_parameters()]
+    for i, p in enumerate(ddp.module.parameters()):
+        out[f"ddp_grad_{i}"] = _bits(p.grad)
+    out["ddp_losses"] = np.array(_train(ddp, rank))
+    for i, p in enumerate(ddp.module.parameters()):
+        out[f"ddp_weight_{i}"] = _bits(p)
+    for tag, reshard in (("fsdp", True), ("fsdp_keep", False)):
+        model = tiny_gpt.GPT(c, seed=0).to(dev)
+        index = {id(p): i for i, p in enumerate(model.parameters())}
+        fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), reshard_after_forward=reshard)
+        _, loss = fsdp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+        if not reshard:  # the blocks stay gathered between forward and backward
+            out[f"{tag}_blocks_gathered"] = np.array(all(u.is_unsharded for u in fsdp._units[:-1]))
+        loss.backward()
+        for u, unit in enumerate(fsdp._units):
+            out[f"{tag}_unit_{u}_params"] = np.array([index[id(p)] for p in unit.params])
+            out[f"{tag}_shard_grad_{u}"] = _bits(unit.flat_shard.grad)
+        out[f"{tag}_losses"] = np.array(_train(fsdp, rank))
+        with fsdp.summon_full_params():
+            for i, p in enumerate(model.parameters()):
+                out[f"{tag}_weight_{i}"] = _bits(p)
+        out[f"{tag}_units"] = np.array(len(fsdp._units))
+    out["n_params"] = np.array(len(names))
+    np.savez(os.path.join(out_dir, f"fsdp_r{rank}.npz"), **out)
+
+
 def _run(kind: str, tmp_path) -> list[dict]:
     store = str(tmp_path / "store")
     print(f"spawning 2 ranks on cuda:0 ({kind})", flush=True)
@@ -196,3 +251,37 @@ def test_fsdp_two_processes_bitwise(tmp_path, dtype):
             want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, o.F32)
             got = res[rank][f"shard_grad_{u}"]
             assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)
+
+
+def _close(got: np.ndarray, want: np.ndarray, tol: float) -> float:
+    """Relative error as the reference's assert_close measures it (tests/common.py:78-88)."""
+    err = float(np.abs(got.astype(np.float64) - want.astype(np.float64)).max(initial=0.0))
+    return err / max(float(np.abs(want).max(initial=0.0)), 1.0)
+
+
+def test_fsdp_matches_ddp_two_processes(tmp_path):
+    """Reference tests/test_fsdp.py:65-130 and :260: FSDP's reassembled gradient equals DDP's
+    (tolerance 1e-6), the weights agree after four SGD steps (1e-5) and the losses step by step
+    (1e-5), whether or not the blocks are resharded after forward."""
+    res = _run("fsdp-vs-ddp", tmp_path)
+    n = int(res[0]["n_params"])
+    for tag in ("fsdp", "fsdp_keep"):
+        n_units = int(res[0][f"{tag}_units"])
+        full = {}
+        for u in range(n_units):
+            idx = [int(i) for i in res[0][f"{tag}_unit_{u}_params"]]
+            sizes = [res[0][f"ddp_grad_{i}"].size for i in idx]
+            flat = np.concatenate([res[r][f"{tag}_shard_grad_{u}"] for r in range(W)])
+            off = 0
+            for i, k in zip(idx, sizes, strict=True):
+                full[i] = flat[off : off + k]
+                off += k
+        for rank in range(W):
+            for i in range(n):
+                assert _close(full[i], res[rank][f"ddp_grad_{i}"], 1e-6) <= 1e-6, f"{tag} grad {i}"
+                assert _close(res[rank][f"{tag}_weight_{i}"], res[rank][f"ddp_weight_{i}"], 1e-5) <= 1e-5, (
+                    f"{tag} rank {rank} weight {i}")
+            assert np.abs(res[rank][f"{tag}_losses"] - res[rank]["ddp_losses"]).max() < 1e-5
+        if tag == "fsdp_keep":
+            assert all(bool(res[r]["fsdp_keep_blocks_gathered"]) for r in range(W))
+
