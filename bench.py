@@ -34,6 +34,8 @@ whose replicas fit in host memory):
           reduce-scatter share per unit                  (26*S per unit)
     cfg4  Llama-7B bf16 grads, W = 8, fp32 buckets (reduce_dtype widening)
                                                          (26*N)
+    cfg3-f16, cfg4-f16   the same with fp16 in place of bf16 (the reference
+          trainer's --fsdp-param-dtype fp16; fp16 gradients)
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 10] [--no-cpu-baseline] [--workload cfg1]
 """
@@ -136,7 +138,13 @@ DDP_WORKLOADS = {
     "cfg4": dict(model="LLAMA_7B", W=8, grad_scale=1e-3, dtype="bf16", reduce_dtype="f32",
                  desc="cfg4: Llama-7B bf16 grads (291 tensors, N=6,738,415,616), W=8 bf16 contributions "
                       "(~108 GB) summed in fp32 into fp32 25 MB buckets (291), unpacked to bf16, loss scale 2^12"),
+    "cfg4-f16": dict(model="LLAMA_7B", W=8, grad_scale=1e-3, dtype="f16", reduce_dtype="f32",
+                     desc="cfg4-f16: Llama-7B fp16 grads (291 tensors, N=6,738,415,616), W=8 fp16 contributions "
+                          "(~108 GB) summed in fp32 into fp32 25 MB buckets (291), unpacked to fp16, loss scale "
+                          "2^12"),
 }
+TORCH_DTYPE_NAMES = {"f32": "float32", "bf16": "bfloat16", "f16": "float16"}
+KERNEL_TYPE_NAMES = {"f32": "float", "bf16": "bf16", "f16": "f16"}
 
 
 def bench_ddp(name: str, args) -> dict:
@@ -150,7 +158,7 @@ def bench_ddp(name: str, args) -> dict:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if cfg["model"] == "LLAMA_7B":
-        specs = wl.llama_specs(**wl.LLAMA_7B)
+        specs = wl.llama_specs(**wl.LLAMA_7B, dtype=getattr(torch, TORCH_DTYPE_NAMES[cfg["dtype"]]))
         loss_scale = 2.0**12
     else:
         specs = wl.gpt_specs(**getattr(wl, cfg["model"]))
@@ -238,7 +246,7 @@ def bench_ddp(name: str, args) -> dict:
             scaler.update()
             return found
 
-    steps = args.steps if name != "cfg4" else min(args.steps, 20)
+    steps = args.steps if not name.startswith("cfg4") else min(args.steps, 20)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -278,7 +286,8 @@ def bench_ddp(name: str, args) -> dict:
     red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
     red_avg_ms = sum(red_ms) / len(red_ms)
     red_bytes = N * (W * s_w + s_b + s_g)
-    kname = ("allreduce_wide_kernel_dev<bf16, float, bf16, 8>" if b0.widening
+    t16 = KERNEL_TYPE_NAMES[cfg["dtype"]]
+    kname = (f"allreduce_wide_kernel_dev<{t16}, float, {t16}, 8>" if b0.widening
              else f"allreduce_unpack_kernel_dev<float, float, {W}>")
     if args.staged:
         red_bytes = N * (W + 1) * s_b  # W buckets read, the sum written
@@ -341,10 +350,10 @@ def bench_ddp(name: str, args) -> dict:
 # ---------------------------------------------------------------------------
 
 
-def bench_fsdp(args) -> dict:
-    """48 FSDP units of GPT-2-XL blocks, W = 8: per unit the fp32 -> bf16 gather
-    cast into this rank's slot and the reduce-scatter share of 8 bf16 full-size
-    contributions into the fp32 shard gradient.
+def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
+    """48 FSDP units of GPT-2-XL blocks, W = 8: per unit the fp32 -> bf16 (or
+    fp16) gather cast into this rank's slot and the reduce-scatter share of 8
+    16-bit full-size contributions into the fp32 shard gradient.
 
     The two kernels of a unit take ~20 us together, far less than the Python
     around them, so the step's dispatches are enqueued behind a spin kernel and
@@ -377,7 +386,9 @@ def bench_fsdp(args) -> dict:
     with torch.no_grad():
         for p in model.parameters():
             p.copy_(torch.randn(p.shape, device=dev, generator=gen) * 0.02)
-    policy = MixedPrecisionPolicy(param_dtype=torch.bfloat16, reduce_dtype=torch.float32)
+    name = "cfg3" if param_dtype_name == "bf16" else f"cfg3-{param_dtype_name}"
+    pdt = getattr(torch, TORCH_DTYPE_NAMES[param_dtype_name])
+    policy = MixedPrecisionPolicy(param_dtype=pdt, reduce_dtype=torch.float32)
     fsdp = FSDP(model, unit_types=(Block,), process_group=ResidentGroup(W, 0, dev), mixed_precision=policy)
     units = fsdp._units
     assert len(units) == n_units
@@ -386,8 +397,8 @@ def bench_fsdp(args) -> dict:
         u.unshard()  # keep the gather buffers allocated: the step re-casts into them
         peers = u.peer_grad_contributions()
         for r in range(1, W):
-            peers[r].copy_((torch.randn(u.padded_numel, device=dev, generator=gen) * 1e-3).to(torch.bfloat16))
-        own_grads.append([(torch.randn(p.shape, device=dev, generator=gen) * 1e-3).to(torch.bfloat16)
+            peers[r].copy_((torch.randn(u.padded_numel, device=dev, generator=gen) * 1e-3).to(pdt))
+        own_grads.append([(torch.randn(p.shape, device=dev, generator=gen) * 1e-3).to(pdt)
                           for p in u.params])
     S = units[0].shard_numel
 
@@ -443,7 +454,7 @@ def bench_fsdp(args) -> dict:
     cast_avg = sum(cast_ms) / len(cast_ms)
     share_gbs = 20 * S / (share_avg * 1e-3) / 1e9
     return {
-        "metric": "FSDP unit gather-cast + reduce-scatter share HBM GB/s (% of 8 TB/s) cfg3; ms/step",
+        "metric": f"FSDP unit gather-cast + reduce-scatter share HBM GB/s (% of 8 TB/s) {name}; ms/step",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -453,12 +464,14 @@ def bench_fsdp(args) -> dict:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16->f32",
-        "data": "synthetic (master randn x 0.02, bf16 grads randn x 1e-3; peers' contributions staged in HBM)",
+        "dtype": f"{param_dtype_name}->f32",
+        "data": f"synthetic (master randn x 0.02, {param_dtype_name} grads randn x 1e-3; peers' contributions staged "
+                "in HBM)",
         "config": {
-            "workload": "cfg3: 48 FSDP units of GPT-2-XL blocks (12 tensors, 30,740,800 elements each, shard "
-                        "S=3,842,600), W=8, param bf16 / reduce fp32; per unit mdx_cast_f32_bf16 + "
-                        "mdx_reduce_scatter_share; GPU time of the step's dispatches",
+            "workload": f"{name}: 48 FSDP units of GPT-2-XL blocks (12 tensors, 30,740,800 elements each, shard "
+                        f"S=3,842,600), W=8, param {param_dtype_name} / reduce fp32; per unit the gather cast ("
+                        + ("mdx_cast_f32_bf16" if param_dtype_name == "bf16" else "mdx_pack, fp32 -> fp16")
+                        + ") + mdx_reduce_scatter_share; GPU time of the step's dispatches",
             "world": W,
             "units": n_units,
             "shard_numel": S,
@@ -470,12 +483,13 @@ def bench_fsdp(args) -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "share_kernel<bf16, float, float, 8> (mdx_reduce_scatter_share)",
+            "kernel": f"share_kernel<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
+                      "(mdx_reduce_scatter_share)",
             "achieved": round(share_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(share_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("cfg3"),
+            "traffic": measured_traffic(name),
             "bytes_per_launch": 20 * S,
             "avg_launch_ms": round(share_avg, 5),
         },
@@ -638,7 +652,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg1", choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4", "cfg1-overlap"])
+    ap.add_argument("--workload", default="cfg1",
+                    choices=["cfg0", "cfg1", "cfg2", "cfg3", "cfg4", "cfg3-f16", "cfg4-f16", "cfg1-overlap"])
     ap.add_argument("--overlap-batch", type=int, default=2, help="sequences of 1024 tokens per cfg1-overlap step")
     ap.add_argument("--overlap-modes", default="compute,serial,overlap",
                     help="cfg1-overlap modes to run (all three for the JSON line)")
@@ -677,8 +692,8 @@ def main() -> int:
         cpu = cpu_baseline(args.workload, steps[args.workload], threads)
         print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
 
-    if args.workload == "cfg3":
-        out = bench_fsdp(args)
+    if args.workload in ("cfg3", "cfg3-f16"):
+        out = bench_fsdp(args, "f16" if args.workload == "cfg3-f16" else "bf16")
     elif args.workload == "cfg1-overlap":
         out = bench_overlap(args)
     else:
