@@ -6,21 +6,23 @@ GPT-2-124M's fp32 gradients with W = 8 data-parallel replicas resident in HBM
 buckets in reverse parameter order, loss scale 2^16.  One step is
 
     DistributedDataParallel.finish_gradient_sync()
-        pack + 1/W       -> mdx_pack_planned (all 148 gradients, one dispatch)
-        W-way SUM + unpack + unscale + found-inf
-                         -> mdx_allreduce_unpack_planned (all 18 buckets, one dispatch:
-                            average written to the bucket and into every .grad)
+        pack + 1/W + W-way SUM + unpack + unscale + found-inf
+                         -> mdx_pack_allreduce_unpack_planned (all 148 gradients, 18 buckets,
+                            one dispatch: each gradient is read, packed into this rank's
+                            contribution row, summed with the 7 peers' rows in rank order;
+                            the average is written to the bucket and into every .grad)
     DistributedGradScaler.unscale_(opt) -> the found-inf flag read (the path's one host sync)
     DistributedGradScaler.update()
 
 value = the metric's algorithmic bytes of the staged pipeline, 52*N (pack 8N,
 W-way 36N, unpack 8N for fp32, W = 8), divided by the measured step time.  The
-implementation moves 48*N (the fused kernel does not read the reduced bucket
+implementation moves 44*N (the rank's own contribution is summed from
+registers instead of re-read from its row, and the reduced bucket is not read
 back); config.hbm_gbs reports that actual traffic over the same time.  The
-roofline object is for the dominant kernel, the fused W-way reduction:
-(W+2)*N*4 bytes per dispatch (W buckets read, bucket and gradients written)
-over its average HIP-event time, recorded on its own stream around every
-dispatch of the timed region.  The CPU baseline
+roofline object is for the dominant (and only) kernel: (2 + W + 1)*N*4 bytes
+per dispatch (gradients read, W-1 peer rows read, the packed row, the bucket
+and the gradients written) over its average HIP-event time, recorded on its
+own stream around every dispatch of the timed region.  The CPU baseline
 (reference op chain on torch CPU + gloo, W processes) runs first, before
 anything touches the GPU.
 
@@ -171,6 +173,9 @@ def bench_ddp(name: str, args) -> dict:
     group = ResidentGroup(W, 0, dev)
     ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler, reduce_dtype=reduce_dtype,
               capture_graphs=args.graphs)
+    # --two-dispatch: pack, then the fused all-reduce + unpack (the pipeline before the pack was fused in)
+    ddp._fuse_pack = not (args.two_dispatch or args.staged)
+    fused_pack = ddp._fuse_pack
     ddp.allocate_buckets()
     gen = torch.Generator(device=dev).manual_seed(1234)
     scale = cfg["grad_scale"] * loss_scale
@@ -193,7 +198,8 @@ def bench_ddp(name: str, args) -> dict:
     # dispatch, recorded on the stream it is launched on.
     red_events: list = []
     timing = {"on": False}
-    orig = ResidentGroup.all_reduce_unpack_planned
+    hook_name = "pack_all_reduce_unpack_planned" if fused_pack else "all_reduce_unpack_planned"
+    orig = getattr(ResidentGroup, hook_name)
 
     def timed_all_reduce(self, *a, **k):
         if not timing["on"]:
@@ -208,16 +214,27 @@ def bench_ddp(name: str, args) -> dict:
 
     # With --graphs the dispatch is replayed from a captured graph, where no host code runs
     # around it: the events then come from a separate pass of eager steps.
-    ResidentGroup.all_reduce_unpack_planned = timed_all_reduce
+    setattr(ResidentGroup, hook_name, timed_all_reduce)
 
-    def timed_sum(bufs):
+    def staged_sum() -> None:
+        """--staged: the W-way sum of the contribution rows into the buckets (one mdx_allreduce_sum)."""
+        from minidist import _native
+
+        wire, flat = ddp._arenas[(ddp._buckets[0].wire_dtype, ddp._buckets[0].dtype)]
+        rows = group.replicas(wire)
+        _native.allreduce_sum(
+            [r.data_ptr() for r in rows], _native.dtype_code(wire.dtype), [b.arena_offset for b in ddp._buckets],
+            [b.numel for b in ddp._buckets], flat.data_ptr(), torch.cuda.current_stream(dev).cuda_stream,
+        )
+
+    def timed_sum():
         """--staged: the W-way sum dispatch, with HIP events like the fused reduction's."""
         if not timing["on"]:
-            return group.all_reduce_sum(bufs)
+            return staged_sum()
         s = torch.cuda.current_stream(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        group.all_reduce_sum(bufs)
+        staged_sum()
         e1.record(s)
         red_events.append((e0, e1))
 
@@ -233,14 +250,15 @@ def bench_ddp(name: str, args) -> dict:
         # unpack from the buckets into the gradients with the scaler's unscale + found-inf.
         if cfg["reduce_dtype"] is not None:
             raise SystemExit("--staged covers the same-dtype workloads (cfg0, cfg1, cfg2)")
+        if len({(b.wire_dtype, b.dtype) for b in ddp._buckets}) != 1:
+            raise SystemExit("--staged needs every bucket in one dtype")
         plan = ddp._plan(0, len(ddp._buckets))
-        bucket_bufs = [b.buffer for b in ddp._buckets]
 
         def step() -> bool:  # noqa: F811 - the staged variant of the step above
             plan.refresh()
             plan.pack(1.0 / W)
             inv_scale, flag = scaler._begin_fused_unscale(dev, plan.param_ids)
-            timed_sum(bucket_bufs)
+            timed_sum()
             plan.unpack(inv_scale, flag)
             found = scaler.unscale_(opt)
             scaler.update()
@@ -266,36 +284,43 @@ def bench_ddp(name: str, args) -> dict:
             step()
         torch.cuda.synchronize()
     timing["on"] = False
-    ResidentGroup.all_reduce_unpack_planned = orig
+    setattr(ResidentGroup, hook_name, orig)
 
     b0 = ddp._buckets[0]
     s_w = b0.wire.element_size()
     s_b = b0.buffer.element_size()
     s_g = b0.params[0].element_size()
     ms_per_step = elapsed / steps * 1e3
+    # Fused pack: the gradient read, W-1 peer rows read, this rank's packed row, the bucket and
+    # the gradient written -- one dispatch.  Two-dispatch pipeline: the pack (gradient read, row
+    # written), then W rows read, bucket and gradient written.
+    red_bytes = (N * (2 * s_g + W * s_w + s_b) if fused_pack
+                 else N * (W * s_w + s_b + s_g))
     if b0.widening:
-        # pack: own bf16 grads -> own bf16 row (4N); fused: W bf16 rows read, fp32 bucket + bf16 grads written
         alg_bytes = N * (W * s_w + s_b + s_b + s_g)  # the configuration's accounting (26*N)
-        hbm_bytes = N * (2 * s_g + W * s_w + s_b + s_g)
+        hbm_bytes = red_bytes if fused_pack else N * (2 * s_g) + red_bytes
         alg_note = "W*N*2 + N*4 + N*4 + N*2 = 26*N (bf16 contributions, fp32 bucket, bf16 grads)"
     else:
         alg_bytes = N * (2 * s_g + (W + 3) * s_b)  # pack + W-way + unpack, staged
-        hbm_bytes = N * (s_g + s_b) + N * (W * s_b + s_b + s_g)
+        hbm_bytes = red_bytes if fused_pack else N * (s_g + s_b) + red_bytes
         alg_note = f"staged pack + W-way + unpack: N*(2*s_g + (W+3)*s_b) = {2 * s_g + (W + 3) * s_b}*N"
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
     red_avg_ms = sum(red_ms) / len(red_ms)
-    red_bytes = N * (W * s_w + s_b + s_g)
     t16 = KERNEL_TYPE_NAMES[cfg["dtype"]]
-    kname = (f"allreduce_wide_kernel_dev<{t16}, float, {t16}, 8>" if b0.widening
-             else f"allreduce_unpack_kernel_dev<float, float, {W}>")
+    if fused_pack:
+        kname = (f"allreduce_pack_kernel_dev<{t16}, float, {W}>" if b0.widening
+                 else f"allreduce_pack_kernel_dev<float, float, {W}>")
+    else:
+        kname = (f"allreduce_wide_kernel_dev<{t16}, float, {t16}, {W}>" if b0.widening
+                 else f"allreduce_unpack_kernel_dev<float, float, {W}>")
     if args.staged:
         red_bytes = N * (W + 1) * s_b  # W buckets read, the sum written
         hbm_bytes = N * (s_g + s_b) + red_bytes + N * (s_b + s_g)
         kname = f"allreduce_kernel<float, float, {W}, false> (mdx_allreduce_sum)"
     red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
 
-    traffic = None if args.staged else measured_traffic(name)
+    traffic = measured_traffic(name) if fused_pack else None
 
     return {
         "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",
@@ -327,12 +352,14 @@ def bench_ddp(name: str, args) -> dict:
             "found_inf": bool(found_any),
             "launch": "hip graph replay (capture_graphs=True)" if args.graphs else "eager dispatches",
             "pipeline": "staged: pack, W-way sum, unpack (three dispatches)" if args.staged
-                        else "pack + fused W-way sum / unpack / unscale (two dispatches)",
+                        else "pack + fused W-way sum / unpack / unscale (two dispatches)" if not fused_pack
+                        else "pack fused into the W-way sum / unpack / unscale (one dispatch)",
         },
         "roofline": {
             "bound": "hbm",
             "kernel": kname if args.staged else
-                      f"{kname} (mdx_allreduce_unpack_planned, all {len(ddp._buckets)} buckets in one dispatch)",
+                      f"{kname} ({'mdx_pack_allreduce_unpack_planned' if fused_pack else 'mdx_allreduce_unpack_planned'}"
+                      f", all {len(ddp._buckets)} buckets in one dispatch)",
             "achieved": round(red_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -661,6 +688,9 @@ def main() -> int:
     ap.add_argument("--staged", action="store_true",
                     help="DDP workloads: time the reference's staged pipeline (pack, W-way sum, unpack as three "
                          "dispatches) instead of the fused one, for comparison")
+    ap.add_argument("--two-dispatch", action="store_true",
+                    help="DDP workloads: pack, then the fused all-reduce + unpack, as two dispatches (the pipeline "
+                         "before the pack was fused into the reduction), for comparison")
     ap.add_argument("--graphs", action="store_true",
                     help="DDP workloads: replay each step's launches from a captured HIP graph (capture_graphs=True)")
     ap.add_argument("--cpu-steps", type=int, default=20)

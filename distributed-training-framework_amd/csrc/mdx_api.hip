@@ -96,10 +96,12 @@ int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool
 }
 
 // `grads` (may be NULL) adds each piece's gradient pointer, of `grad_size`
-// bytes per element, to the alignment requirement (fused unpack).
+// bytes per element, to the alignment requirement (fused unpack); `own_row`
+// adds replica `rank`'s row (written by the fused pack).
 template <typename Emit>
 int for_each_piece_run(const mdx_piece* pieces, void* const* grads, int n_pieces, const ReduceParams& params,
-                       int in_size, int out_size, int grad_size, int E, int U, Emit&& emit) {
+                       int in_size, int out_size, int grad_size, int E, int U, Emit&& emit,
+                       bool own_row = false) {
   const int64_t VPB = int64_t(kBlock) * U;
   const int64_t EPB = VPB * E;
   for (int i = 0; i < n_pieces; ++i) {
@@ -119,7 +121,7 @@ int for_each_piece_run(const mdx_piece* pieces, void* const* grads, int n_pieces
         sizes[np++] = in_size;
       }
       for (int r = 0; r < params.world; ++r) {
-        if (r == params.rank) continue;
+        if (r == params.rank && !own_row) continue;
         ptrs[np] = addr(params.peer[r]) + uintptr_t(pos) * uintptr_t(in_size);
         sizes[np++] = in_size;
       }
@@ -425,6 +427,78 @@ int plan_grad_runs(const void* const* replicas, int world, int dtype, int out_dt
   return build_plan(proto, gen, plan, plan_bytes);
 }
 
+// Arguments of a fused pack + all-reduce + unpack, validated.  The kernel
+// parameters are those of the fused all-reduce + unpack with replica `rank`
+// read from each run's gradient and written by the pack.
+int check_pack_fused(const void* const* replicas, int world, int rank, int dtype, int out_dtype,
+                     const mdx_pack_run* runs, int n_runs, void* out, float scale, int32_t* found_inf,
+                     int32_t* clear_flag, FusedArgs* f) {
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return MDX_EDTYPE;
+  if (dtype != out_dtype && !wide_dtypes(dtype, out_dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD || rank < 0 || rank >= world) return MDX_EWORLD;
+  if (n_runs < 0 || (n_runs > 0 && runs == nullptr) || replicas == nullptr) return MDX_EINVAL;
+  if (clear_flag != nullptr && clear_flag == found_inf) return MDX_EALIAS;
+  const int es = dtype_size(dtype), os = dtype_size(out_dtype);
+  int64_t end = 0;
+  bool any = false;
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].offset < 0 || runs[k].numel < 0 || runs[k].offset < end) return MDX_EINVAL;
+    if (runs[k].numel > 0 && runs[k].grad == nullptr) return MDX_EINVAL;
+    end = runs[k].offset + runs[k].numel;
+    any = any || runs[k].numel > 0;
+  }
+  memset(&f->p, 0, sizeof(f->p));
+  f->any = any;
+  f->p.clear = clear_flag;
+  if (!any) return MDX_OK;
+  // The pack writes row `rank` and the bucket is written beside the rows: the
+  // bucket must not overlap any replica, a gradient (read and written by the
+  // same lane) neither the replicas nor the bucket.
+  for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
+    if (out && any_overlap(replicas[r], end * es, out, end * os)) return MDX_EALIAS;
+  }
+  for (int k = 0; k < n_runs; ++k) {
+    const int64_t gb = runs[k].numel * es;
+    for (int r = 0; r < world; ++r) {
+      if (any_overlap(runs[k].grad, gb, replicas[r], end * es)) return MDX_EALIAS;
+      if (runs[k].src && any_overlap(runs[k].src, gb, replicas[r], end * es)) return MDX_EALIAS;
+    }
+    if (out && any_overlap(runs[k].grad, gb, out, end * os)) return MDX_EALIAS;
+    if (out && runs[k].src && any_overlap(runs[k].src, gb, out, end * os)) return MDX_EALIAS;
+    if (runs[k].src && runs[k].src != runs[k].grad && any_overlap(runs[k].src, gb, runs[k].grad, gb)) {
+      return MDX_EALIAS;
+    }
+  }
+  for (int r = 0; r < world; ++r) f->p.peer[r] = replicas[r];
+  f->p.out = out;
+  f->p.world = world;
+  f->p.rank = rank;
+  f->p.pre = scale;
+  f->p.inv_scale = 1.0f;
+  f->p.found_inf = found_inf;
+  f->p.flags = (dtype == out_dtype && scale != 1.0f) ? kRedPackScale : 0;
+  f->es = es;
+  f->os = os;
+  f->gs = es;
+  f->E = store_frag_elems(max_size(os, es));  // as the kernel's compile-time fragment
+  f->U = allreduce_unroll(world, f->E * es);
+  return MDX_OK;
+}
+
+// Replays the pack runs as (gradient source, gradient) runs of the kernel.
+template <typename Emit>
+int for_each_pack_run(const mdx_pack_run* runs, int n_runs, const FusedArgs& f, Emit&& emit) {
+  for (int k = 0; k < n_runs; ++k) {
+    if (runs[k].numel == 0) continue;
+    const mdx_piece pc{runs[k].src, runs[k].offset, runs[k].numel};
+    void* grad = runs[k].grad;
+    const int rc = for_each_piece_run(&pc, &grad, 1, f.p, f.es, f.os, f.gs, f.E, f.U, emit, true);
+    if (rc != MDX_OK) return rc;
+  }
+  return MDX_OK;
+}
+
 }  // namespace
 }  // namespace mdx
 
@@ -585,6 +659,30 @@ int mdx_allreduce_unpack_wide(const void* const* replicas, int world, int wire_d
   return rc != MDX_OK ? rc : flush();
 }
 
+int mdx_pack_allreduce_unpack(const void* const* replicas, int world, int rank, int wire_dtype,
+                              const mdx_pack_run* runs, int n_runs, void* out, int reduce_dtype, float scale,
+                              float inv_scale, int32_t* found_inf, int32_t* clear_flag, void* stream) {
+  FusedArgs f;
+  int rc = check_pack_fused(replicas, world, rank, wire_dtype, reduce_dtype, runs, n_runs, out, scale, found_inf,
+                            clear_flag, &f);
+  if (rc != MDX_OK) return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!f.any) return clear_flag != nullptr ? status(launch_clear_flag(clear_flag, st)) : MDX_OK;
+  f.p.inv_scale = inv_scale;
+  if (inv_scale != 1.0f) f.p.flags |= kRedUnscale;
+  PieceBatch b;
+  memset(&b, 0, sizeof(b));
+  auto flush = [&]() -> int {
+    if (b.count == 0) return MDX_OK;
+    const int r = status(launch_pack_allreduce(wire_dtype, reduce_dtype, world, b, f.p, st));
+    f.p.clear = nullptr;  // the flag clear rides on the first dispatch only
+    memset(&b, 0, sizeof(b));
+    return r;
+  };
+  rc = for_each_pack_run(runs, n_runs, f, [&](const Rec& r) { return push_piece(b, r, flush); });
+  return rc != MDX_OK ? rc : flush();
+}
+
 int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const* peers, int world,
                              int rank, int in_dtype, int reduce_dtype, int divide, void* shard,
                              int shard_dtype, int accumulate, float inv_scale, int32_t* found_inf,
@@ -682,6 +780,55 @@ int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int world, int w
   if (!wide_dtypes(wire_dtype, reduce_dtype)) return MDX_EDTYPE;
   return plan_grad_runs(replicas, world, wire_dtype, reduce_dtype, runs, n_runs, out, grad_dtype, prescale, plan,
                         plan_bytes);
+}
+
+int mdx_plan_pack_allreduce_unpack(const void* const* replicas, int world, int rank, int wire_dtype,
+                                   const mdx_pack_run* runs, int n_runs, void* out, int reduce_dtype, float scale,
+                                   void* plan, int64_t* plan_bytes) {
+  if (plan_bytes == nullptr) return MDX_EINVAL;
+  FusedArgs f;
+  const int rc = check_pack_fused(replicas, world, rank, wire_dtype, reduce_dtype, runs, n_runs, out, scale,
+                                  nullptr, nullptr, &f);
+  if (rc != MDX_OK) return rc;
+  PlanHeader proto;
+  memset(&proto, 0, sizeof(proto));
+  proto.kind = kPlanPackRuns;
+  proto.dtype_a = wire_dtype;
+  proto.dtype_b = wire_dtype;
+  proto.reduce_dtype = reduce_dtype;
+  proto.prescale = scale;
+  proto.world = world;
+  proto.rank = rank;
+  if (f.any) {
+    for (int r = 0; r < world; ++r) proto.replicas[r] = addr(replicas[r]);
+    proto.out = addr(out);
+  }
+  auto gen = [&](auto&& emit) { return f.any ? for_each_pack_run(runs, n_runs, f, emit) : MDX_OK; };
+  return build_plan(proto, gen, plan, plan_bytes);
+}
+
+int mdx_pack_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale, int32_t* found_inf,
+                                      int32_t* clear_flag, void* stream) {
+  const PlanHeader* h;
+  DevTable t;
+  const int rc = plan_view(plan, d_plan, kPlanPackRuns, &h, &t);
+  if (rc != MDX_OK) return rc;
+  if (clear_flag != nullptr && clear_flag == found_inf) return MDX_EALIAS;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (h->count == 0) return clear_flag != nullptr ? status(launch_clear_flag(clear_flag, st)) : MDX_OK;
+  ReduceParams p;
+  memset(&p, 0, sizeof(p));
+  for (int r = 0; r < h->world; ++r) p.peer[r] = reinterpret_cast<const void*>(h->replicas[r]);
+  p.out = reinterpret_cast<void*>(h->out);
+  p.world = h->world;
+  p.rank = h->rank;
+  p.pre = h->prescale;
+  p.inv_scale = inv_scale;
+  p.flags = (h->dtype_a == h->reduce_dtype && h->prescale != 1.0f ? kRedPackScale : 0) |
+            (inv_scale != 1.0f ? kRedUnscale : 0);
+  p.found_inf = found_inf;
+  p.clear = clear_flag;
+  return status(launch_pack_allreduce_dev(h->dtype_a, h->reduce_dtype, h->world, t, h->blocks, p, st));
 }
 
 int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, int32_t* clear_flag,

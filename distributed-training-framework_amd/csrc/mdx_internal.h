@@ -270,6 +270,7 @@ enum : int32_t {
   kRedPreDiv = 2,      // every contribution / pre, rounded to the reduce dtype
   kRedAccumulate = 4,  // out = out + result (rounded to the out dtype)
   kRedUnscale = 8,     // stored value * inv_scale, rounded to its dtype
+  kRedPackScale = 16,  // fused pack: this rank's gradient * pre, rounded to the bucket dtype
 };
 
 struct ReduceParams {
@@ -281,6 +282,7 @@ struct ReduceParams {
   float pre;
   float inv_scale;
   int32_t* found_inf;
+  int32_t* clear;  // fused pack: a flag the dispatch's first lane sets to 0 (never found_inf), or NULL
 };
 
 // Fragments per lane and contribution (U) of the W-way reductions: each lane
@@ -367,7 +369,7 @@ struct DevView {
 // byte offsets.  The same bytes live on the host (read at launch for the grid
 // size and kernel arguments) and in device memory (read by the kernel).
 constexpr uint32_t kPlanMagic = 0x5058444du;  // "MDXP"
-enum : int32_t { kPlanSpans = 1, kPlanGradRuns = 2 };
+enum : int32_t { kPlanSpans = 1, kPlanGradRuns = 2, kPlanPackRuns = 3 };
 
 struct PlanHeader {
   uint32_t magic;
@@ -379,7 +381,10 @@ struct PlanHeader {
   int32_t world;
   int32_t reserved;
   int32_t reduce_dtype;  // grad runs: bucket (out) dtype; differs from dtype_a when widening
-  float prescale;        // grad runs: receiver-side pre-scale of every contribution (widening only)
+  float prescale;        // grad runs: receiver-side pre-scale of every contribution (widening only);
+                         // pack runs: the 1/W factor (pack side, or receiver side when widening)
+  int32_t rank;          // pack runs: the replica this rank packs into
+  int32_t pad;
   uint64_t replicas[MDX_MAX_WORLD];
   uint64_t out;
   int64_t off_first_block, off_head, off_numel, off_a, off_b, off_pos;
@@ -392,6 +397,12 @@ hipError_t launch_copy_dev(int src_dtype, int dst_dtype, const DevTable& t, int 
 hipError_t launch_allreduce_dev(int dtype, int grad_dtype, int world, const DevTable& t, int blocks,
                                 const ReduceParams& p, hipStream_t stream);
 hipError_t launch_allreduce_wide_dev(int wire_dtype, int grad_dtype, int world, const DevTable& t, int blocks,
+                                     const ReduceParams& p, hipStream_t stream);
+// Pack fused into the all-reduce + unpack (gradients of the wire dtype; the
+// bucket dtype equals it or is fp32 for bf16 / fp16 wires).
+hipError_t launch_pack_allreduce(int wire_dtype, int reduce_dtype, int world, const PieceBatch& b,
+                                 const ReduceParams& p, hipStream_t stream);
+hipError_t launch_pack_allreduce_dev(int wire_dtype, int reduce_dtype, int world, const DevTable& t, int blocks,
                                      const ReduceParams& p, hipStream_t stream);
 
 inline int dtype_size(int dt) { return dt == MDX_F32 ? 4 : 2; }

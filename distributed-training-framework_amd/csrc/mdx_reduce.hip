@@ -23,6 +23,14 @@ hipError_t launch_allreduce_wide_dev_bf16(int grad_dtype, int world, const DevTa
                                           const ReduceParams& p, hipStream_t stream);
 hipError_t launch_allreduce_wide_dev_f16(int grad_dtype, int world, const DevTable& t, int blocks,
                                          const ReduceParams& p, hipStream_t stream);
+hipError_t launch_pack_allreduce_same(int dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                                      hipStream_t stream);
+hipError_t launch_pack_allreduce_dev_same(int dtype, int world, const DevTable& t, int blocks,
+                                          const ReduceParams& p, hipStream_t stream);
+hipError_t launch_pack_allreduce_wide(int wire_dtype, int world, const PieceBatch& b, const ReduceParams& p,
+                                      hipStream_t stream);
+hipError_t launch_pack_allreduce_dev_wide(int wire_dtype, int world, const DevTable& t, int blocks,
+                                          const ReduceParams& p, hipStream_t stream);
 hipError_t launch_share_fast(int in_dtype, int wmax, const PieceBatch& b, const ReduceParams& p,
                              hipStream_t stream);
 hipError_t launch_share_generic_f32(int acc_dtype, int out_dtype, const PieceBatch& b, const ReduceParams& p,
@@ -56,6 +64,18 @@ hipError_t launch_allreduce_wide_dev(int wire_dtype, int grad_dtype, int world, 
                                      const ReduceParams& p, hipStream_t stream) {
   if (wire_dtype == MDX_F16) return launch_allreduce_wide_dev_f16(grad_dtype, world, t, blocks, p, stream);
   return launch_allreduce_wide_dev_bf16(grad_dtype, world, t, blocks, p, stream);
+}
+
+hipError_t launch_pack_allreduce(int wire_dtype, int reduce_dtype, int world, const PieceBatch& b,
+                                 const ReduceParams& p, hipStream_t stream) {
+  if (wire_dtype == reduce_dtype) return launch_pack_allreduce_same(wire_dtype, world, b, p, stream);
+  return launch_pack_allreduce_wide(wire_dtype, world, b, p, stream);
+}
+
+hipError_t launch_pack_allreduce_dev(int wire_dtype, int reduce_dtype, int world, const DevTable& t, int blocks,
+                                     const ReduceParams& p, hipStream_t stream) {
+  if (wire_dtype == reduce_dtype) return launch_pack_allreduce_dev_same(wire_dtype, world, t, blocks, p, stream);
+  return launch_pack_allreduce_dev_wide(wire_dtype, world, t, blocks, p, stream);
 }
 
 static bool fast_triple(int in_dtype, int acc_dtype, int out_dtype) {

@@ -19,6 +19,18 @@
 // `mul_(1/W)`) would have put on the wire; the rank-ordered sum, the write of
 // the T bucket and the unpack epilogue are as above.
 //
+// allreduce_pack_kernel<In, T, W> (+ _dev): the pack fused in front of the
+// fused all-reduce + unpack, for gradients of the wire dtype In.  Replica
+// `rank` is read from the run's gradient (NULL = zeros) and packed in
+// registers, c = rnd_T(g * pre) for a bucket of the same dtype (the pack's
+// `copy_` + `mul_(1/W)`) or the raw gradient for a widening bucket (which
+// pre-scales every contribution where it is widened, as above); c is stored
+// to replica `rank`'s row -- what the peers read -- and enters the rank-ordered
+// sum without being read back, and the bucket is a separate output.  Per
+// element: the gradient and W-1 peer rows read; the packed row, the bucket
+// and the gradient written.  The dispatch also clears the loss scaler's flag
+// for the next step (ReduceParams::clear).
+//
 // share_kernel<In, Acc, Out, WMAX>: FSDP's reduce-scatter share, runtime
 // W <= WMAX.  x_r = cvt_Acc(contribution_r[p]); x_r = rnd_Acc(x_r * pre | x_r / pre);
 // acc = rank-ordered sum in Acc; y = cvt_Out(acc); y = rnd_Out(out + y) when
@@ -40,8 +52,9 @@ namespace reduce_impl {
 // all-reduce (+ fused unpack)
 // ---------------------------------------------------------------------------
 
-template <typename In, typename T, typename G, int W, bool UNPACK, bool PRE, typename View>
+template <typename In, typename T, typename G, int W, bool UNPACK, bool PRE, bool PACK, typename View>
 __device__ __forceinline__ void allreduce_body(const View& tab, const ReduceParams& p) {
+  static_assert(!PACK || (UNPACK && sizeof(G) == sizeof(In)), "the fused pack reads gradients of the wire dtype");
   constexpr int E = store_frag_elems(UNPACK ? max_size(int(sizeof(T)), int(sizeof(G))) : int(sizeof(T)));
   constexpr int U = allreduce_unroll(W, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
@@ -61,15 +74,33 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   const float inv = p.inv_scale;
   const float pre = p.pre;
 
+  // Replica `rank` is read through the run's own pointer: the rank's packed
+  // row, or with PACK its gradient (NULL = zeros), packed here.
   const In* src[W];
 #pragma unroll
   for (int r = 0; r < W; ++r) {
     src[r] = (r == rank) ? static_cast<const In*>(tab.own(s)) : static_cast<const In*>(p.peer[r]) + pos;
   }
+  const bool own_zero = PACK && tab.own(s) == nullptr;
+  In* own_row = PACK ? static_cast<In*>(const_cast<void*>(p.peer[rank])) + pos : nullptr;
+  const bool pack_scale = PACK && !PRE && (p.flags & kRedPackScale) != 0;
   T* out = p.out ? static_cast<T*>(p.out) + pos : nullptr;
   G* grad = static_cast<G*>(tab.grad(s));
   bool bad = false;
+  // The next step's found-inf flag rides on the fused pack (nothing reads or
+  // sets it during this step): one lane of the first workgroup.
+  if (PACK && p.clear != nullptr && blk == 0 && t == 0) *p.clear = 0;
 
+  // The pack's `copy_` + `mul_(1/W)` of this rank's gradient (same-dtype
+  // buckets; a widening bucket carries the raw gradient and pre-scales where
+  // every contribution is widened).
+  auto pack_op = [&](In x) -> In {
+    if constexpr (PACK && !PRE) {
+      const In xs = from_f32<In>(to_f32(x) * pre);
+      return pack_scale ? xs : x;
+    }
+    return x;
+  };
   auto widen = [&](In x) -> T {
     T a = Cvt<In, T>::run(x);
     if constexpr (PRE) a = from_f32<T>(to_f32(a) * pre);
@@ -84,9 +115,21 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
     return g;
   };
   auto element = [&](int64_t i) {
-    T acc = widen(src[0][i]);
+    T acc = zero_of<T>();
+    In packed = zero_of<In>();
 #pragma unroll
-    for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(src[r][i])));
+    for (int r = 0; r < W; ++r) {
+      In xr;
+      if (PACK && r == rank) {
+        xr = pack_op(own_zero ? zero_of<In>() : src[r][i]);
+        packed = xr;
+      } else {
+        xr = src[r][i];
+      }
+      const T a = widen(xr);
+      acc = (r == 0) ? a : from_f32<T>(to_f32(acc) + to_f32(a));
+    }
+    if constexpr (PACK) own_row[i] = packed;
     if (out) out[i] = acc;
     if constexpr (UNPACK) grad[i] = finish(acc);
   };
@@ -99,7 +142,14 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
       const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
       if (v < nvec) {
 #pragma unroll
-        for (int r = 0; r < W; ++r) vload<In, E, true>(x[u][r], src[r] + h + v * E);
+        for (int r = 0; r < W; ++r) {
+          if (PACK && r == rank && own_zero) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[u][r][e] = zero_of<In>();
+          } else {
+            vload<In, E, true>(x[u][r], src[r] + h + v * E);
+          }
+        }
       }
     }
 #pragma unroll
@@ -107,6 +157,24 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
       const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
       if (v < nvec) {
         const int64_t i = h + v * E;
+        if constexpr (PACK) {
+          // This rank's fragment, packed in registers (static indices: the
+          // branch on the wave-uniform rank picks the replica slot).
+          In po[E];
+#pragma unroll
+          for (int e = 0; e < E; ++e) po[e] = zero_of<In>();
+#pragma unroll
+          for (int r = 0; r < W; ++r) {
+            if (r == rank) {
+#pragma unroll
+              for (int e = 0; e < E; ++e) {
+                x[u][r][e] = pack_op(x[u][r][e]);
+                po[e] = x[u][r][e];
+              }
+            }
+          }
+          vstore<In, E, true>(own_row + i, po);
+        }
         T y[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -142,24 +210,36 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
 // Table in the kernel-argument segment.
 template <typename T, typename G, int W, bool UNPACK>
 __global__ void __launch_bounds__(kBlock) allreduce_kernel(PieceBatch b, ReduceParams p) {
-  allreduce_body<T, T, G, W, UNPACK, false>(PieceArgView{b}, p);
+  allreduce_body<T, T, G, W, UNPACK, false, false>(PieceArgView{b}, p);
 }
 
 // Table (plan) in device memory; the fused all-reduce + unpack only.
 template <typename T, typename G, int W>
 __global__ void __launch_bounds__(kBlock) allreduce_unpack_kernel_dev(DevTable t, ReduceParams p) {
-  allreduce_body<T, T, G, W, true, false>(DevView{t}, p);
+  allreduce_body<T, T, G, W, true, false, false>(DevView{t}, p);
 }
 
 // Widening variants (fused all-reduce + unpack with pre-scale at the receiver).
 template <typename In, typename T, typename G, int W>
 __global__ void __launch_bounds__(kBlock) allreduce_wide_kernel(PieceBatch b, ReduceParams p) {
-  allreduce_body<In, T, G, W, true, true>(PieceArgView{b}, p);
+  allreduce_body<In, T, G, W, true, true, false>(PieceArgView{b}, p);
 }
 
 template <typename In, typename T, typename G, int W>
 __global__ void __launch_bounds__(kBlock) allreduce_wide_kernel_dev(DevTable t, ReduceParams p) {
-  allreduce_body<In, T, G, W, true, true>(DevView{t}, p);
+  allreduce_body<In, T, G, W, true, true, false>(DevView{t}, p);
+}
+
+// Pack fused into the all-reduce + unpack: gradients of the wire dtype In,
+// bucket dtype T (T != In: widening, pre-scaled at the receiver).
+template <typename In, typename T, int W>
+__global__ void __launch_bounds__(kBlock) allreduce_pack_kernel(PieceBatch b, ReduceParams p) {
+  allreduce_body<In, T, In, W, true, (sizeof(In) != sizeof(T)), true>(PieceArgView{b}, p);
+}
+
+template <typename In, typename T, int W>
+__global__ void __launch_bounds__(kBlock) allreduce_pack_kernel_dev(DevTable t, ReduceParams p) {
+  allreduce_body<In, T, In, W, true, (sizeof(In) != sizeof(T)), true>(DevView{t}, p);
 }
 
 template <typename T, typename G, bool UNPACK>
@@ -202,6 +282,28 @@ struct DevWide {
   template <int W>
   hipError_t go(const ReduceParams& p, hipStream_t stream) const {
     hipLaunchKernelGGL((allreduce_wide_kernel_dev<In, T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename In, typename T>
+struct ArgPack {
+  const PieceBatch& b;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_pack_kernel<In, T, W>), dim3(b.first_block[b.count]), dim3(kBlock), 0, stream,
+                       b, p);
+    return hipGetLastError();
+  }
+};
+
+template <typename In, typename T>
+struct DevPack {
+  const DevTable& t;
+  int blocks;
+  template <int W>
+  hipError_t go(const ReduceParams& p, hipStream_t stream) const {
+    hipLaunchKernelGGL((allreduce_pack_kernel_dev<In, T, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
     return hipGetLastError();
   }
 };
@@ -284,6 +386,18 @@ hipError_t launch_wide_dev_for(int grad_dtype, int world, const DevTable& t, int
   if (grad_dtype == MDX_F32) return launch_allreduce_wide_dev<In, float, float>(world, t, blocks, p, stream);
   if (grad_dtype == MDX_BF16) return launch_allreduce_wide_dev<In, float, bf16>(world, t, blocks, p, stream);
   return launch_allreduce_wide_dev<In, float, f16>(world, t, blocks, p, stream);
+}
+
+// The fused pack + all-reduce + unpack of one (wire, bucket) dtype pair.
+template <typename In, typename T>
+hipError_t launch_pack_for(int world, const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
+  return by_world(world, ArgPack<In, T>{b}, p, stream);
+}
+
+template <typename In, typename T>
+hipError_t launch_pack_dev_for(int world, const DevTable& t, int blocks, const ReduceParams& p,
+                               hipStream_t stream) {
+  return by_world(world, DevPack<In, T>{t, blocks}, p, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -30,6 +30,8 @@ SOURCES = [
     "mdx_allreduce_f16.hip",
     "mdx_allreduce_wide.hip",
     "mdx_allreduce_wide_f16.hip",
+    "mdx_allreduce_pack.hip",
+    "mdx_allreduce_pack_wide.hip",
     "mdx_share_fast.hip",
     "mdx_share_generic.hip",
     "mdx_share_generic_bf16.hip",

@@ -25,7 +25,7 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -40,12 +40,19 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
     ),
+    "mdx_pack_allreduce_unpack": (
+        _i32, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _f32, _f32, _vp, _vp, _vp],
+    ),
     "mdx_cast_f32_bf16": (_i32, [_vp, _vp, _i64, _vp]),
     "mdx_plan_spans": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "mdx_plan_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _vp, _vp]),
     "mdx_plan_allreduce_unpack_wide": (
         _i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _f32, _vp, _vp],
     ),
+    "mdx_plan_pack_allreduce_unpack": (
+        _i32, [_vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp],
+    ),
+    "mdx_pack_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp, _vp]),
     "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp, _vp]),
     "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
@@ -56,6 +63,7 @@ SIGNATURES: dict[str, tuple] = {
 SPAN_DTYPE = np.dtype([("src", "<u8"), ("dst", "<u8"), ("numel", "<i8")])
 PIECE_DTYPE = np.dtype([("own", "<u8"), ("pos", "<i8"), ("numel", "<i8")])
 GRAD_RUN_DTYPE = np.dtype([("offset", "<i8"), ("numel", "<i8"), ("grad", "<u8")])
+PACK_RUN_DTYPE = np.dtype([("offset", "<i8"), ("numel", "<i8"), ("src", "<u8"), ("grad", "<u8")])
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -212,6 +220,21 @@ def allreduce_unpack_wide(
     check(rc, "mdx_allreduce_unpack_wide")
 
 
+def pack_runs_array(rows: list[tuple[int, int, int, int]]) -> np.ndarray:
+    return np.array(rows, dtype=PACK_RUN_DTYPE)
+
+
+def pack_allreduce_unpack(
+    replicas: list[int], rank: int, wire_dtype: int, runs: np.ndarray, out: int | None, reduce_dtype: int,
+    scale: float, inv_scale: float, found_inf: int | None, clear_flag: int | None, stream: int,
+) -> None:
+    rc = lib().mdx_pack_allreduce_unpack(
+        _ptrs(replicas), len(replicas), rank, wire_dtype, _ptr(runs), len(runs), out, reduce_dtype, scale,
+        inv_scale, found_inf, clear_flag, stream,
+    )
+    check(rc, "mdx_pack_allreduce_unpack")
+
+
 def reduce_scatter_share(
     own: np.ndarray,
     peers: list[int],
@@ -299,6 +322,27 @@ def plan_allreduce_unpack_wide(
         ),
         "mdx_plan_allreduce_unpack_wide", device,
     )
+
+
+def plan_pack_allreduce_unpack(
+    replicas: list[int], rank: int, wire_dtype: int, runs: np.ndarray, out: int | None, reduce_dtype: int,
+    scale: float, device,
+) -> Plan:
+    reps = _ptrs(replicas)
+    return _build_plan(
+        lambda buf, size: lib().mdx_plan_pack_allreduce_unpack(
+            reps, len(replicas), rank, wire_dtype, _ptr(runs), len(runs), out, reduce_dtype, scale, buf, size
+        ),
+        "mdx_plan_pack_allreduce_unpack", device,
+    )
+
+
+def pack_allreduce_unpack_planned(
+    plan: Plan, inv_scale: float, found_inf: int | None, clear_flag: int | None, stream: int
+) -> None:
+    rc = lib().mdx_pack_allreduce_unpack_planned(plan.host_ptr, plan.device_ptr, inv_scale, found_inf, clear_flag,
+                                                 stream)
+    check(rc, "mdx_pack_allreduce_unpack_planned")
 
 
 def pack_planned(plan: Plan, scale: float, divide: bool, stream: int, clear_flag: int | None = None) -> None:

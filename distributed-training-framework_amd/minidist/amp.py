@@ -104,11 +104,17 @@ class DistributedGradScaler:
         self._unscaled = False
         self.num_skipped = 0
         self.num_steps = 0
-        # Device-side found-inf flags (int32 [1] per device) and the flag's
-        # "zeroed for this step" marker; ids of params whose grads a fused
+        # Device-side found-inf flags: a pair of int32 per device, used in
+        # alternate steps (``_parity`` picks this step's), so that a dispatch
+        # that sets this step's flag can clear the next step's.  ``_flag_armed``:
+        # devices whose flag of this step is zero (or will be, by a clear already
+        # requested); ``_next_armed``: devices whose next-step flag a dispatch of
+        # this step clears.  ``_prescaled``: ids of params whose grads a fused
         # producer (DDP unpack) already unscaled this step.
-        self._flags: dict[torch.device, torch.Tensor] = {}
+        self._flags: dict[torch.device, tuple[torch.Tensor, torch.Tensor]] = {}
+        self._parity = 0
         self._flag_armed: set[torch.device] = set()
+        self._next_armed: set[torch.device] = set()
         self._prescaled: set[int] = set()
 
     # -- state --------------------------------------------------------------
@@ -140,20 +146,37 @@ class DistributedGradScaler:
         a memset) so that the step can be captured into a HIP graph; with
         ``defer_clear`` the caller enqueues that clear itself (``flag.zero_()``)
         before anything that sets the flag."""
-        flag = self._flags.get(device)
+        pair = self._flags.get(device)
         pending = False
-        if flag is None:
-            flag = torch.zeros(1, dtype=torch.int32, device=device)
-            self._flags[device] = flag
+        if pair is None:
+            storage = torch.zeros(2, dtype=torch.int32, device=device)
+            pair = (storage[0:1], storage[1:2])
+            self._flags[device] = pair
             self._flag_armed.add(device)
-            pending = defer_clear  # already zero; clearing again keeps every step's launch the same
+            self._next_armed.add(device)  # both flags start at zero
+            flag = pair[self._parity]
         elif device not in self._flag_armed:
+            flag = pair[self._parity]
             if defer_clear:
                 pending = True
             else:
                 flag.zero_()
             self._flag_armed.add(device)
+        else:
+            flag = pair[self._parity]
         return flag, pending
+
+    def _next_flag(self, device: torch.device) -> torch.Tensor:
+        """The flag the next step uses on ``device`` (which nothing reads or sets during this step).
+
+        A producer that clears it in stream order with its own dispatch reports so
+        with :meth:`_next_flag_cleared`; the next step then needs no clear of its own."""
+        if device not in self._flags:
+            self._flag(device)
+        return self._flags[device][self._parity ^ 1]
+
+    def _next_flag_cleared(self, device: torch.device) -> None:
+        self._next_armed.add(device)
 
     def _begin_fused_unscale(
         self, device: torch.device, param_ids: frozenset, defer_clear: bool = False
@@ -257,7 +280,8 @@ class DistributedGradScaler:
                 self._good_steps = 0
         self._found_inf_this_step = False
         self._unscaled = False
-        self._flag_armed.clear()
+        self._parity ^= 1
+        self._flag_armed, self._next_armed = self._next_armed, set()
         self._prescaled.clear()
 
     def summary(self) -> str:

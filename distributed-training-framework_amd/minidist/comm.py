@@ -367,12 +367,14 @@ class ResidentGroup:
         inv_scale: float = 1.0,
         found_inf: torch.Tensor | None = None,
         async_op: bool = False,
+        bucket: torch.Tensor | None = None,
     ):
         """SUM over the W replicas of ``buffer``'s runs, delivered into gradients.
 
         ``runs`` is an ``mdx_grad_run`` table (numpy, ``_native.GRAD_RUN_DTYPE``)
         of (offset into ``buffer``, numel, gradient address) in increasing
-        offset order.  The sum is written back into ``buffer`` (the in-place
+        offset order.  The sum is written into ``bucket`` (same offsets and
+        dtype as ``buffer``; default ``buffer`` itself, the in-place
         all-reduce) and, converted to ``grad_dtype``, multiplied by
         ``inv_scale`` and checked for inf/NaN into ``found_inf``, into each
         gradient -- one dispatch, the reduced values never re-read."""
@@ -380,9 +382,10 @@ class ResidentGroup:
         arena, off = self._locate(buffer)
         esize = arena.esize
         bases = [b + off * esize for b in arena.row_ptrs]
+        out = self._bucket_out(buffer, bucket)
         stream = torch.cuda.current_stream(buffer.device)
         _native.allreduce_unpack(
-            bases, _native.dtype_code(arena.dtype), runs, buffer.data_ptr(), _native.dtype_code(grad_dtype),
+            bases, _native.dtype_code(arena.dtype), runs, out, _native.dtype_code(grad_dtype),
             _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
             stream.cuda_stream,
         )
@@ -420,14 +423,26 @@ class ResidentGroup:
         )
         return StreamWork(stream) if async_op else None
 
-    def plan_all_reduce_unpack(self, buffer: torch.Tensor, runs, grad_dtype: torch.dtype) -> "_native.Plan":
+    @staticmethod
+    def _bucket_out(buffer: torch.Tensor, bucket: torch.Tensor | None) -> int:
+        """Address the fused all-reduce writes the sum to: ``bucket``, or ``buffer`` in place."""
+        if bucket is None:
+            return buffer.data_ptr()
+        _native.require_device_tensor(bucket, "all_reduce output")
+        if bucket.dtype != buffer.dtype or bucket.numel() < buffer.numel():
+            raise ValueError("all_reduce: the bucket must have the contributions' dtype and at least their length")
+        return bucket.data_ptr()
+
+    def plan_all_reduce_unpack(
+        self, buffer: torch.Tensor, runs, grad_dtype: torch.dtype, bucket: torch.Tensor | None = None
+    ) -> "_native.Plan":
         """Device plan of :meth:`all_reduce_unpack` for fixed ``runs`` (one dispatch per launch)."""
         _native.require_device_tensor(buffer, "all_reduce input")
         arena, off = self._locate(buffer)
         bases = [b + off * arena.esize for b in arena.row_ptrs]
         return _native.plan_allreduce_unpack(
-            bases, _native.dtype_code(arena.dtype), runs, buffer.data_ptr(), _native.dtype_code(grad_dtype),
-            buffer.device,
+            bases, _native.dtype_code(arena.dtype), runs, self._bucket_out(buffer, bucket),
+            _native.dtype_code(grad_dtype), buffer.device,
         )
 
     def plan_all_reduce_unpack_wide(
@@ -460,6 +475,77 @@ class ResidentGroup:
         _native.allreduce_unpack_planned(
             plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
             stream.cuda_stream,
+        )
+        return StreamWork(stream) if async_op else None
+
+    def pack_all_reduce_unpack(
+        self,
+        wire: torch.Tensor,
+        bucket: torch.Tensor | None,
+        runs,
+        scale: float,
+        inv_scale: float = 1.0,
+        found_inf: torch.Tensor | None = None,
+        clear_flag: torch.Tensor | None = None,
+        async_op: bool = False,
+    ):
+        """Pack this rank's gradients into its row of ``wire``, then SUM over the W rows into gradients.
+
+        ``runs`` is an ``mdx_pack_run`` table (``_native.PACK_RUN_DTYPE``) of
+        (offset into ``wire``, numel, gradient source or 0, gradient) in
+        increasing offset order; gradients have ``wire``'s dtype.  Each source
+        is packed as ``gather_into_buffer`` would (times ``scale`` = 1/W for a
+        bucket of the wire dtype; raw into a bf16 / fp16 wire of an fp32
+        ``bucket``, then every contribution times ``scale`` where it is
+        widened); the rank-ordered sum lands in ``bucket`` (when given) and,
+        times ``inv_scale`` and checked into ``found_inf``, in every gradient.
+        ``clear_flag`` is set to 0 by the same dispatch (the scaler's flag for
+        the next step).  One dispatch; this rank's contribution is summed from
+        registers, not re-read from its row."""
+        _native.require_device_tensor(wire, "all_reduce input")
+        arena, off = self._locate(wire)
+        bases = [b + off * arena.esize for b in arena.row_ptrs]
+        reduce_dtype = wire.dtype if bucket is None else bucket.dtype
+        if bucket is not None:
+            _native.require_device_tensor(bucket, "all_reduce output")
+            if bucket.numel() < wire.numel():
+                raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
+        stream = torch.cuda.current_stream(wire.device)
+        _native.pack_allreduce_unpack(
+            bases, self._rank, _native.dtype_code(arena.dtype), runs,
+            None if bucket is None else bucket.data_ptr(), _native.dtype_code(reduce_dtype), _native.f32(scale),
+            _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
+            clear_flag.data_ptr() if clear_flag is not None else None, stream.cuda_stream,
+        )
+        return StreamWork(stream) if async_op else None
+
+    def plan_pack_all_reduce_unpack(
+        self, wire: torch.Tensor, bucket: torch.Tensor | None, runs, scale: float
+    ) -> "_native.Plan":
+        """Device plan of :meth:`pack_all_reduce_unpack` for fixed ``runs`` (one dispatch per launch)."""
+        _native.require_device_tensor(wire, "all_reduce input")
+        arena, off = self._locate(wire)
+        bases = [b + off * arena.esize for b in arena.row_ptrs]
+        reduce_dtype = wire.dtype if bucket is None else bucket.dtype
+        if bucket is not None:
+            _native.require_device_tensor(bucket, "all_reduce output")
+            if bucket.numel() < wire.numel():
+                raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
+        return _native.plan_pack_allreduce_unpack(
+            bases, self._rank, _native.dtype_code(arena.dtype), runs,
+            None if bucket is None else bucket.data_ptr(), _native.dtype_code(reduce_dtype), _native.f32(scale),
+            wire.device,
+        )
+
+    def pack_all_reduce_unpack_planned(
+        self, plan: "_native.Plan", device: torch.device, inv_scale: float = 1.0,
+        found_inf: torch.Tensor | None = None, clear_flag: torch.Tensor | None = None, async_op: bool = False,
+    ):
+        """Launch a plan from :meth:`plan_pack_all_reduce_unpack` on the current stream."""
+        stream = torch.cuda.current_stream(device)
+        _native.pack_allreduce_unpack_planned(
+            plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
+            clear_flag.data_ptr() if clear_flag is not None else None, stream.cuda_stream,
         )
         return StreamWork(stream) if async_op else None
 

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 4
+#define MDX_ABI_VERSION 5
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -178,6 +178,51 @@ MDX_API int mdx_allreduce_unpack_wide(const void* const* replicas, int world, in
                                       int grad_dtype, float prescale, float inv_scale, int32_t* found_inf,
                                       void* stream);
 
+/* One parameter's gradient in a fused pack + all-reduce + unpack: elements
+ * [offset, offset + numel) of the replica layout.  This rank's contribution
+ * is packed from `src` (device pointer; NULL reads as zeros, a parameter
+ * whose .grad is None) and the reduced values are delivered to `grad` (which
+ * may be `src` itself: each element is read before it is written). */
+typedef struct mdx_pack_run {
+  int64_t offset;
+  int64_t numel;
+  const void* src;
+  void* grad;
+} mdx_pack_run;
+
+/* The pack fused into the all-reduce + unpack: one dispatch for DDP's whole
+ * per-rank chain of a run of ready buckets.  Gradients have the wire dtype;
+ * the bucket dtype (reduce_dtype) equals it, or is MDX_F32 for bf16 / fp16
+ * wires (widening).  Per run and element j (o = offset), with `scale` = 1/W
+ * rounded to fp32:
+ *   same dtype:  c = rnd(src[j] * scale)            (src = 0 when NULL; no
+ *                                                    multiply when scale == 1)
+ *   widening:    c = src[j]  (raw; every contribution x is then read as
+ *                rnd_f32(f32(x) * scale), as in mdx_allreduce_unpack_wide)
+ *   replicas[rank][o+j] = c          (the packed row the peers would read)
+ *   acc = rank-ordered SUM of replicas[r][o+j], with c itself for r = rank
+ *   out[o+j] = acc                   (the bucket; skipped when out == NULL)
+ *   g = rnd_grad(acc); if inv_scale != 1: g = rnd_grad(g * inv_scale)
+ *   grad[j] = g; flag if !isfinite(g)
+ * Replaces, for one run of ready buckets, _Bucket.gather_into_buffer
+ * (minidist/ddp.py:75-92), comm.all_reduce (minidist/comm.py:223-234),
+ * _Bucket.scatter_from_buffer (minidist/ddp.py:94-102) and the per-gradient
+ * body of DistributedGradScaler.unscale_ (minidist/amp.py:212-213).  The
+ * bucket must not overlap the replicas (it holds the average, while row
+ * `rank` keeps the packed contribution); gradients and sources must not
+ * overlap the replicas or the bucket; a source either is its run's gradient
+ * or does not overlap it.
+ * `clear_flag` (may be NULL, must differ from found_inf): a flag the call
+ * sets to 0, in stream order with the rest of the call -- the loss scaler's
+ * flag for the NEXT step, which nothing reads or sets during this one.  The
+ * flag this call sets cannot be cleared by the same dispatch, so the scaler
+ * alternates two flags and each step's fused pack clears the other.  It is
+ * cleared even when there is nothing to reduce. */
+MDX_API int mdx_pack_allreduce_unpack(const void* const* replicas, int world, int rank, int wire_dtype,
+                                      const mdx_pack_run* runs, int n_runs, void* out, int reduce_dtype,
+                                      float scale, float inv_scale, int32_t* found_inf, int32_t* clear_flag,
+                                      void* stream);
+
 /* This rank's share of a SUM reduce-scatter, with FSDP's pre-division,
  * dtype changes and optional accumulation fused.
  * Replaces _FSDPUnit.reduce_scatter_grads (minidist/fsdp.py:215-237): widen
@@ -239,6 +284,16 @@ MDX_API int mdx_plan_allreduce_unpack(const void* const* replicas, int world, in
 MDX_API int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int world, int wire_dtype,
                                            const mdx_grad_run* runs, int n_runs, void* out, int reduce_dtype,
                                            int grad_dtype, float prescale, void* plan, int64_t* plan_bytes);
+
+/* Plan for mdx_pack_allreduce_unpack_planned (arguments as
+ * mdx_pack_allreduce_unpack; rank and scale are frozen into the plan). */
+MDX_API int mdx_plan_pack_allreduce_unpack(const void* const* replicas, int world, int rank, int wire_dtype,
+                                           const mdx_pack_run* runs, int n_runs, void* out, int reduce_dtype,
+                                           float scale, void* plan, int64_t* plan_bytes);
+
+/* mdx_pack_allreduce_unpack over a plan: one dispatch. */
+MDX_API int mdx_pack_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale,
+                                              int32_t* found_inf, int32_t* clear_flag, void* stream);
 
 /* mdx_pack over a plan: one dispatch.  `plan` = host copy, `d_plan` = device copy. */
 MDX_API int mdx_pack_planned(const void* plan, const void* d_plan, float scale, int divide, int32_t* clear_flag,

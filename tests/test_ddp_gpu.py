@@ -179,7 +179,8 @@ def test_comm_stream_carries_every_launch(monkeypatch):
 
     seen = []
     # position of the stream argument in each entry point's Python binding
-    for name, at in (("pack", 5), ("pack_planned", 3), ("allreduce_unpack", 7), ("allreduce_unpack_planned", 3)):
+    for name, at in (("pack", 5), ("pack_planned", 3), ("allreduce_unpack", 7), ("allreduce_unpack_planned", 3),
+                     ("pack_allreduce_unpack", 10), ("pack_allreduce_unpack_planned", 4)):
         orig = getattr(_native, name)
 
         def spy(*a, _orig=orig, _name=name, _at=at):
@@ -304,9 +305,10 @@ def test_set_to_none_backward_steps(comm_stream):
 def test_graph_replays_match_eager(rng):
     """capture_graphs: every replay is bit-exact with the eager launches on the same inputs.
 
-    Eager work and host syncs run between replays; the graph is re-captured when the
-    scale backs off (found-inf at step 2) and when the gradients move (set to None
-    before step 4), and replayed otherwise."""
+    Eager work and host syncs run between replays.  The scaler alternates two
+    found-inf flags, so even and odd steps have graphs of their own; a graph is
+    re-captured when the scale backs off (found-inf at step 2) and when the
+    gradients move (set to None before step 4), and replayed otherwise."""
     W, rank, init = 4, 1, 2.0**10
     shapes = [(int(rng.integers(1, 300)),) if i % 3 else (int(rng.integers(1, 40)), 33) for i in range(60)]
     numels = [int(np.prod(s)) for s in shapes]
@@ -336,6 +338,9 @@ def test_graph_replays_match_eager(rng):
                 else:
                     p.grad.copy_(dev_from(g, p.shape))  # same tensors: the graph replays
             ddp.finish_gradient_sync()
+            if graphs:  # the graph of this step's flag
+                flag = scaler._flags[DEV][scaler._parity]
+                captured.append(id(ddp._graphs[(0, len(ddp._buckets), flag.data_ptr())][1]))
 
             class _Opt:
                 param_groups = [{"params": list(model.parameters())}]
@@ -343,8 +348,6 @@ def test_graph_replays_match_eager(rng):
             found = scaler.unscale_(_Opt())
             scaler.update()
             results[graphs] = (found, [host_bits(p.grad) for p in model.parameters()])
-            if graphs:
-                captured.append(id(ddp._graphs[(0, len(ddp._buckets))][1]))
             # unrelated eager work and a host sync between replays
             x = torch.randn(1 << 16, device=DEV)
             assert torch.isfinite(x.sum()).item()
@@ -355,8 +358,9 @@ def test_graph_replays_match_eager(rng):
         for i in range(len(shapes)):
             assert same_bits(results[True][1][i], results[False][1][i]), f"step {step} param {i}"
             assert same_bits(results[True][1][i], want["grads"][i]), f"step {step} param {i} vs oracle"
-    # captured at step 0, re-captured at 3 (scale backed off at the end of step 2) and 4 (new gradients)
-    assert captured[0] == captured[1] == captured[2] != captured[3] != captured[4] == captured[5]
+    # even steps: captured at 0, replayed at 2, re-captured at 4 (new gradients); odd steps: captured
+    # at 1, re-captured at 3 (scale backed off at the end of step 2) and 5 (new gradients)
+    assert captured[0] == captured[2] and len({captured[i] for i in (0, 1, 3, 4, 5)}) == 5
     assert runs[True][2]._graphs and not runs[False][2]._graphs
 
 

@@ -289,10 +289,10 @@ def test_span_table_layout_is_the_c_struct():
 def _plan_header(buf: np.ndarray) -> dict:
     h = buf.view(np.int32)
     q = buf.view(np.int64)
-    # PlanHeader (csrc/mdx_internal.h): 10 int32 fields, replicas[16] and out (uint64), then the
+    # PlanHeader (csrc/mdx_internal.h): 12 int32 fields, replicas[16] and out (uint64), then the
     # int64 offsets first_block, head, numel, a, b, pos, the total size and the hint offset.
     return {"magic": int(h[0]) & 0xFFFFFFFF, "kind": int(h[1]), "count": int(h[2]), "blocks": int(h[3]),
-            "off_first_block": int(q[22]), "bytes": int(q[28]), "off_hint": int(q[29])}
+            "rank": int(h[10]), "off_first_block": int(q[23]), "bytes": int(q[29]), "off_hint": int(q[30])}
 
 
 HINT_SHIFT = 6  # kHintShift: one run hint per 64 workgroups
