@@ -105,19 +105,25 @@ def calibrate_copy() -> int:
     return 0
 
 
-# Committed rocprofv3 FETCH_SIZE + WRITE_SIZE summaries of each workload's dominant kernel.
+# Committed rocprofv3 FETCH_SIZE + WRITE_SIZE summaries of each workload's dominant kernel: the
+# pack fused into the all-reduce + unpack (default), or the two-dispatch pipeline's fused
+# all-reduce + unpack (--two-dispatch).
 TRAFFIC_FILES = {
-    "cfg0": "allreduce_unpack_tiny_gpt_w4_traffic.json",
-    "cfg1": "allreduce_unpack_gpt2_124m_w8_traffic.json",
-    "cfg2": "allreduce_unpack_gpt2_medium_w4_traffic.json",
-    "cfg3": "share_cast_gpt2_xl_fsdp_w8_traffic.json",
-    "cfg4": "allreduce_wide_llama7b_w8_traffic.json",
+    ("cfg0", True): "pack_allreduce_tiny_gpt_w4_traffic.json",
+    ("cfg1", True): "pack_allreduce_gpt2_124m_w8_traffic.json",
+    ("cfg2", True): "pack_allreduce_gpt2_medium_w4_traffic.json",
+    ("cfg4", True): "pack_allreduce_llama7b_w8_traffic.json",
+    ("cfg0", False): "allreduce_unpack_tiny_gpt_w4_traffic.json",
+    ("cfg1", False): "allreduce_unpack_gpt2_124m_w8_traffic.json",
+    ("cfg2", False): "allreduce_unpack_gpt2_medium_w4_traffic.json",
+    ("cfg4", False): "allreduce_wide_llama7b_w8_traffic.json",
+    ("cfg3", False): "share_cast_gpt2_xl_fsdp_w8_traffic.json",
 }
 
 
-def measured_traffic(workload: str) -> int | None:
+def measured_traffic(workload: str, fused_pack: bool = False) -> int | None:
     """HBM bytes per dispatch of the dominant kernel, from the committed PMC summary."""
-    path = ROOT / "profiles" / TRAFFIC_FILES.get(workload, "")
+    path = ROOT / "profiles" / TRAFFIC_FILES.get((workload, fused_pack), "")
     if not path.is_file():
         return None
     return json.loads(path.read_text()).get("bytes_per_launch")
@@ -320,7 +326,7 @@ def bench_ddp(name: str, args) -> dict:
         kname = f"allreduce_kernel<float, float, {W}, false> (mdx_allreduce_sum)"
     red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
 
-    traffic = measured_traffic(name) if fused_pack else None
+    traffic = None if args.staged else measured_traffic(name, fused_pack)
 
     return {
         "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",

@@ -139,7 +139,13 @@ def require_dense(t: torch.Tensor, what: str) -> None:
         raise RuntimeError(f"{what} must be contiguous for the flat-span kernels")
 
 
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """The raw handle of ``device``'s current stream (one C call where torch exposes it)."""
+    if _current_raw_stream is not None:
+        return _current_raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

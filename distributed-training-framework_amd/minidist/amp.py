@@ -109,13 +109,13 @@ class DistributedGradScaler:
         # that sets this step's flag can clear the next step's.  ``_flag_armed``:
         # devices whose flag of this step is zero (or will be, by a clear already
         # requested); ``_next_armed``: devices whose next-step flag a dispatch of
-        # this step clears.  ``_prescaled``: ids of params whose grads a fused
-        # producer (DDP unpack) already unscaled this step.
+        # this step clears.  ``_prescaled``: the id sets of params whose grads a
+        # fused producer (DDP unpack) already unscaled this step, one per launch.
         self._flags: dict[torch.device, tuple[torch.Tensor, torch.Tensor]] = {}
         self._parity = 0
         self._flag_armed: set[torch.device] = set()
         self._next_armed: set[torch.device] = set()
-        self._prescaled: set[int] = set()
+        self._prescaled: list[frozenset] = []
 
     # -- state --------------------------------------------------------------
 
@@ -191,12 +191,12 @@ class DistributedGradScaler:
         the flag (first producer of the step) before its kernels run."""
         if self._unscaled:
             raise RuntimeError("gradients were already unscaled this step; call update() first")
-        if not self._prescaled.isdisjoint(param_ids):
+        if not all(ids.isdisjoint(param_ids) for ids in self._prescaled):
             raise RuntimeError(
                 "a second synchronised backward ran before scaler.step()/update(): its gradients "
                 "would accumulate onto already-unscaled ones"
             )
-        self._prescaled |= param_ids
+        self._prescaled.append(param_ids)
         flag, pending = self._flag(device, defer_clear)
         if defer_clear:
             return 1.0 / self._scale, flag, pending
@@ -225,11 +225,12 @@ class DistributedGradScaler:
         device = comm.current_device()
         flag, _ = self._flag(device)
 
+        prescaled = self._prescaled[0] if len(self._prescaled) == 1 else frozenset().union(*self._prescaled)
         groups: dict[torch.dtype, list[tuple[int, int, int]]] = {}
         for group in optimizer.param_groups:
             for p in group["params"]:
                 g = p.grad
-                if g is None or id(p) in self._prescaled:
+                if g is None or id(p) in prescaled:
                     continue
                 _native.require_device_tensor(g, "gradient")
                 if not g.is_contiguous():

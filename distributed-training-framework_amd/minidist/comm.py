@@ -471,12 +471,11 @@ class ResidentGroup:
         found_inf: torch.Tensor | None = None, async_op: bool = False,
     ):
         """Launch a plan from :meth:`plan_all_reduce_unpack` on the current stream."""
-        stream = torch.cuda.current_stream(device)
         _native.allreduce_unpack_planned(
             plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
-            stream.cuda_stream,
+            _native.stream_of(device),
         )
-        return StreamWork(stream) if async_op else None
+        return StreamWork(torch.cuda.current_stream(device)) if async_op else None
 
     def pack_all_reduce_unpack(
         self,
@@ -542,12 +541,12 @@ class ResidentGroup:
         found_inf: torch.Tensor | None = None, clear_flag: torch.Tensor | None = None, async_op: bool = False,
     ):
         """Launch a plan from :meth:`plan_pack_all_reduce_unpack` on the current stream."""
-        stream = torch.cuda.current_stream(device)
         _native.pack_allreduce_unpack_planned(
             plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
-            clear_flag.data_ptr() if clear_flag is not None else None, stream.cuda_stream,
+            clear_flag.data_ptr() if clear_flag is not None else None, _native.stream_of(device),
         )
-        return StreamWork(stream) if async_op else None
+        # the Work's stream object is built after the launch, off the path to the GPU
+        return StreamWork(torch.cuda.current_stream(device)) if async_op else None
 
     def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
