@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -75,13 +76,44 @@ def _compile(src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
+HOST_HELPER_SRC = CSRC / "host_grad_ptrs.cpp"
+
+
+def host_helper_path() -> Path:
+    return PKG_DIR / ("_hostptrs" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_host_helper() -> Path:
+    """Compile the ``_hostptrs`` CPython module (host-only, g++ against torch's headers)."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    libdir = ce.library_paths()[0]
+    out = host_helper_path()
+    tmp = out.with_suffix(".tmp")
+    cmd = [
+        shutil.which("g++") or "g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        *[f"-I{d}" for d in ce.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+        str(HOST_HELPER_SRC), "-o", str(tmp),
+        f"-L{libdir}", f"-Wl,-rpath,{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+    ]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"build of {out.name} failed:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build_native(jobs: int | None = None) -> Path:
     """Compile every translation unit for gfx950 and link ``libmdx.so``."""
     BUILD_DIR.mkdir(exist_ok=True)
     objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
+        helper = pool.submit(build_host_helper)
         list(pool.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+        helper.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)

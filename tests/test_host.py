@@ -407,3 +407,25 @@ def test_bench_refuses_more_than_one_gpu():
     assert res.returncode == 2
     assert "one GPU" in res.stderr or "single" in res.stderr
     assert res.stdout.strip() == ""
+
+
+def test_host_grad_ptrs_helper_matches_python():
+    """The native gather of gradient addresses (minidist._hostptrs) equals p.grad.data_ptr() per
+    parameter, 0 where .grad is None, for Parameters and plain tensors, and rejects non-tensors."""
+    import torch
+
+    from minidist import _hostptrs
+
+    ps = [torch.nn.Parameter(torch.zeros(i + 1)) for i in range(40)]
+    for i, p in enumerate(ps):
+        if i % 3:
+            p.grad = torch.randn(i + 1)
+    views = torch.zeros(100)
+    ps[5].grad = views[7:13]  # a view: the address of its first element
+    want = [0 if p.grad is None else p.grad.data_ptr() for p in ps]
+    assert _hostptrs.grad_ptrs(ps) == want
+    assert _hostptrs.grad_ptrs([]) == []
+    with pytest.raises(TypeError):
+        _hostptrs.grad_ptrs([ps[0], 3])
+    with pytest.raises(TypeError):
+        _hostptrs.grad_ptrs(tuple(ps))
