@@ -379,7 +379,7 @@ int check_fused(const void* const* replicas, int world, int dtype, int out_dtype
   f->es = es;
   f->os = os;
   f->gs = gs;
-  f->E = store_frag_elems(max_size(os, gs));  // as the kernel's compile-time fragment
+  f->E = reduce_frag_elems(es, os, gs);  // as the kernel's compile-time fragment
   f->U = allreduce_unroll(world, f->E * es);
   return MDX_OK;
 }
@@ -481,7 +481,7 @@ int check_pack_fused(const void* const* replicas, int world, int rank, int dtype
   f->es = es;
   f->os = os;
   f->gs = es;
-  f->E = store_frag_elems(max_size(os, es));  // as the kernel's compile-time fragment
+  f->E = reduce_frag_elems(es, os, es);  // as the kernel's compile-time fragment
   f->U = allreduce_unroll(world, f->E * es);
   return MDX_OK;
 }
@@ -740,7 +740,7 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   p.flags = flags;
   const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
   const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
-  const int E = store_frag_elems(os);
+  const int E = reduce_frag_elems(is, os, os);  // as the kernel's compile-time fragment
   const int U = share_unroll(wmax, E * is);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](const PieceBatch& b) {

@@ -169,6 +169,32 @@ __device__ __forceinline__ void vstore(T* p, const T (&src)[E]) {
   }
 }
 
+// A wave's 8 four-byte values per lane, stored so that each store instruction
+// writes 1 KB of consecutive bytes.  Lane t holds elements [8t, 8t + 8) of the
+// wave's 512-element chunk at `chunk`; store k (0, 1) writes elements
+// [256k + 4t, 256k + 4t + 4), which lane 32k + t/2 holds (its half t & 1),
+// fetched with ds_bpermute.  Every lane of the wave must reach this call (the
+// permutes read other lanes' registers); only elements below `limit` are
+// stored, and each of them comes from a lane below limit / 8.
+template <typename T>
+__device__ __forceinline__ void vstore_wave8(T* chunk, const T (&src)[8], int t, int limit) {
+  static_assert(sizeof(T) == 4, "four-byte elements");
+  const bool upper = (t & 1) != 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int from = (32 * k + (t >> 1)) << 2;
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int lo = __builtin_amdgcn_ds_bpermute(from, __builtin_bit_cast(int, src[e]));
+      const int hi = __builtin_amdgcn_ds_bpermute(from, __builtin_bit_cast(int, src[e + 4]));
+      w[e] = uint32_t(upper ? hi : lo);
+    }
+    const int first = 256 * k + 4 * t;
+    if (first + 4 <= limit) __builtin_nontemporal_store(w, (gu32x4*)(chunk + first));
+  }
+}
+
 // Workgroup -> run lookup: largest s in [lo, hi) with first_block[s] <= blk
 // (first_block[lo] <= blk must hold).
 __device__ __forceinline__ int find_run_in(const int32_t* first_block, int lo, int hi, int blk) {
@@ -240,6 +266,7 @@ struct CopyParams {
 // reductions.
 constexpr int min_size(int a, int b) { return a < b ? a : b; }
 constexpr int max_size(int a, int b) { return a > b ? a : b; }
+constexpr int64_t min_i64(int64_t a, int64_t b) { return a < b ? a : b; }
 constexpr int store_frag_elems(int widest_store_size) { return 16 / widest_store_size; }
 constexpr int copy_unroll(int frag_in_bytes) { return frag_in_bytes >= 16 ? 1 : 16 / frag_in_bytes; }
 // Alignment heads are searched over 16 bytes of the narrowest (2-byte) type,
@@ -292,6 +319,14 @@ struct ReduceParams {
 // all-reduce's bandwidth, and a workgroup that streams several chunks in a
 // double-buffered loop loses to one short-lived workgroup per chunk.
 constexpr int kReduceLoadBytesPerLane = 128;
+// Elements per fragment of the W-way reductions with an unpack.  A widening
+// reduction (16-bit contributions, fp32 bucket) loads its contributions 16
+// bytes per lane -- 8 elements, whose 4-byte results vstore_wave8 writes in
+// whole 1 KB rows (measured: 4% faster than 8-byte loads with 16-byte stores);
+// otherwise a fragment is one 16-byte vector of the widest stored type.
+constexpr int reduce_frag_elems(int in_size, int out_size, int grad_size) {
+  return in_size < out_size ? 16 / in_size : store_frag_elems(max_size(out_size, grad_size));
+}
 constexpr int clamp_unroll(int u) { return u < 1 ? 1 : (u > 8 ? 8 : u); }
 constexpr int allreduce_unroll(int world, int frag_in_bytes) {
   return clamp_unroll(kReduceLoadBytesPerLane / (world * frag_in_bytes));

@@ -55,10 +55,18 @@ namespace reduce_impl {
 template <typename In, typename T, typename G, int W, bool UNPACK, bool PRE, bool PACK, typename View>
 __device__ __forceinline__ void allreduce_body(const View& tab, const ReduceParams& p) {
   static_assert(!PACK || (UNPACK && sizeof(G) == sizeof(In)), "the fused pack reads gradients of the wire dtype");
-  constexpr int E = store_frag_elems(UNPACK ? max_size(int(sizeof(T)), int(sizeof(G))) : int(sizeof(T)));
+  constexpr int E = UNPACK ? reduce_frag_elems(int(sizeof(In)), int(sizeof(T)), int(sizeof(G)))
+                            : store_frag_elems(int(sizeof(T)));
   constexpr int U = allreduce_unroll(W, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
+  // 32-byte fragments of a stored type go out through vstore_wave8, which
+  // every lane of the wave takes part in: lanes past the end then compute on
+  // zeros (finite: they never raise the flag) and store nothing.
+  constexpr bool kWaveT = E * int(sizeof(T)) == 32;
+  constexpr bool kWaveG = UNPACK && E * int(sizeof(G)) == 32;
+  constexpr bool kWave = kWaveT || kWaveG;
+  static_assert(!kWave || E == 8, "wave-permuted stores take 8 four-byte elements per lane");
 
   const int blk = int(blockIdx.x);
   const int32_t* fb = tab.first_block();
@@ -140,6 +148,13 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if constexpr (kWave) {
+#pragma unroll
+        for (int r = 0; r < W; ++r) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) x[u][r][e] = zero_of<In>();
+        }
+      }
       if (v < nvec) {
 #pragma unroll
         for (int r = 0; r < W; ++r) {
@@ -154,8 +169,12 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
-      if (v < nvec) {
+      const int64_t v0 = int64_t(c) * VPB + int64_t(u) * kBlock;  // the fragment of lane 0
+      const int64_t v = v0 + t;
+      const bool active = v < nvec;
+      // elements of this wave's fragment that exist (wave-permuted stores only)
+      const int limit = int(max_size(0, int(min_i64(nvec - v0, kBlock)))) * E;
+      if (kWave || active) {
         const int64_t i = h + v * E;
         if constexpr (PACK) {
           // This rank's fragment, packed in registers (static indices: the
@@ -173,7 +192,7 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
               }
             }
           }
-          vstore<In, E, true>(own_row + i, po);
+          if (active) vstore<In, E, true>(own_row + i, po);
         }
         T y[E];
 #pragma unroll
@@ -183,12 +202,22 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
           for (int r = 1; r < W; ++r) acc = from_f32<T>(to_f32(acc) + to_f32(widen(x[u][r][e])));
           y[e] = acc;
         }
-        if (out) vstore<T, E, true>(out + i, y);
+        if (out) {
+          if constexpr (kWaveT) {
+            vstore_wave8<T>(out + h + v0 * E, y, t, limit);
+          } else if (active) {
+            vstore<T, E, true>(out + i, y);
+          }
+        }
         if constexpr (UNPACK) {
           G gy[E];
 #pragma unroll
           for (int e = 0; e < E; ++e) gy[e] = finish(y[e]);
-          vstore<G, E, true>(grad + i, gy);
+          if constexpr (kWaveG) {
+            vstore_wave8<G>(grad + h + v0 * E, gy, t, limit);
+          } else if (active) {
+            vstore<G, E, true>(grad + i, gy);
+          }
         }
       }
     }
@@ -408,10 +437,14 @@ enum : int { kPreNone = 0, kPreMul = 1, kPreDiv = 2 };
 
 template <typename In, typename Acc, typename Out, int WMAX, int PRE, bool ACC>
 __device__ __forceinline__ void share_body(const PieceBatch& b, const ReduceParams& p, int s, int c, int nblk) {
-  constexpr int E = store_frag_elems(int(sizeof(Out)));
+  constexpr int E = reduce_frag_elems(int(sizeof(In)), int(sizeof(Out)), int(sizeof(Out)));
   constexpr int U = share_unroll(WMAX, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
+  // 32-byte fragments of the shard dtype go out through vstore_wave8 (16-bit
+  // contributions into an fp32 shard), as in allreduce_body.
+  constexpr bool kWave = E * int(sizeof(Out)) == 32;
+  static_assert(!kWave || E == 8, "wave-permuted stores take 8 four-byte elements per lane");
 
   const int64_t pos = b.pos[s];
   const int64_t n = b.numel[s];
@@ -467,6 +500,14 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
+      if constexpr (kWave) {
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+#pragma unroll
+          for (int r = 0; r < WMAX; ++r) x[u][r][k] = zero_of<In>();
+          prev[u][k] = zero_of<Out>();
+        }
+      }
       if (v < nvec) {
         const int64_t i = h + v * E;
 #pragma unroll
@@ -485,9 +526,11 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t v = int64_t(c) * VPB + int64_t(u) * kBlock + t;
-      if (v < nvec) {
-        const int64_t i = h + v * E;
+      const int64_t v0 = int64_t(c) * VPB + int64_t(u) * kBlock;  // the fragment of lane 0
+      const int64_t v = v0 + t;
+      const bool active = v < nvec;
+      const int limit = int(max_size(0, int(min_i64(nvec - v0, kBlock)))) * E;
+      if (kWave || active) {
         Out y[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
@@ -498,7 +541,11 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
           }
           y[k] = finish(acc, ACC ? prev[u][k] : zero_of<Out>());
         }
-        vstore<Out, E, true>(out + i, y);
+        if constexpr (kWave) {
+          vstore_wave8<Out>(out + h + v0 * E, y, t, limit);
+        } else {
+          vstore<Out, E, true>(out + h + v * E, y);
+        }
       }
     }
     if (c == 0 && t < h && t < n) element(t);
