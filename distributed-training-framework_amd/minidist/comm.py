@@ -240,7 +240,7 @@ _ROW_ALIGN_BYTES = 256
 class _Arena:
     """W equally laid-out rows (one per replica) of one symmetric allocation."""
 
-    __slots__ = ("data", "numel", "row_elems", "dtype", "own_base", "esize", "row_ptrs")
+    __slots__ = ("data", "numel", "row_elems", "dtype", "own_base", "esize", "row_ptrs", "target")
 
     def __init__(self, world: int, rank: int, numel: int, dtype: torch.dtype, device: torch.device):
         esize = torch.empty((), dtype=dtype).element_size()
@@ -252,6 +252,7 @@ class _Arena:
         self.esize = esize
         self.own_base = self.data[rank].data_ptr()
         self.row_ptrs = [self.data[r].data_ptr() for r in range(world)]
+        self.target: torch.Tensor | None = None  # where SUM all-reduces write (None: this rank's row)
 
     def row(self, r: int) -> torch.Tensor:
         return self.data[r, : self.numel]
@@ -327,14 +328,35 @@ class ResidentGroup:
         """Drop every symmetric buffer (views handed out keep their memory alive)."""
         self._arenas.clear()
 
+    def set_reduce_target(self, row: torch.Tensor, target: torch.Tensor) -> None:
+        """Make SUM all-reduces of ``row``'s symmetric buffer write into ``target``.
+
+        ``row`` is this rank's row as :meth:`zeros` returned it; ``target`` has
+        its dtype and at least its length, and receives the sum at the same
+        element offsets, while the row keeps this rank's contribution -- what
+        the peers read, which a real group could not overwrite while they still
+        read it.  DDP registers each bucket buffer as the target of its
+        contribution rows, so the reference's sequence ``gather_into_buffer``
+        -> ``comm.all_reduce`` -> ``scatter_from_buffer`` ends in the same state
+        as DDP's fused launch: the packed contribution in the row, the average
+        in the bucket."""
+        arena, off = self._locate(row)
+        if off != 0 or row.numel() != arena.numel:
+            raise ValueError("set_reduce_target takes the whole row that zeros() returned")
+        _native.require_device_tensor(target, "all_reduce target")
+        if target.dtype != arena.dtype or target.numel() < arena.numel:
+            raise ValueError("the reduce target must have the row's dtype and at least its length")
+        arena.target = target
+
     # -- collectives ----------------------------------------------------------
 
     def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
-        """In-place SUM over the W replicas of each tensor, rank order 0..W-1.
+        """SUM over the W replicas of each tensor, rank order 0..W-1.
 
-        Tensors living in the same symmetric buffer are reduced by one
-        dispatch (the runs must be in increasing offset order, as DDP's
-        buckets are)."""
+        In place, or into the buffer's reduce target when one is registered
+        (:meth:`set_reduce_target`).  Tensors living in the same symmetric
+        buffer are reduced by one dispatch (the runs must be in increasing
+        offset order, as DDP's buckets are)."""
         if not tensors:
             return None
         device = tensors[0].device
@@ -354,7 +376,7 @@ class ResidentGroup:
                 _native.dtype_code(arena.dtype),
                 [offs[i] for i in order],
                 [nums[i] for i in order],
-                arena.own_base,
+                arena.own_base if arena.target is None else arena.target.data_ptr(),
                 stream.cuda_stream,
             )
         return StreamWork(stream) if async_op else None

@@ -300,3 +300,46 @@ def test_found_inf_flags_alternate_across_steps(rng, graphs):
             assert same_bits(host_bits(p.grad), want["grads"][i]), f"step {step} param {i}"
         scaler.update()
         scale = scaler.scale
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_bucket_sequence_leaves_the_fused_state(rng, dtype):
+    """The reference's per-bucket sequence (ddp.py:243-247, 269-273) -- ``gather_into_buffer(1/W)``,
+    ``comm.all_reduce`` of the returned buffer, ``scatter_from_buffer`` -- over a ResidentGroup:
+    the gradients equal the oracle's, and the rows and buckets end as DDP's fused launch leaves
+    them (the packed contribution in this rank's row, the average in the bucket)."""
+    from minidist import DDP, ResidentGroup, comm
+    from test_ddp_gpu import Flat, odt, stage_peers, synthetic_grads, dev_from, host_bits
+
+    W, rank, cap = 4, 2, 0.001
+    shapes = [(33,), (64, 8), (5,), (130,), (7, 9), (3,)]
+    dts = [odt(dtype)] * len(shapes)
+    numels = [int(np.prod(s)) for s in shapes]
+    grads = synthetic_grads(rng, shapes, W, dtype, 2.0**10)
+    states = []
+    for manual in (True, False):
+        model = Flat(shapes, dtype)
+        ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap)
+        stage_peers(ddp, grads, dts, rank, W)
+        for p, g in zip(model.parameters(), grads[rank], strict=True):
+            p.grad = dev_from(g, p.shape)
+        if manual:
+            for b in ddp._buckets:
+                buf = b.gather_into_buffer(1.0 / W)
+                comm.all_reduce(buf, group=ddp.process_group, async_op=True).wait()
+                b.scatter_from_buffer()
+        else:
+            ddp.finish_gradient_sync()
+        states.append((
+            [host_bits(p.grad) for p in model.parameters()],
+            [host_bits(b.buffer) for b in ddp._buckets],
+            [host_bits(ddp.bucket_replicas(i)[rank]) for i in range(len(ddp._buckets))],
+        ))
+    want = o.ddp_pipeline(grads, dts, numels, cap, rank, None)
+    (g_m, b_m, r_m), (g_f, b_f, r_f) = states
+    for i in range(len(shapes)):
+        assert same_bits(g_m[i], want["grads"][i]), f"param {i}"
+        assert same_bits(g_f[i], g_m[i]), f"param {i}"
+    for k in range(len(b_m)):
+        assert same_bits(b_m[k], want["reduced"][k]), f"bucket {k}"
+        assert same_bits(b_f[k], b_m[k]) and same_bits(r_f[k], r_m[k]), f"bucket {k}"
