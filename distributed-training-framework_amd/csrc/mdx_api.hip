@@ -482,7 +482,7 @@ int check_pack_fused(const void* const* replicas, int world, int rank, int dtype
   f->os = os;
   f->gs = es;
   f->E = reduce_frag_elems(es, os, es);  // as the kernel's compile-time fragment
-  f->U = allreduce_unroll(world, f->E * es);
+  f->U = pack_allreduce_unroll();
   return MDX_OK;
 }
 

@@ -57,7 +57,7 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   static_assert(!PACK || (UNPACK && sizeof(G) == sizeof(In)), "the fused pack reads gradients of the wire dtype");
   constexpr int E = UNPACK ? reduce_frag_elems(int(sizeof(In)), int(sizeof(T)), int(sizeof(G)))
                             : store_frag_elems(int(sizeof(T)));
-  constexpr int U = allreduce_unroll(W, E * int(sizeof(In)));
+  constexpr int U = PACK ? pack_allreduce_unroll() : allreduce_unroll(W, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
   constexpr int EPB = VPB * E;
   // 32-byte fragments of a stored type go out through vstore_wave8, which
