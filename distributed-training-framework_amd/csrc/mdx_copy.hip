@@ -44,14 +44,13 @@ __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) 
   constexpr int EPB = kBlock * EPT;
 
   const int blk = int(blockIdx.x);
-  const int32_t* fb = tab.first_block();
-  const int s = tab.run_of(blk);
-  const int c = blk - fb[s];
-  const int nblk = fb[s + 1] - fb[s];
-  const S* src = static_cast<const S*>(tab.src(s));
-  D* dst = static_cast<D*>(tab.dst(s));
-  const int64_t n = tab.numel(s);
-  const int32_t h = tab.head(s);
+  const SpanRun run = tab.span_run(blk);
+  const int c = run.c;
+  const int nblk = run.nblk;
+  const S* src = static_cast<const S*>(run.src);
+  D* dst = static_cast<D*>(run.dst);
+  const int64_t n = run.numel;
+  const int32_t h = run.head;
   const int t = int(threadIdx.x);
   const bool zero_src = (src == nullptr);
   const CopyOp<S, D, SCALE, CHECK> op{p.scale};

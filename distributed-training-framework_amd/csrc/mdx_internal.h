@@ -209,10 +209,6 @@ __device__ __forceinline__ int find_run_in(const int32_t* first_block, int lo, i
   return lo;
 }
 
-__device__ __forceinline__ int find_run(const int32_t* first_block, int count, int blk) {
-  return find_run_in(first_block, 0, count, blk);
-}
-
 // Device plans also hold one hint per kHintBlocks workgroups: hint[g] is the
 // run that contains workgroup g * kHintBlocks, and hint[groups] = count - 1.
 // The run of workgroup blk then lies in [hint[g], hint[g + 1]], g = blk /
@@ -369,41 +365,68 @@ struct DevTable {
   int32_t count;
 };
 
+// A workgroup's run: its chunk index within the run, the run's chunk count
+// and its table fields.  Views of a kernel-argument table read run 0's fields
+// in the same round of scalar loads as the table's count and first boundary,
+// so a workgroup of run 0 -- every workgroup of a one-run dispatch, such as an
+// FSDP unit's cast -- starts its vector loads one dependent round earlier.
+struct SpanRun {
+  int c;
+  int nblk;
+  const void* src;
+  void* dst;
+  int64_t numel;
+  int32_t head;
+};
+
+struct PieceRun {
+  int c;
+  int nblk;
+  const void* own;
+  void* grad;
+  int64_t pos;
+  int64_t numel;
+  int32_t head;
+};
+
 struct SpanArgView {
   const SpanBatch& t;
-  __device__ __forceinline__ int run_of(int blk) const { return find_run(t.first_block, t.count, blk); }
-  __device__ __forceinline__ int count() const { return t.count; }
-  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
-  __device__ __forceinline__ const void* src(int i) const { return t.src[i]; }
-  __device__ __forceinline__ void* dst(int i) const { return t.dst[i]; }
-  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
-  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+  __device__ __forceinline__ SpanRun span_run(int blk) const {
+    const int32_t end0 = t.first_block[1];
+    const SpanRun r0{blk, end0, t.src[0], t.dst[0], t.numel[0], t.head[0]};
+    if (blk < end0) return r0;  // first_block[0] == 0
+    const int s = find_run_in(t.first_block, 1, t.count, blk);
+    return {blk - t.first_block[s], t.first_block[s + 1] - t.first_block[s], t.src[s], t.dst[s], t.numel[s],
+            t.head[s]};
+  }
 };
 
 struct PieceArgView {
   const PieceBatch& t;
-  __device__ __forceinline__ int run_of(int blk) const { return find_run(t.first_block, t.count, blk); }
-  __device__ __forceinline__ int count() const { return t.count; }
-  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
-  __device__ __forceinline__ const void* own(int i) const { return t.own[i]; }
-  __device__ __forceinline__ void* grad(int i) const { return t.grad[i]; }
-  __device__ __forceinline__ int64_t pos(int i) const { return t.pos[i]; }
-  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
-  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+  __device__ __forceinline__ PieceRun piece_run(int blk) const {
+    const int32_t end0 = t.first_block[1];
+    const PieceRun r0{blk, end0, t.own[0], t.grad[0], t.pos[0], t.numel[0], t.head[0]};
+    if (blk < end0) return r0;  // first_block[0] == 0
+    const int s = find_run_in(t.first_block, 1, t.count, blk);
+    return {blk - t.first_block[s], t.first_block[s + 1] - t.first_block[s], t.own[s], t.grad[s], t.pos[s],
+            t.numel[s], t.head[s]};
+  }
 };
 
+// A device plan's a / b columns hold the span's src / dst or the piece's
+// own / grad pointers.
 struct DevView {
   DevTable t;
-  __device__ __forceinline__ int run_of(int blk) const { return find_run_hinted(t.first_block, t.hint, blk); }
-  __device__ __forceinline__ int count() const { return t.count; }
-  __device__ __forceinline__ const int32_t* first_block() const { return t.first_block; }
-  __device__ __forceinline__ const void* src(int i) const { return reinterpret_cast<const void*>(t.a[i]); }
-  __device__ __forceinline__ void* dst(int i) const { return reinterpret_cast<void*>(t.b[i]); }
-  __device__ __forceinline__ const void* own(int i) const { return reinterpret_cast<const void*>(t.a[i]); }
-  __device__ __forceinline__ void* grad(int i) const { return reinterpret_cast<void*>(t.b[i]); }
-  __device__ __forceinline__ int64_t pos(int i) const { return t.pos[i]; }
-  __device__ __forceinline__ int64_t numel(int i) const { return t.numel[i]; }
-  __device__ __forceinline__ int32_t head(int i) const { return t.head[i]; }
+  __device__ __forceinline__ SpanRun span_run(int blk) const {
+    const int s = find_run_hinted(t.first_block, t.hint, blk);
+    return {blk - t.first_block[s], t.first_block[s + 1] - t.first_block[s], reinterpret_cast<const void*>(t.a[s]),
+            reinterpret_cast<void*>(t.b[s]), t.numel[s], t.head[s]};
+  }
+  __device__ __forceinline__ PieceRun piece_run(int blk) const {
+    const int s = find_run_hinted(t.first_block, t.hint, blk);
+    return {blk - t.first_block[s], t.first_block[s + 1] - t.first_block[s], reinterpret_cast<const void*>(t.a[s]),
+            reinterpret_cast<void*>(t.b[s]), t.pos[s], t.numel[s], t.head[s]};
+  }
 };
 
 // Plan blob: this header followed by the DevTable arrays at the recorded

@@ -69,13 +69,12 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   static_assert(!kWave || E == 8, "wave-permuted stores take 8 four-byte elements per lane");
 
   const int blk = int(blockIdx.x);
-  const int32_t* fb = tab.first_block();
-  const int s = tab.run_of(blk);
-  const int c = blk - fb[s];
-  const int nblk = fb[s + 1] - fb[s];
-  const int64_t pos = tab.pos(s);
-  const int64_t n = tab.numel(s);
-  const int32_t h = tab.head(s);
+  const PieceRun run = tab.piece_run(blk);
+  const int c = run.c;
+  const int nblk = run.nblk;
+  const int64_t pos = run.pos;
+  const int64_t n = run.numel;
+  const int32_t h = run.head;
   const int rank = p.rank;
   const int t = int(threadIdx.x);
   const bool unscale = (p.flags & kRedUnscale) != 0;
@@ -87,13 +86,13 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   const In* src[W];
 #pragma unroll
   for (int r = 0; r < W; ++r) {
-    src[r] = (r == rank) ? static_cast<const In*>(tab.own(s)) : static_cast<const In*>(p.peer[r]) + pos;
+    src[r] = (r == rank) ? static_cast<const In*>(run.own) : static_cast<const In*>(p.peer[r]) + pos;
   }
-  const bool own_zero = PACK && tab.own(s) == nullptr;
+  const bool own_zero = PACK && run.own == nullptr;
   In* own_row = PACK ? static_cast<In*>(const_cast<void*>(p.peer[rank])) + pos : nullptr;
   const bool pack_scale = PACK && !PRE && (p.flags & kRedPackScale) != 0;
   T* out = p.out ? static_cast<T*>(p.out) + pos : nullptr;
-  G* grad = static_cast<G*>(tab.grad(s));
+  G* grad = static_cast<G*>(run.grad);
   bool bad = false;
   // The next step's found-inf flag rides on the fused pack (nothing reads or
   // sets it during this step): one lane of the first workgroup.
@@ -436,7 +435,7 @@ hipError_t launch_pack_dev_for(int world, const DevTable& t, int blocks, const R
 enum : int { kPreNone = 0, kPreMul = 1, kPreDiv = 2 };
 
 template <typename In, typename Acc, typename Out, int WMAX, int PRE, bool ACC>
-__device__ __forceinline__ void share_body(const PieceBatch& b, const ReduceParams& p, int s, int c, int nblk) {
+__device__ __forceinline__ void share_body(const PieceRun& run, const ReduceParams& p) {
   constexpr int E = reduce_frag_elems(int(sizeof(In)), int(sizeof(Out)), int(sizeof(Out)));
   constexpr int U = share_unroll(WMAX, E * int(sizeof(In)));
   constexpr int VPB = kBlock * U;
@@ -446,12 +445,14 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
   constexpr bool kWave = E * int(sizeof(Out)) == 32;
   static_assert(!kWave || E == 8, "wave-permuted stores take 8 four-byte elements per lane");
 
-  const int64_t pos = b.pos[s];
-  const int64_t n = b.numel[s];
-  const int32_t h = b.head[s];
+  const int c = run.c;
+  const int nblk = run.nblk;
+  const int64_t pos = run.pos;
+  const int64_t n = run.numel;
+  const int32_t h = run.head;
   const int world = p.world;
   const int rank = p.rank;
-  const bool own_zero = (b.own[s] == nullptr);
+  const bool own_zero = (run.own == nullptr);
   const int t = int(threadIdx.x);
   const float pre = p.pre;
   const bool unscale = (p.flags & kRedUnscale) != 0;
@@ -460,7 +461,7 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
   const In* src[WMAX];
 #pragma unroll
   for (int r = 0; r < WMAX; ++r) {
-    src[r] = (r == rank) ? static_cast<const In*>(b.own[s]) : static_cast<const In*>(p.peer[r]) + pos;
+    src[r] = (r == rank) ? static_cast<const In*>(run.own) : static_cast<const In*>(p.peer[r]) + pos;
   }
   Out* out = static_cast<Out*>(p.out) + pos;
   bool bad = false;
@@ -563,20 +564,17 @@ __device__ __forceinline__ void share_body(const PieceBatch& b, const ReducePara
 
 template <typename In, typename Acc, typename Out, int WMAX>
 __global__ void __launch_bounds__(kBlock) share_kernel(PieceBatch b, ReduceParams p) {
-  const int blk = int(blockIdx.x);
-  const int s = find_run(b.first_block, b.count, blk);
-  const int c = blk - b.first_block[s];
-  const int nblk = b.first_block[s + 1] - b.first_block[s];
+  const PieceRun run = PieceArgView{b}.piece_run(int(blockIdx.x));
   const bool acc = (p.flags & kRedAccumulate) != 0;
   if (p.flags & kRedPreMul) {
-    if (acc) share_body<In, Acc, Out, WMAX, kPreMul, true>(b, p, s, c, nblk);
-    else share_body<In, Acc, Out, WMAX, kPreMul, false>(b, p, s, c, nblk);
+    if (acc) share_body<In, Acc, Out, WMAX, kPreMul, true>(run, p);
+    else share_body<In, Acc, Out, WMAX, kPreMul, false>(run, p);
   } else if (p.flags & kRedPreDiv) {
-    if (acc) share_body<In, Acc, Out, WMAX, kPreDiv, true>(b, p, s, c, nblk);
-    else share_body<In, Acc, Out, WMAX, kPreDiv, false>(b, p, s, c, nblk);
+    if (acc) share_body<In, Acc, Out, WMAX, kPreDiv, true>(run, p);
+    else share_body<In, Acc, Out, WMAX, kPreDiv, false>(run, p);
   } else {
-    if (acc) share_body<In, Acc, Out, WMAX, kPreNone, true>(b, p, s, c, nblk);
-    else share_body<In, Acc, Out, WMAX, kPreNone, false>(b, p, s, c, nblk);
+    if (acc) share_body<In, Acc, Out, WMAX, kPreNone, true>(run, p);
+    else share_body<In, Acc, Out, WMAX, kPreNone, false>(run, p);
   }
 }
 
