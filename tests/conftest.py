@@ -72,6 +72,16 @@ def first_mismatch(a: np.ndarray, b: np.ndarray) -> str:
     return f"{idx.size} mismatches; first at {i}: {a[i]!r} ({int(ua[i]):#x}) vs {b[i]!r} ({int(ub[i]):#x})"
 
 
+def bf16_bits_torch(u):
+    """The oracle's fp32 -> bf16 rounding (round to nearest even, NaN -> 0xFFFF) on int64
+    tensors of fp32 bit patterns in [0, 2^32), as torch integer ops, so that it can be
+    evaluated on the device over all 2^32 patterns.  Returns int64 values in [0, 0xFFFF].
+    test_oracle.py checks it against oracle.gradpath.bf16_from_f32."""
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return r.masked_fill(nan, 0xFFFF)
+
+
 @pytest.fixture(scope="session")
 def rng():
     return np.random.default_rng(1234)

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import first_mismatch, load_golden, same_bits
+from conftest import bf16_bits_torch, first_mismatch, load_golden, same_bits
 from minidist import _native as nat
 from oracle import gradpath as o
 
@@ -383,6 +383,28 @@ def test_cast_matches_golden_and_ties():
         dst = empty_dev(x.size, o.BF16)
         nat.cast_f32_bf16(src.data_ptr(), dst.data_ptr(), x.size, stream())
         assert np.array_equal(to_host(dst), want), first_mismatch(to_host(dst), want)
+
+
+def test_cast_exhaustive():
+    """All 2^32 fp32 bit patterns, in 16 dispatches of 2^28, through mdx_cast_f32_bf16 against
+    the oracle's rounding (bf16_bits_torch, evaluated on the device): every non-NaN input,
+    ties, subnormals and overflow to inf included, and every NaN -> 0xFFFF."""
+    chunk = 1 << 28
+    for c in range(16):
+        u = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int64, device=DEV)
+        x = (u - ((u >> 31) << 32)).to(torch.int32).view(torch.float32)
+        dst = torch.empty(chunk, dtype=torch.int16, device=DEV)
+        nat.cast_f32_bf16(x.data_ptr(), dst.data_ptr(), chunk, stream())
+        got = dst.to(torch.int64) & 0xFFFF
+        want = bf16_bits_torch(u)
+        bad = torch.nonzero(got != want)
+        if bad.numel():
+            i = int(bad[0])
+            pytest.fail(
+                f"chunk {c}: {bad.numel()} mismatches; first input {int(u[i]):#010x} -> "
+                f"{int(got[i]):#06x}, want {int(want[i]):#06x}"
+            )
+        del u, x, dst, got, want, bad
 
 
 def _cast_f16(x: np.ndarray) -> np.ndarray:

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import GOLDEN, first_mismatch, load_golden, same_bits
+from conftest import GOLDEN, bf16_bits_torch, first_mismatch, load_golden, same_bits
 from oracle import gradpath as o
 
 
@@ -65,6 +65,17 @@ def test_bf16_structured_sweep_matches_torch():
     x = u.view(np.float32)
     got = o.bf16_from_f32(x)
     want = _torch_bits(torch.from_numpy(x.copy()).to(torch.bfloat16))
+    assert np.array_equal(got, want), first_mismatch(got, want)
+
+
+def test_bf16_torch_restatement_matches_oracle(rng):
+    """The integer torch form used by the exhaustive device test equals the oracle on every
+    (sign, exponent, top-7 mantissa) pattern x tie-deciding low halves, and on random patterns."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << np.uint32(16)
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x4000, 0xC000], dtype=np.uint32)
+    u = np.concatenate([(hi[:, None] | lows[None, :]).reshape(-1), rng.integers(0, 1 << 32, 1 << 20, dtype=np.uint32)])
+    got = bf16_bits_torch(torch.from_numpy(u.astype(np.int64))).numpy().astype(np.uint16)
+    want = o.bf16_from_f32(u.view(np.float32))
     assert np.array_equal(got, want), first_mismatch(got, want)
 
 
