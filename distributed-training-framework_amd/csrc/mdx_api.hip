@@ -301,6 +301,7 @@ int plan_view(const void* plan, const void* d_plan, int32_t kind, const PlanHead
   t->pos = reinterpret_cast<const int64_t*>(d + h->off_pos);
   t->hint = reinterpret_cast<const int32_t*>(d + h->off_hint);
   t->count = h->count;
+  t->base = 0;
   *hdr = h;
   return MDX_OK;
 }

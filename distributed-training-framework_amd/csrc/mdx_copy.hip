@@ -43,7 +43,7 @@ __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) 
   constexpr int EPT = U * E;
   constexpr int EPB = kBlock * EPT;
 
-  const int blk = int(blockIdx.x);
+  const int blk = tab.block();
   const SpanRun run = tab.span_run(blk);
   const int c = run.c;
   const int nblk = run.nblk;
@@ -141,8 +141,9 @@ struct DevLaunch {
   int blocks;
   template <typename S, typename D, int SCALE, bool CHECK>
   hipError_t go(const CopyParams& p, hipStream_t stream) const {
-    hipLaunchKernelGGL((copy_kernel_dev<S, D, SCALE, CHECK>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
-    return hipGetLastError();
+    return launch_plan_slices(t, blocks, [&](const DevTable& slice, int grid) {
+      hipLaunchKernelGGL((copy_kernel_dev<S, D, SCALE, CHECK>), dim3(grid), dim3(kBlock), 0, stream, slice, p);
+    });
   }
 };
 

@@ -362,7 +362,30 @@ struct DevTable {
   const uint64_t* b;  // span: dst    piece: grad
   const int64_t* pos;  // piece position (pieces only)
   int32_t count;
+  int32_t base;  // plan workgroup of this dispatch's first workgroup (see launch_plan_slices)
 };
+
+// A dispatch holds at most 2^32 - 1 work-items (the AQL packet's grid size is
+// 32-bit), 2^26 - 1 workgroups of kBlock lanes.  A plan with more workgroups
+// than kPlanSliceBlocks goes out as several dispatches in stream order, each
+// covering the plan's workgroups [base, base + grid); the slice (2^22
+// workgroups, at least 2^30 elements) keeps the extra dispatch boundaries far
+// below a percent of the work.  Kernel-argument batches stay under the limit
+// by construction (kRunsPerLaunch runs of at most kMaxRunElems elements).
+constexpr int kPlanSliceBlocks = 1 << 22;
+static_assert(int64_t(kRunsPerLaunch) * kMaxRunElems / kBlock < (int64_t(1) << 32) / kBlock,
+              "a kernel-argument batch fits one dispatch");
+
+template <typename Launch>
+hipError_t launch_plan_slices(DevTable t, int blocks, Launch&& launch) {
+  for (int64_t b0 = 0; b0 < blocks; b0 += kPlanSliceBlocks) {
+    t.base = int32_t(b0);
+    launch(t, int(min_i64(kPlanSliceBlocks, blocks - b0)));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 // A workgroup's run: its chunk index within the run, the run's chunk count
 // and its table fields.  Views of a kernel-argument table read run 0's fields
@@ -390,6 +413,7 @@ struct PieceRun {
 
 struct SpanArgView {
   const SpanBatch& t;
+  __device__ __forceinline__ int block() const { return int(blockIdx.x); }
   __device__ __forceinline__ SpanRun span_run(int blk) const {
     const int32_t end0 = t.first_block[1];
     const SpanRun r0{blk, end0, t.src[0], t.dst[0], t.numel[0], t.head[0]};
@@ -402,6 +426,7 @@ struct SpanArgView {
 
 struct PieceArgView {
   const PieceBatch& t;
+  __device__ __forceinline__ int block() const { return int(blockIdx.x); }
   __device__ __forceinline__ PieceRun piece_run(int blk) const {
     const int32_t end0 = t.first_block[1];
     const PieceRun r0{blk, end0, t.own[0], t.grad[0], t.pos[0], t.numel[0], t.head[0]};
@@ -416,6 +441,7 @@ struct PieceArgView {
 // own / grad pointers.
 struct DevView {
   DevTable t;
+  __device__ __forceinline__ int block() const { return t.base + int(blockIdx.x); }
   __device__ __forceinline__ SpanRun span_run(int blk) const {
     const int s = find_run_hinted(t.first_block, t.hint, blk);
     return {blk - t.first_block[s], t.first_block[s + 1] - t.first_block[s], reinterpret_cast<const void*>(t.a[s]),

@@ -68,7 +68,7 @@ __device__ __forceinline__ void allreduce_body(const View& tab, const ReducePara
   constexpr bool kWave = kWaveT || kWaveG;
   static_assert(!kWave || E == 8, "wave-permuted stores take 8 four-byte elements per lane");
 
-  const int blk = int(blockIdx.x);
+  const int blk = tab.block();
   const PieceRun run = tab.piece_run(blk);
   const int c = run.c;
   const int nblk = run.nblk;
@@ -287,8 +287,9 @@ struct DevAllreduceUnpack {
   int blocks;
   template <int W>
   hipError_t go(const ReduceParams& p, hipStream_t stream) const {
-    hipLaunchKernelGGL((allreduce_unpack_kernel_dev<T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
-    return hipGetLastError();
+    return launch_plan_slices(t, blocks, [&](const DevTable& slice, int grid) {
+      hipLaunchKernelGGL((allreduce_unpack_kernel_dev<T, G, W>), dim3(grid), dim3(kBlock), 0, stream, slice, p);
+    });
   }
 };
 
@@ -309,8 +310,9 @@ struct DevWide {
   int blocks;
   template <int W>
   hipError_t go(const ReduceParams& p, hipStream_t stream) const {
-    hipLaunchKernelGGL((allreduce_wide_kernel_dev<In, T, G, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
-    return hipGetLastError();
+    return launch_plan_slices(t, blocks, [&](const DevTable& slice, int grid) {
+      hipLaunchKernelGGL((allreduce_wide_kernel_dev<In, T, G, W>), dim3(grid), dim3(kBlock), 0, stream, slice, p);
+    });
   }
 };
 
@@ -331,8 +333,9 @@ struct DevPack {
   int blocks;
   template <int W>
   hipError_t go(const ReduceParams& p, hipStream_t stream) const {
-    hipLaunchKernelGGL((allreduce_pack_kernel_dev<In, T, W>), dim3(blocks), dim3(kBlock), 0, stream, t, p);
-    return hipGetLastError();
+    return launch_plan_slices(t, blocks, [&](const DevTable& slice, int grid) {
+      hipLaunchKernelGGL((allreduce_pack_kernel_dev<In, T, W>), dim3(grid), dim3(kBlock), 0, stream, slice, p);
+    });
   }
 };
 

@@ -172,6 +172,60 @@ def test_pack_allreduce_unpack_run_past_the_run_limit(rng):
     assert flag.item() == 0
 
 
+@pytest.mark.parametrize("copy_plan", [False, True])
+def test_plan_larger_than_one_dispatch(rng, copy_plan):
+    """A plan of more than 2^22 workgroups (the slice a dispatch takes; 2^30 + 2^20 fp32 elements
+    in three gradients) goes out as several dispatches: every element is checked against the same
+    IEEE ops in torch on the device, and windows at the ends and across the first slice boundary
+    (workgroup 2^22 of 256 elements) against the oracle.  ``copy_plan`` runs the pack's copy plan
+    (mdx_pack_planned, x 1/2) instead of the fused plan."""
+    W, rank, inv = 2, 1, 2.0**-10
+    numels = [(1 << 29) - 3, (1 << 29) + (1 << 20) - 1000, 1003]
+    offs = [1, 1 + numels[0] + 2, 1 + numels[0] + 2 + numels[1] + 5]
+    extent = offs[-1] + numels[-1] + 3
+    gen = torch.Generator(device=DEV).manual_seed(77)
+    grads = [torch.randn(n, device=DEV, generator=gen) for n in numels]
+    if copy_plan:
+        dst = torch.full((extent,), float(SENTINEL[o.F32]), device=DEV)
+        plan = nat.plan_spans(nat.spans_array([(g.data_ptr(), dst.data_ptr() + 4 * a, n)
+                                               for g, a, n in zip(grads, offs, numels)]),
+                              nat.MDX_F32, nat.MDX_F32, DEV)
+        nat.pack_planned(plan, nat.f32(1.0 / W), False, stream())
+        for g, a, n in zip(grads, offs, numels):
+            assert torch.equal(dst[a : a + n], g * 0.5)
+        windows = [(0, 0, 4096), (1, (1 << 30) - numels[0] - 4096, 8192), (2, 0, numels[2])]
+        for k, lo, m in windows:
+            want = o.mul_scalar(to_host(grads[k][lo : lo + m]), o.F32, 1.0 / W)
+            got = to_host(dst[offs[k] + lo : offs[k] + lo + m])
+            assert same_bits(got, want), first_mismatch(got, want)
+        return
+    peer = torch.randn(extent, device=DEV, generator=gen)
+    own = torch.full((extent,), float(SENTINEL[o.F32]), device=DEV)
+    out = torch.full((extent,), float(SENTINEL[o.F32]), device=DEV)
+    runs = nat.pack_runs_array([(a, n, g.data_ptr(), g.data_ptr()) for g, a, n in zip(grads, offs, numels)])
+    plan = nat.plan_pack_allreduce_unpack([peer.data_ptr(), own.data_ptr()], rank, nat.MDX_F32, runs, out.data_ptr(),
+                                          nat.MDX_F32, nat.f32(1.0 / W), DEV)
+    windows = [(0, 0, 4096), (1, (1 << 30) - numels[0] - 4096, 8192), (2, 0, numels[2])]
+    before = [(k, lo, m, to_host(grads[k][lo : lo + m])) for k, lo, m in windows]
+    packed = [g * 0.5 for g in grads]
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nxt = torch.ones(1, dtype=torch.int32, device=DEV)
+    nat.pack_allreduce_unpack_planned(plan, nat.f32(inv), flag.data_ptr(), nxt.data_ptr(), stream())
+    for g, pk, a, n in zip(grads, packed, offs, numels):
+        assert torch.equal(own[a : a + n], pk)
+        acc = peer[a : a + n] + pk
+        assert torch.equal(out[a : a + n], acc)
+        assert torch.equal(g, acc * inv)
+    for k, lo, m, src_host in before:
+        a = offs[k] + lo
+        peers_host = [to_host(peer[a : a + m]), None]
+        want_row, want_acc, want_g = _want(src_host, peers_host, 0, m, W, rank, o.F32, o.F32, inv)
+        for got, want in ((own[a : a + m], want_row), (out[a : a + m], want_acc), (grads[k][lo : lo + m], want_g)):
+            got = to_host(got)
+            assert same_bits(got, want), first_mismatch(got, want)
+    assert flag.item() == 0 and nxt.item() == 0
+
+
 @pytest.mark.parametrize("planned", [False, True])
 def test_pack_allreduce_unpack_nothing_to_do_still_clears(planned):
     reps = [torch.zeros(64, device=DEV) for _ in range(2)]
