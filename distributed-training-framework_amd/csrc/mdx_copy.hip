@@ -120,19 +120,31 @@ __global__ void __launch_bounds__(kBlock) copy_kernel(SpanBatch b, CopyParams p)
   copy_body<S, D, SCALE, CHECK>(SpanArgView{b}, p);
 }
 
+// One run in the kernel-argument segment.
+template <typename S, typename D, int SCALE, bool CHECK>
+__global__ void __launch_bounds__(kBlock) copy_kernel_one(SpanOne b, CopyParams p) {
+  copy_body<S, D, SCALE, CHECK>(SpanOneView{b}, p);
+}
+
 // Table (plan) in device memory.
 template <typename S, typename D, int SCALE, bool CHECK>
 __global__ void __launch_bounds__(kBlock) copy_kernel_dev(DevTable t, CopyParams p) {
   copy_body<S, D, SCALE, CHECK>(DevView{t}, p);
 }
 
-// Either table kind: Batch = SpanBatch (grid from its prefix) or DevTable.
+// Either table kind: a kernel-argument SpanBatch (grid from its prefix; one run goes
+// out as a SpanOne) or a DevTable.
 struct ArgLaunch {
   const SpanBatch& b;
   template <typename S, typename D, int SCALE, bool CHECK>
   hipError_t go(const CopyParams& p, hipStream_t stream) const {
-    hipLaunchKernelGGL((copy_kernel<S, D, SCALE, CHECK>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
-                       stream, b, p);
+    if (b.count == 1) {
+      hipLaunchKernelGGL((copy_kernel_one<S, D, SCALE, CHECK>), dim3(b.first_block[1]), dim3(kBlock), 0, stream,
+                         one_run_of(b), p);
+    } else {
+      hipLaunchKernelGGL((copy_kernel<S, D, SCALE, CHECK>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
+                         stream, b, p);
+    }
     return hipGetLastError();
   }
 };

@@ -566,8 +566,7 @@ __device__ __forceinline__ void share_body(const PieceRun& run, const ReducePara
 }
 
 template <typename In, typename Acc, typename Out, int WMAX>
-__global__ void __launch_bounds__(kBlock) share_kernel(PieceBatch b, ReduceParams p) {
-  const PieceRun run = PieceArgView{b}.piece_run(int(blockIdx.x));
+__device__ __forceinline__ void share_run(const PieceRun& run, const ReduceParams& p) {
   const bool acc = (p.flags & kRedAccumulate) != 0;
   if (p.flags & kRedPreMul) {
     if (acc) share_body<In, Acc, Out, WMAX, kPreMul, true>(run, p);
@@ -582,9 +581,25 @@ __global__ void __launch_bounds__(kBlock) share_kernel(PieceBatch b, ReduceParam
 }
 
 template <typename In, typename Acc, typename Out, int WMAX>
+__global__ void __launch_bounds__(kBlock) share_kernel(PieceBatch b, ReduceParams p) {
+  share_run<In, Acc, Out, WMAX>(PieceArgView{b}.piece_run(int(blockIdx.x)), p);
+}
+
+// One piece (an FSDP unit's shard) in the kernel-argument segment.
+template <typename In, typename Acc, typename Out, int WMAX>
+__global__ void __launch_bounds__(kBlock) share_kernel_one(PieceOne b, ReduceParams p) {
+  share_run<In, Acc, Out, WMAX>(PieceOneView{b}.piece_run(int(blockIdx.x)), p);
+}
+
+template <typename In, typename Acc, typename Out, int WMAX>
 hipError_t launch_share_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
-  const int blocks = b.first_block[b.count];
-  hipLaunchKernelGGL((share_kernel<In, Acc, Out, WMAX>), dim3(blocks), dim3(kBlock), 0, stream, b, p);
+  if (b.count == 1) {
+    hipLaunchKernelGGL((share_kernel_one<In, Acc, Out, WMAX>), dim3(b.first_block[1]), dim3(kBlock), 0, stream,
+                       one_run_of(b), p);
+  } else {
+    hipLaunchKernelGGL((share_kernel<In, Acc, Out, WMAX>), dim3(b.first_block[b.count]), dim3(kBlock), 0, stream,
+                       b, p);
+  }
   return hipGetLastError();
 }
 
