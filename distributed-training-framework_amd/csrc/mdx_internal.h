@@ -9,6 +9,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <climits>
 #include <stdint.h>
 
 #include "mdx.h"
@@ -467,6 +468,59 @@ inline SpanOne one_run_of(const SpanBatch& b) {
 inline PieceOne one_run_of(const PieceBatch& b) {
   return {b.own[0], b.grad[0], b.pos[0], b.numel[0], b.head[0], b.first_block[1]};
 }
+
+// Few-piece tables: up to kFewRuns pieces (an FSDP shard that spans a few
+// parameters).  Every field of every piece is read in the same scalar round
+// and the workgroup's piece is picked with compares and selects, so no load
+// waits on another; the table is ~170 bytes instead of ~1.9 KB.
+constexpr int kFewRuns = 4;
+
+struct PieceFew {
+  const void* own[kFewRuns];
+  void* grad[kFewRuns];
+  int64_t pos[kFewRuns];
+  int64_t numel[kFewRuns];
+  int32_t head[kFewRuns];
+  int32_t first_block[kFewRuns + 1];  // entries past the last piece hold INT32_MAX
+};
+
+inline PieceFew few_runs_of(const PieceBatch& b) {
+  PieceFew f{};
+  for (int k = 0; k < kFewRuns; ++k) {
+    const bool used = k < b.count;
+    f.own[k] = used ? b.own[k] : nullptr;
+    f.grad[k] = used ? b.grad[k] : nullptr;
+    f.pos[k] = used ? b.pos[k] : 0;
+    f.numel[k] = used ? b.numel[k] : 0;
+    f.head[k] = used ? b.head[k] : -1;
+  }
+  for (int k = 0; k <= kFewRuns; ++k) f.first_block[k] = k <= b.count ? b.first_block[k] : INT32_MAX;
+  return f;
+}
+
+struct PieceFewView {
+  const PieceFew& t;
+  __device__ __forceinline__ int block() const { return int(blockIdx.x); }
+  __device__ __forceinline__ PieceRun piece_run(int blk) const {
+    int32_t lo = t.first_block[0], hi = t.first_block[1];
+    const void* own = t.own[0];
+    void* grad = t.grad[0];
+    int64_t pos = t.pos[0], numel = t.numel[0];
+    int32_t head = t.head[0];
+#pragma unroll
+    for (int k = 1; k < kFewRuns; ++k) {
+      const bool in = blk >= t.first_block[k];
+      lo = in ? t.first_block[k] : lo;
+      hi = in ? t.first_block[k + 1] : hi;
+      own = in ? t.own[k] : own;
+      grad = in ? t.grad[k] : grad;
+      pos = in ? t.pos[k] : pos;
+      numel = in ? t.numel[k] : numel;
+      head = in ? t.head[k] : head;
+    }
+    return {blk - lo, hi - lo, own, grad, pos, numel, head};
+  }
+};
 
 struct SpanOneView {
   const SpanOne& t;

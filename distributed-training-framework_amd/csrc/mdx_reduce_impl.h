@@ -591,11 +591,20 @@ __global__ void __launch_bounds__(kBlock) share_kernel_one(PieceOne b, ReducePar
   share_run<In, Acc, Out, WMAX>(PieceOneView{b}.piece_run(int(blockIdx.x)), p);
 }
 
+// Up to kFewRuns pieces in the kernel-argument segment.
+template <typename In, typename Acc, typename Out, int WMAX>
+__global__ void __launch_bounds__(kBlock) share_kernel_few(PieceFew b, ReduceParams p) {
+  share_run<In, Acc, Out, WMAX>(PieceFewView{b}.piece_run(int(blockIdx.x)), p);
+}
+
 template <typename In, typename Acc, typename Out, int WMAX>
 hipError_t launch_share_w(const PieceBatch& b, const ReduceParams& p, hipStream_t stream) {
   if (b.count == 1) {
     hipLaunchKernelGGL((share_kernel_one<In, Acc, Out, WMAX>), dim3(b.first_block[1]), dim3(kBlock), 0, stream,
                        one_run_of(b), p);
+  } else if (b.count <= kFewRuns) {
+    hipLaunchKernelGGL((share_kernel_few<In, Acc, Out, WMAX>), dim3(b.first_block[b.count]), dim3(kBlock), 0,
+                       stream, few_runs_of(b), p);
   } else {
     hipLaunchKernelGGL((share_kernel<In, Acc, Out, WMAX>), dim3(b.first_block[b.count]), dim3(kBlock), 0, stream,
                        b, p);

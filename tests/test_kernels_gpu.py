@@ -322,7 +322,20 @@ def test_allreduce_unpack_rejects_grad_overlapping_a_replica():
 @pytest.mark.parametrize("W,rank", [(1, 0), (2, 1), (3, 2), (4, 0), (8, 5)])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_reduce_scatter_share_matches_oracle(rng, idt, rdt, sdt, W, rank, accumulate):
-    numels = [7, 12, 5, 33, 640, 3, 4099, 1]
+    _share_case(rng, [7, 12, 5, 33, 640, 3, 4099, 1], idt, rdt, sdt, W, rank, accumulate)
+
+
+@pytest.mark.parametrize("k", range(7))
+@pytest.mark.parametrize("idt", [o.BF16, o.F32])
+def test_reduce_scatter_share_piece_counts(rng, k, idt):
+    """Rank 0's shard covers k whole parameters and part of one more: k + 1 pieces, across the
+    one-piece, few-piece (up to 4) and full kernel-argument tables."""
+    numels = [37 + 64 * i for i in range(k)]
+    numels.append(sum(numels) + 4100 + 8 * k)
+    _share_case(rng, numels, idt, o.F32, o.F32, 2, 0, k % 2 == 1)
+
+
+def _share_case(rng, numels, idt, rdt, sdt, W, rank, accumulate):
     total = sum(numels)
     S = (total + W - 1) // W
     P = S * W
