@@ -516,8 +516,8 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"share_kernel<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
-                      "(mdx_reduce_scatter_share)",
+            "kernel": f"share_kernel_few<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
+                      "(mdx_reduce_scatter_share; rank 0's shard is 3 parameter pieces)",
             "achieved": round(share_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
