@@ -301,6 +301,42 @@ def test_allreduce_unpack_matches_oracle(rng, bdt, gdt, W, inv_scale, write_out)
     assert bool(flag.item()) == any_bad
 
 
+@pytest.mark.parametrize("wide", [False, True])
+def test_allreduce_unpack_plan_larger_than_one_dispatch(wide):
+    """The two-dispatch pipeline's planned all-reduce + unpack over more than 2^22 workgroups, sent
+    as several dispatches: W = 8 fp32 contributions (256 elements per workgroup), or 8 bf16
+    contributions widened, x 1/8 and summed into an fp32 bucket (512 per workgroup).  Every element
+    is checked against the same IEEE ops in torch on the device: the rank-ordered sum, then the
+    gradient converted and unscaled."""
+    W, inv = 8, 2.0**-10
+    per_block = 512 if wide else 256
+    n = (1 << 22) * per_block + (1 << 18)
+    wdt = torch.bfloat16 if wide else torch.float32
+    gen = torch.Generator(device=DEV).manual_seed(91)
+    reps = [torch.randn(n + 8, device=DEV, generator=gen).to(wdt) for _ in range(W)]
+    out = torch.empty(n + 8, dtype=torch.float32, device=DEV)
+    grad = torch.empty(n, dtype=wdt, device=DEV)
+    runs = nat.grad_runs_array([(4, n, grad.data_ptr())])
+    ptrs = [r.data_ptr() for r in reps]
+    if wide:
+        plan = nat.plan_allreduce_unpack_wide(ptrs, nat.MDX_BF16, runs, out.data_ptr(), nat.MDX_F32, nat.MDX_BF16,
+                                              nat.f32(1.0 / W), DEV)
+    else:
+        plan = nat.plan_allreduce_unpack(ptrs, nat.MDX_F32, runs, out.data_ptr(), nat.MDX_F32, DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    nat.allreduce_unpack_planned(plan, nat.f32(inv), flag.data_ptr(), stream())
+    acc = None
+    for r in reps:
+        x = r[4 : 4 + n].float()
+        x = x * (1.0 / W) if wide else x  # exact: a power of two on normal values
+        acc = x if acc is None else acc + x
+        del x
+    assert torch.equal(out[4 : 4 + n], acc)
+    want = (acc.to(wdt).float() * inv).to(wdt) if wide else acc * inv
+    assert torch.equal(grad, want)
+    assert flag.item() == 0
+
+
 def test_allreduce_unpack_rejects_grad_overlapping_a_replica():
     reps = [torch.zeros(1024, device=DEV) for _ in range(2)]
     runs = nat.grad_runs_array([(0, 16, reps[1][4:].data_ptr())])  # inside the reduced extent
