@@ -371,6 +371,19 @@ def test_reduce_scatter_share_piece_counts(rng, k, idt):
     _share_case(rng, numels, idt, o.F32, o.F32, 2, 0, k % 2 == 1)
 
 
+@pytest.mark.parametrize("seed", range(40))
+def test_reduce_scatter_share_fuzz(seed):
+    """Seeded random shares: 1-10 parameters of 1-5000 elements, W in [2, 16], any rank, fp32 / bf16 /
+    fp16 contributions into an fp32 shard, with or without accumulation -- shards of one piece, a
+    few pieces or many, against the oracle."""
+    r = np.random.default_rng(1000 + seed)
+    W = int(r.integers(2, 17))
+    rank = int(r.integers(0, W))
+    numels = [int(x) for x in r.integers(1, 5000, int(r.integers(1, 11)))]
+    idt = (o.F32, o.BF16, o.F16)[seed % 3]
+    _share_case(r, numels, idt, o.F32, o.F32, W, rank, seed % 2 == 1)
+
+
 def _share_case(rng, numels, idt, rdt, sdt, W, rank, accumulate):
     total = sum(numels)
     S = (total + W - 1) // W
