@@ -259,7 +259,10 @@ MDX_API int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, vo
  * copy is what the workgroups read -- for as long as the addresses inside
  * stay valid.  This is the device-side pointer/offset table that lets the
  * ~150 gradients of a GPT-2 step (most of them small biases and norms) move
- * in one launch per stage.
+ * in one launch per stage.  A plan of more than 2^22 workgroups (2^30 or more
+ * elements; one dispatch holds at most 2^32 - 1 work-items) goes out as
+ * several dispatches in stream order over consecutive slices of its
+ * workgroups: "one dispatch" below means one per 2^22 workgroups.
  *
  * Sizing: on entry *plan_bytes is the capacity of `plan`; on return it is the
  * size the plan needs.  With plan == NULL or too small a capacity nothing is
