@@ -469,6 +469,26 @@ def test_cast_exhaustive():
         del u, x, dst, got, want, bad
 
 
+@pytest.mark.parametrize("sdt,ddt", [(o.F32, o.BF16), (o.F32, o.F16), (o.BF16, o.F32), (o.F32, o.F32)])
+def test_single_span_pack_every_misalignment(rng, sdt, ddt):
+    """One span per call (the one-run kernel-argument table): source and destination at every
+    element offset 0-7 of a 16-byte line, lengths from 1 to a few thousand, x 1/8 -- the
+    alignment head, the vector body and the ragged tail, against the oracle; the destination's
+    neighbours keep their sentinels."""
+    for so in range(8):
+        for do in range(8):
+            n = int(rng.integers(1, 3000)) if (so + do) % 3 else int(rng.integers(1, 24))
+            x = values(rng, n + 16, sdt, scale=4.0)
+            src = to_dev(x)
+            dst = empty_dev(n + 16, ddt)
+            nat.pack(nat.spans_array([(src.data_ptr() + so * esize(sdt), dst.data_ptr() + do * esize(ddt), n)]),
+                     code(sdt), code(ddt), nat.f32(0.125), False, stream())
+            got = to_host(dst)
+            want = o.mul_scalar(o.convert(x[so : so + n], sdt, ddt), ddt, 0.125)
+            assert same_bits(got[do : do + n], want), (so, do, n, first_mismatch(got[do : do + n], want))
+            assert np.all(got[:do] == SENTINEL[ddt]) and np.all(got[do + n :] == SENTINEL[ddt]), (so, do, n)
+
+
 def _cast_f16(x: np.ndarray) -> np.ndarray:
     """fp32 -> fp16 through the pack entry point (one span, scale 1): the gather cast for
     param_dtype = float16.  Returns the fp16 bit patterns."""
