@@ -60,7 +60,9 @@ def _capture(store):
 
 @pytest.mark.parametrize("W", [2, 4, 3])
 @pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_shard_grads_match_oracle_and_full_batch(W, param_dtype):
+@pytest.mark.parametrize("comm_streams", [False, True])
+def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams):
+    """With ``comm_streams`` the gathers and reduce-scatters run on side streams: the same bits."""
     c = tiny_gpt.Config(n_layer=3)
     ids, tgt = tiny_gpt.batch(c, 12 if W == 3 else 8, seed=1234)
     rank = W - 1
@@ -70,7 +72,8 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype):
     for p in model.parameters():
         p.register_post_accumulate_grad_hook(_capture(captured))
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
-    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
+                comm_streams=comm_streams)
     # peers' gradients are computed by replicas whose parameters are the gathered (param_dtype) values
     replica = []
     for r in range(W):
@@ -115,14 +118,15 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype):
             assert rel <= 1e-6
 
 
-def test_unshard_casts_into_own_slot_and_gathers_peers():
+@pytest.mark.parametrize("comm_streams", [False, True])
+def test_unshard_casts_into_own_slot_and_gathers_peers(comm_streams):
     c = tiny_gpt.Config()
     W, rank = 4, 2
     model = tiny_gpt.GPT(c).to(DEV)
     init = {n: p.detach().clone() for n, p in model.named_parameters()}
     fsdp = FSDP(
         model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV),
-        mixed_precision=MixedPrecisionPolicy(param_dtype=torch.bfloat16),
+        mixed_precision=MixedPrecisionPolicy(param_dtype=torch.bfloat16), comm_streams=comm_streams,
     )
     with fsdp.summon_full_params():
         for n, p in model.named_parameters():
@@ -146,19 +150,22 @@ def test_sharding_is_real_and_unit_count():
         assert s["fsdp_state_MB"] < s["ddp_state_MB"]
 
 
-def test_no_sync_accumulates_then_flushes():
+@pytest.mark.parametrize("comm_streams", [False, True])
+def test_no_sync_accumulates_then_flushes(comm_streams):
     """Reference tests/test_fsdp.py:214-238 on one GPU (world emulated, peers zero)."""
     c = tiny_gpt.Config()
     W, rank = 2, 1
     ids, tgt = tiny_gpt.batch(c, 8)
     my_ids, my_tgt = ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV)
 
-    single = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV))
+    single = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV),
+                  comm_streams=comm_streams)
     _, loss = single(my_ids, my_tgt)
     loss.backward()
     expected = [p.grad.clone() for p in single.parameters()]
 
-    accum = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV))
+    accum = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV),
+                 comm_streams=comm_streams)
     with accum.no_sync():
         for h_ids, h_tgt in zip(my_ids.chunk(2), my_tgt.chunk(2), strict=True):
             _, l = accum(h_ids, h_tgt)
@@ -186,7 +193,7 @@ def test_second_backward_accumulates_into_shard_grad():
         assert rel <= 1e-6
 
 
-def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1):
+def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1, comm_streams=False):
     """FSDP on rank ``rank`` of a ResidentGroup next to a full-batch reference, both SGD.
 
     Every step the emulated peers get what they would hold: their shard of the
@@ -198,7 +205,8 @@ def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1):
     model = tiny_gpt.GPT(c).to(DEV)
     names_by_id = {id(p): n for n, p in model.named_parameters()}
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
-    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
+                comm_streams=comm_streams)
     opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
     opt_ref = torch.optim.SGD(ref.parameters(), lr=lr)
     out = []
@@ -237,11 +245,12 @@ def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1):
     return fsdp, ref, names_by_id, out
 
 
-@pytest.mark.parametrize("W,rank", [(2, 1), (4, 2)])
-def test_sgd_steps_track_full_batch(W, rank):
+@pytest.mark.parametrize("W,rank,comm_streams", [(2, 1, False), (4, 2, False), (4, 2, True)])
+def test_sgd_steps_track_full_batch(W, rank, comm_streams):
     """Reference tests/test_fsdp.py:92-127: after 4 SGD steps this rank's shard equals its slice of
-    the full-batch model's weights (the reference compares with DDP; both equal the full batch)."""
-    fsdp, ref, names_by_id, _ = _sgd_run(W, rank, torch.float32)
+    the full-batch model's weights (the reference compares with DDP; both equal the full batch).
+    With ``comm_streams`` the optimizer must see the side streams' shard gradients."""
+    fsdp, ref, names_by_id, _ = _sgd_run(W, rank, torch.float32, comm_streams=comm_streams)
     final = {n: p.detach() for n, p in ref.named_parameters()}
     for unit in fsdp._units:
         flat = torch.cat([final[names_by_id[id(p)]].reshape(-1) for p in unit.params])
