@@ -14,17 +14,17 @@ buckets in reverse parameter order, loss scale 2^16.  One step is
     DistributedGradScaler.unscale_(opt) -> the found-inf flag read (the path's one host sync)
     DistributedGradScaler.update()
 
-value = the metric's algorithmic bytes of the staged pipeline, 52*N (pack 8N,
-W-way 36N, unpack 8N for fp32, W = 8), divided by the measured step time.  The
-implementation moves 44*N (the rank's own contribution is summed from
-registers instead of re-read from its row, and the reduced bucket is not read
-back); config.hbm_gbs reports that actual traffic over the same time.  The
-roofline object is for the dominant (and only) kernel: (2 + W + 1)*N*4 bytes
-per dispatch (gradients read, W-1 peer rows read, the packed row, the bucket
-and the gradients written) over its average HIP-event time, recorded on its
-own stream around every dispatch of the timed region.  The CPU baseline
-(reference op chain on torch CPU + gloo, W processes) runs first, before
-anything touches the GPU.
+value = the bytes the step's dispatch actually reads and writes, 44*N for fp32
+at W = 8 (gradients read, W-1 peer rows read, this rank's packed row, the
+bucket and the gradients written), divided by the median step time -- the
+traffic the rocprofv3 FETCH_SIZE / WRITE_SIZE counters measure.  The
+configuration's staged accounting, 52*N (pack 8N, W-way 36N, unpack 8N: the
+pipeline as three passes, which the fused kernel does not need), is reported
+beside it as config.alg_gbs.  The roofline object is for the dominant (and
+only) kernel: the same 44*N bytes per dispatch over its average HIP-event
+time, recorded on its own stream around every dispatch of the timed region.
+The CPU baseline (reference op chain on torch CPU + gloo, W processes) runs
+first, before anything touches the GPU.
 
 The other benchmark configurations are parity cases; ``--workload`` measures
 them too (one JSON line each, same fields; the CPU baseline for cfg0 and cfg2,
@@ -62,15 +62,26 @@ CAP_MB = 25.0
 LOSS_SCALE = 2.0**16
 
 
-# The reference's CPU path is timed beside the DDP workloads it can hold in host memory.
-CPU_BASELINE = {"cfg0": ("tiny", 4), "cfg1": ("gpt2-small", W_CFG1), "cfg2": ("gpt2-medium", 4)}
+# The reference's CPU path (oracle/gloo_path.py) for each workload: the configuration, W, and
+# the runner's arguments that bound it to about 10-30 s of CPU work.  cfg3 times 2 of its 48
+# FSDP units per step and cfg4 (~324 GB of host memory at W = 8) its first decoder layer and
+# final norm; both are scaled to the whole step and say so.
+CPU_BASELINE = {
+    "cfg0": ("tiny", 4, []),
+    "cfg1": ("gpt2-small", W_CFG1, []),
+    "cfg2": ("gpt2-medium", 4, []),
+    "cfg3": (None, 8, ["--fsdp", "--units", "2"]),
+    "cfg4": ("llama-7b", 8, ["--layers", "1", "--layers-only", "--scale", str(2.0**12)]),
+}
 
 
 def cpu_baseline(workload: str, steps: int, threads: int) -> dict | None:
     """Time the reference's CPU path (oracle/gloo_path.py) in a child process."""
-    config, world = CPU_BASELINE[workload]
-    cmd = [sys.executable, "-m", "oracle.gloo_path", "--config", config, "--world", str(world), "--steps",
-           str(steps), "--warmup", "1", "--threads", str(threads)]
+    config, world, extra = CPU_BASELINE[workload]
+    cmd = [sys.executable, "-m", "oracle.gloo_path", "--world", str(world), "--steps", str(steps), "--warmup", "1",
+           "--threads", str(threads), *extra]
+    if config is not None:
+        cmd += ["--config", config]
     res = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
     if res.returncode != 0:
         print(res.stderr[-2000:], file=sys.stderr, flush=True)
@@ -79,11 +90,60 @@ def cpu_baseline(workload: str, steps: int, threads: int) -> dict | None:
     return json.loads(line)
 
 
-def host_cores() -> int:
+def affinity_cpus() -> int:
     try:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+def cgroup_cpus() -> float | None:
+    """CPUs the cgroup's CPU quota grants (cgroup v2 ``cpu.max``), or None without a quota."""
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+    except (OSError, ValueError):
+        return None
+    return None if quota == "max" else int(quota) / int(period)
+
+
+def granted_cpus() -> int | None:
+    """The CPU share the environment grants this job (``OMP_NUM_THREADS``; 16 per GPU on the
+    GPU boxes, whatever the machine's own CPU count), or None when unset."""
+    try:
+        return int(os.environ["OMP_NUM_THREADS"])
+    except (KeyError, ValueError):
+        return None
+
+
+def host_cores() -> int:
+    """Cores the CPU baseline may keep busy: the affinity set, capped by the cgroup quota and
+    by the granted share."""
+    cores = affinity_cpus()
+    for cap in (cgroup_cpus(), granted_cpus()):
+        if cap is not None:
+            cores = min(cores, int(cap))
+    return max(1, cores)
+
+
+def host_description() -> dict:
+    """The host the CPU baseline ran on: logical CPUs, the affinity set, the CPU model."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:  # pragma: no cover
+        pass
+    if model is None:
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), None)
+        except (OSError, subprocess.SubprocessError):  # pragma: no cover
+            pass
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity_cpus(), "cgroup_quota_cpus": cgroup_cpus(),
+            "granted_cpus_OMP_NUM_THREADS": granted_cpus(),
+            "cores_used": host_cores(), "model": model}
 
 
 def calibrate_copy() -> int:
@@ -177,8 +237,13 @@ def bench_ddp(name: str, args) -> dict:
     model = wl.SpecModule(specs, dev)
     scaler = DistributedGradScaler(init_scale=loss_scale)
     group = ResidentGroup(W, 0, dev)
-    ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler, reduce_dtype=reduce_dtype,
-              capture_graphs=args.graphs)
+    # --dropin: DDP built exactly as the reference's callers build it (no grad_scaler=, no
+    # reduce_dtype=), so the scaler's unscale_ makes its own pass over every gradient.
+    fused_unscale = not args.dropin
+    if args.dropin and reduce_dtype is not None:
+        raise SystemExit("--dropin covers the same-dtype workloads (cfg0, cfg1, cfg2)")
+    ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler if fused_unscale else None,
+              reduce_dtype=reduce_dtype, capture_graphs=args.graphs)
     # --two-dispatch: pack, then the fused all-reduce + unpack (the pipeline before the pack was fused in)
     ddp._fuse_pack = not (args.two_dispatch or args.staged)
     fused_pack = ddp._fuse_pack
@@ -186,14 +251,25 @@ def bench_ddp(name: str, args) -> dict:
     gen = torch.Generator(device=dev).manual_seed(1234)
     scale = cfg["grad_scale"] * loss_scale
     for p in model.parameters():
-        p.grad = (torch.randn(p.shape, device=dev, generator=gen) * scale).to(p.dtype)
-    for b in range(len(ddp._buckets)):
+        g = (torch.randn(p.shape, device=dev, generator=gen) * scale).to(p.dtype)
+        if args.misaligned:
+            # the gradient is a view one element into its own allocation: its address is 4 bytes
+            # (fp32) or 2 bytes (16-bit) past the 16-byte alignment the bucket rows have
+            holder = torch.empty(p.numel() + 1, dtype=p.dtype, device=dev)
+            holder[1:].copy_(g.reshape(-1))
+            g = holder[1:].view(p.shape)
+        p.grad = g
+    n_buckets = len(ddp._buckets)
+    for b in range(n_buckets):
         rows = ddp.bucket_replicas(b)
         wire_dtype, prescaled = ddp.bucket_wire_format(b)
         for r in range(1, W):
             x = torch.randn(rows[r].shape, device=dev, generator=gen) * (scale / W if prescaled else scale)
             rows[r].copy_(x.to(wire_dtype))
             del x
+        if (b + 1) % 32 == 0 or b + 1 == n_buckets:  # staging cfg4's 108 GB takes a while under a profiler
+            print(f"[bench] staged the peers' contributions of {b + 1}/{n_buckets} buckets", file=sys.stderr,
+                  flush=True)
 
     class _Opt:  # the scaler only reads param_groups
         param_groups = [{"params": list(model.parameters())}]
@@ -275,14 +351,19 @@ def bench_ddp(name: str, args) -> dict:
         step()
     torch.cuda.synchronize()
     # Timed region, with HIP events around every fused reduction dispatch on its
-    # own stream (two event records per step cost ~0.8% of a cfg1 step).
+    # own stream (two event records per step cost ~0.8% of a cfg1 step).  Every
+    # step ends in the scaler's flag read (a host synchronisation), so the host
+    # clock between step ends is each step's own time.
     timing["on"] = not args.graphs
     t0 = time.perf_counter()
     found_any = False
+    ends = []
     for _ in range(steps):
         found_any |= step()
+        ends.append(time.perf_counter())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    step_ms = sorted((b - a) * 1e3 for a, b in zip([t0] + ends[:-1], ends))
     if args.graphs:
         ddp._capture_graphs = False
         timing["on"] = True
@@ -296,7 +377,8 @@ def bench_ddp(name: str, args) -> dict:
     s_w = b0.wire.element_size()
     s_b = b0.buffer.element_size()
     s_g = b0.params[0].element_size()
-    ms_per_step = elapsed / steps * 1e3
+    ms_per_step = step_ms[len(step_ms) // 2]  # median of the timed steps
+    mean_ms = elapsed / steps * 1e3
     # Fused pack: the gradient read, W-1 peer rows read, this rank's packed row, the bucket and
     # the gradient written -- one dispatch.  Two-dispatch pipeline: the pack (gradient read, row
     # written), then W rows read, bucket and gradient written.
@@ -310,7 +392,12 @@ def bench_ddp(name: str, args) -> dict:
         alg_bytes = N * (2 * s_g + (W + 3) * s_b)  # pack + W-way + unpack, staged
         hbm_bytes = red_bytes if fused_pack else N * (s_g + s_b) + red_bytes
         alg_note = f"staged pack + W-way + unpack: N*(2*s_g + (W+3)*s_b) = {2 * s_g + (W + 3) * s_b}*N"
-    value = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    if not fused_unscale:
+        hbm_bytes += N * 2 * s_g  # unscale_'s own pass: every gradient read and written again
+    # The headline is the bytes the step's kernels actually move (what the PMC
+    # counters read); the configuration's staged accounting is reported beside it.
+    value = hbm_bytes / (ms_per_step * 1e-3) / 1e9
+    alg_gbs = alg_bytes / (ms_per_step * 1e-3) / 1e9
     red_ms = sorted(e0.elapsed_time(e1) for e0, e1 in red_events)
     red_avg_ms = sum(red_ms) / len(red_ms)
     t16 = KERNEL_TYPE_NAMES[cfg["dtype"]]
@@ -329,7 +416,10 @@ def bench_ddp(name: str, args) -> dict:
     traffic = None if args.staged else measured_traffic(name, fused_pack)
 
     return {
-        "metric": METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step",
+        "metric": (METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step")
+                  + "".join(f" [{tag}]" for tag, on in (("staged", args.staged), ("two-dispatch", args.two_dispatch),
+                                                        ("graphs", args.graphs), ("dropin", args.dropin),
+                                                        ("misaligned", args.misaligned)) if on),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -347,16 +437,26 @@ def bench_ddp(name: str, args) -> dict:
             "world": W,
             "numel": N,
             "buckets": len(ddp._buckets),
+            "value_bytes": "hbm_bytes_per_step: the bytes the step's dispatches read and write (PMC-backed)",
+            "hbm_bytes_per_step": hbm_bytes,
+            "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
             "alg_bytes_per_step": alg_bytes,
             "alg_bytes_formula": alg_note,
-            "hbm_bytes_per_step": hbm_bytes,
-            "hbm_gbs": round(hbm_bytes / (ms_per_step * 1e-3) / 1e9, 2),
-            "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "alg_gbs": round(alg_gbs, 2),
+            "alg_frac_of_peak": round(alg_gbs / HBM_PEAK_GBS, 4),
+            "ms_per_step_stat": f"median of {steps} timed steps",
+            "ms_per_step_mean": round(mean_ms, 4),
+            "ms_per_step_min": round(step_ms[0], 4),
             # a full 25 MiB bucket's share of the measured step (one bucket alone would sit in the
             # 256 MB Infinity Cache, so it is not timed on its own)
             "us_per_25MiB_bucket": round(ms_per_step * 1e3 * (25 * 2**20 // b0.buffer.element_size()) / N, 2),
             "found_inf": bool(found_any),
             "launch": "hip graph replay (capture_graphs=True)" if args.graphs else "eager dispatches",
+            "api": "drop-in: DDP(module, process_group, bucket_cap_mb) then scaler.unscale_(opt) as its own pass "
+                   "(the reference's call sequence)" if args.dropin
+                   else "DDP(..., grad_scaler=scaler): unscale + found-inf fused into the unpack",
+            "gradients": "views one element into their allocations (no common 16-byte alignment with the rows)"
+                         if args.misaligned else "tensors of their own (16-byte aligned)",
             "pipeline": "staged: pack, W-way sum, unpack (three dispatches)" if args.staged
                         else "pack + fused W-way sum / unpack / unscale (two dispatches)" if not fused_pack
                         else "pack fused into the W-way sum / unpack / unscale (one dispatch)",
@@ -392,7 +492,12 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     around them, so the step's dispatches are enqueued behind a spin kernel and
     the step is timed on the GPU (first to last dispatch, HIP events): the
     number is the dispatch sequence's own throughput, as when FSDP's launches
-    overlap forward/backward compute."""
+    overlap forward/backward compute.  By default the wrapper runs with
+    ``comm_streams=True``: every gather cast goes to its gather stream and
+    every reduce-scatter share to its reduce stream, so a cast overlaps the
+    shares around it (``--serial``: everything on one stream).  The per-kernel
+    times of the roofline come from a separate pass with the dispatches on one
+    stream and HIP events around each."""
     import torch
     from torch import nn
 
@@ -422,7 +527,9 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     name = "cfg3" if param_dtype_name == "bf16" else f"cfg3-{param_dtype_name}"
     pdt = getattr(torch, TORCH_DTYPE_NAMES[param_dtype_name])
     policy = MixedPrecisionPolicy(param_dtype=pdt, reduce_dtype=torch.float32)
-    fsdp = FSDP(model, unit_types=(Block,), process_group=ResidentGroup(W, 0, dev), mixed_precision=policy)
+    streams = not args.serial
+    fsdp = FSDP(model, unit_types=(Block,), process_group=ResidentGroup(W, 0, dev), mixed_precision=policy,
+                comm_streams=streams)
     units = fsdp._units
     assert len(units) == n_units
     own_grads = []
@@ -448,6 +555,12 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
             u.reduce_scatter_grads()
             if events is not None:
                 events[i][2].record()
+        fsdp.finish_gradient_sync()  # with side streams: the caller's stream joins both
+
+    def one_stream(on: bool) -> None:
+        """Route the units' work to the caller's stream (the per-kernel event pass) or back."""
+        for u in units:
+            u.streams = None if on else fsdp._streams
 
     for _ in range(args.warmup):
         step()
@@ -471,8 +584,9 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
         e1.record()
         torch.cuda.synchronize()
         per_step.append(e0.elapsed_time(e1))
-    # Kernel pass: the same steps with events around every dispatch.
+    # Kernel pass: the same steps on one stream with events around every dispatch.
     cast_ms, share_ms = [], []
+    one_stream(True)
     for _ in range(min(steps, 5)):
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in units]
         torch.cuda._sleep(hold_cycles)
@@ -480,6 +594,7 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
         torch.cuda.synchronize()
         cast_ms += [e[0].elapsed_time(e[1]) for e in ev]
         share_ms += [e[1].elapsed_time(e[2]) for e in ev]
+    one_stream(False)
     ms_per_step = sorted(per_step)[len(per_step) // 2]
     alg_bytes = n_units * 26 * S  # cast 6S (fp32 read, bf16 write) + share 20S (8 bf16 reads, fp32 write)
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
@@ -505,6 +620,9 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                         f"S=3,842,600), W=8, param {param_dtype_name} / reduce fp32; per unit the gather cast ("
                         + ("mdx_cast_f32_bf16" if param_dtype_name == "bf16" else "mdx_pack, fp32 -> fp16")
                         + ") + mdx_reduce_scatter_share; GPU time of the step's dispatches",
+            "streams": "comm_streams=True: casts on the gather stream, shares on the reduce stream" if streams
+                       else "one stream (--serial)",
+            "ms_per_step_stat": f"median of {steps} steps",
             "world": W,
             "units": n_units,
             "shard_numel": S,
@@ -699,6 +817,13 @@ def main() -> int:
                          "before the pack was fused into the reduction), for comparison")
     ap.add_argument("--graphs", action="store_true",
                     help="DDP workloads: replay each step's launches from a captured HIP graph (capture_graphs=True)")
+    ap.add_argument("--dropin", action="store_true",
+                    help="DDP workloads: the reference's call sequence unchanged (no grad_scaler=): the scaler's "
+                         "unscale_ runs its own pass over the gradients")
+    ap.add_argument("--misaligned", action="store_true",
+                    help="DDP workloads: every gradient a view one element into its allocation")
+    ap.add_argument("--serial", action="store_true",
+                    help="cfg3: run every unit's cast and share on one stream (default: FSDP comm_streams=True)")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument(
         "--calibrate-copy", action="store_true",
@@ -720,10 +845,10 @@ def main() -> int:
     cpu = None
     if args.workload in CPU_BASELINE and not args.no_cpu_baseline:
         world = CPU_BASELINE[args.workload][1]
-        cores = max(world, min(16, host_cores()))
-        threads = max(1, cores // world)
+        threads = max(1, host_cores() // world)  # every core this process may run on, split over the ranks
         # about 10 s of CPU work: a GPT-2-medium step takes ~3x a GPT-2-124M one, the tiny GPT ~1%
-        steps = {"cfg0": args.cpu_steps * 10, "cfg1": args.cpu_steps, "cfg2": max(3, args.cpu_steps // 3)}
+        steps = {"cfg0": args.cpu_steps * 10, "cfg1": args.cpu_steps, "cfg2": max(3, args.cpu_steps // 3),
+                 "cfg3": 3, "cfg4": 2}
         t0 = time.perf_counter()
         cpu = cpu_baseline(args.workload, steps[args.workload], threads)
         print(f"[bench] cpu baseline done in {time.perf_counter() - t0:.1f}s: {cpu}", file=sys.stderr, flush=True)
@@ -735,18 +860,21 @@ def main() -> int:
     else:
         out = bench_ddp(args.workload, args)
     if cpu is not None:
-        alg_bytes = out["config"]["alg_bytes_per_step"]
-        cpu_gbs = alg_bytes / (cpu["median_ms"] * 1e-3) / 1e9
+        # the same byte count as `value`, over the CPU step time: value / cpu value = the speedup
+        nbytes = out["config"].get("hbm_bytes_per_step", out["config"]["alg_bytes_per_step"])
+        cpu_gbs = nbytes / (cpu["median_ms"] * 1e-3) / 1e9
         out["cpu_baseline"] = {
             "value": round(cpu_gbs, 3),
             "unit": "GB/s",
             "cores": cpu["cores"],
             "kind": "port",
-            "sample": f"{cpu['steps']} timed steps (+1 warmup) of the full {args.workload} pipeline, reference op "
-                      f"chain on torch CPU + gloo, {cpu['world']} processes x {cpu['threads_per_rank']} threads; "
-                      f"median {cpu['median_ms']:.1f} ms/step",
+            "sample": f"{cpu['steps']} timed steps (+1 warmup) of the {args.workload} pipeline, reference op "
+                      f"chain on torch CPU + gloo, {cpu['world']} processes x {cpu['threads_per_rank']} threads, "
+                      f"each step from the same pristine gradients; median {cpu['median_ms']:.1f} ms/step"
+                      + (f"; {cpu['note']}" if cpu.get("note") else ""),
             "ms_per_step": round(cpu["median_ms"], 2),
             "speedup": round(cpu["median_ms"] / out["ms_per_step"], 1),
+            "host": host_description(),
         }
     print(json.dumps(out), flush=True)
     return 0

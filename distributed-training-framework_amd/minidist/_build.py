@@ -105,15 +105,29 @@ def build_host_helper() -> Path:
     return out
 
 
-def build_native(jobs: int | None = None) -> Path:
-    """Compile every translation unit for gfx950 and link ``libmdx.so``."""
+def _stale(src: Path, obj: Path) -> bool:
+    """True when ``obj`` is missing or older than its source or any shared header."""
+    if not obj.exists():
+        return True
+    deps = [src, *(CSRC / h for h in HEADERS), INCLUDE / "mdx.h"]
+    return obj.stat().st_mtime < max(d.stat().st_mtime for d in deps)
+
+
+def build_native(jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every translation unit for gfx950 and link ``libmdx.so``.
+
+    ``incremental`` recompiles only the objects older than their source or a
+    shared header (and skips the host helper when it exists); the default
+    rebuilds everything."""
     BUILD_DIR.mkdir(exist_ok=True)
     objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
+    todo = [(s, o) for s, o in zip(SOURCES, objs) if not incremental or _stale(CSRC / s, o)]
+    jobs = jobs or max(1, min(len(todo), os.cpu_count() or 1))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        helper = pool.submit(build_host_helper)
-        list(pool.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
-        helper.result()
+        helper = None if incremental and host_helper_path().exists() else pool.submit(build_host_helper)
+        list(pool.map(lambda so: _compile(CSRC / so[0], so[1]), todo))
+        if helper is not None:
+            helper.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -124,4 +138,4 @@ def build_native(jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    print(build_native())
+    print(build_native(incremental="--incremental" in sys.argv[1:]))
