@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "mdx_internal.h"
 
@@ -500,6 +501,93 @@ int for_each_pack_run(const mdx_pack_run* runs, int n_runs, const FusedArgs& f, 
   return MDX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free plan launch (mdx_pack_allreduce_unpack_planned_noalloc)
+// ---------------------------------------------------------------------------
+
+// The device copy of a plan launched without caller-allocated memory.  Each
+// GPU the library runs on holds its own instance until the process ends.  In
+// host code the name `scratch` is only a stand-in for the symbol: kernels and
+// copies get the address hipGetSymbolAddress returns on the device
+// (scratch_on), never the name.
+__device__ __align__(256) unsigned char scratch[MDX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices];
+hipError_t g_scratch_status[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+
+// This device's address of `scratch`, resolved once per device while that
+// device is current (the caller checked that it is).
+hipError_t scratch_on(int device, unsigned char** out) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[device], [device]() {
+    void* p = nullptr;
+    g_scratch_status[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch[device] = p;
+  });
+  *out = static_cast<unsigned char*>(g_scratch[device]);
+  return g_scratch_status[device];
+}
+
+// Plan bytes per upload dispatch.  The chunk is a kernel argument: the
+// runtime copies it when the dispatch is enqueued, so the caller's host plan
+// is free to change once the call returns, and nothing waits for the stream.
+constexpr int kUploadWords = 768;  // 3 KB
+
+struct UploadChunk {
+  uint32_t word[kUploadWords];
+  int64_t offset;  // byte offset of word[0] in the buffer (a multiple of 4)
+  int32_t count;   // words of this chunk, at most kUploadWords
+};
+
+__global__ void __launch_bounds__(kBlock) upload_kernel(UploadChunk c, unsigned char* dst) {
+  uint32_t* out = reinterpret_cast<uint32_t*>(dst + c.offset);
+  for (int i = int(threadIdx.x); i < c.count; i += kBlock) out[i] = c.word[i];
+}
+
+// Copies plan bytes [0, bytes) into `dst` with upload dispatches on `stream`.
+int upload_plan(const void* plan, int64_t bytes, unsigned char* dst, hipStream_t stream) {
+  const unsigned char* src = static_cast<const unsigned char*>(plan);
+  UploadChunk c;
+  for (int64_t off = 0; off < bytes; off += int64_t(kUploadWords) * 4) {
+    const int64_t n = std::min<int64_t>(int64_t(kUploadWords) * 4, bytes - off);
+    c.offset = off;
+    c.count = int32_t(n / 4);
+    memcpy(c.word, src + off, size_t(n));
+    hipLaunchKernelGGL(upload_kernel, dim3(1), dim3(kBlock), 0, stream, c, dst);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return int(e);
+  }
+  return MDX_OK;
+}
+
+// A plan's table offsets are the ones its own counts give (plan_layout), so
+// every array the kernel reads lies inside its `bytes`.
+bool plan_layout_matches(const PlanHeader* h) {
+  if (h->count < 0 || h->blocks < 0) return false;
+  PlanHeader ref = *h;
+  plan_layout(&ref, h->count, h->blocks);
+  return ref.bytes == h->bytes && ref.off_first_block == h->off_first_block && ref.off_head == h->off_head &&
+         ref.off_numel == h->off_numel && ref.off_a == h->off_a && ref.off_b == h->off_b &&
+         ref.off_pos == h->off_pos && ref.off_hint == h->off_hint;
+}
+
+// The device `stream` runs on, which must be the current one.
+int stream_device(hipStream_t stream, int* device) {
+  int current = -1;
+  hipError_t e = hipGetDevice(&current);
+  if (e != hipSuccess) return int(e);
+  int owner = current;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, &owner);
+    if (e != hipSuccess) return int(e);
+  }
+  if (owner != current) return MDX_ESCRATCH;
+  *device = current;
+  return MDX_OK;
+}
+
 }  // namespace
 }  // namespace mdx
 
@@ -517,6 +605,8 @@ const char* mdx_strerror(int code) {
     case MDX_EWORLD: return "mdx: world size outside [1, MDX_MAX_WORLD] or rank outside [0, world)";
     case MDX_EALIAS: return "mdx: output overlaps an input it must not overlap";
     case MDX_ESIZE: return "mdx: plan buffer missing or too small (required size returned)";
+    case MDX_ESCRATCH:
+      return "mdx: plan larger than MDX_NOALLOC_SCRATCH_BYTES (256 KiB), or stream not on the current device";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -881,6 +971,26 @@ int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv
     return status(launch_allreduce_wide_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p, st));
   }
   return status(launch_allreduce_dev(h->dtype_a, h->dtype_b, h->world, t, h->blocks, p, st));
+}
+
+int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float inv_scale, int32_t* found_inf,
+                                              int32_t* clear_flag, void* stream) {
+  if (plan == nullptr) return MDX_EINVAL;
+  const PlanHeader* h = static_cast<const PlanHeader*>(plan);
+  if (h->magic != kPlanMagic || h->kind != kPlanPackRuns || !plan_layout_matches(h)) return MDX_EINVAL;
+  if (clear_flag != nullptr && clear_flag == found_inf) return MDX_EALIAS;
+  if (h->bytes > MDX_NOALLOC_SCRATCH_BYTES) return MDX_ESCRATCH;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (h->count == 0) return clear_flag != nullptr ? status(launch_clear_flag(clear_flag, st)) : MDX_OK;
+  int device = -1;
+  int rc = stream_device(st, &device);
+  if (rc != MDX_OK) return rc;
+  unsigned char* d_plan = nullptr;
+  rc = status(scratch_on(device, &d_plan));
+  if (rc != MDX_OK) return rc;
+  rc = upload_plan(plan, h->bytes, d_plan, st);
+  if (rc != MDX_OK) return rc;
+  return mdx_pack_allreduce_unpack_planned(plan, d_plan, inv_scale, found_inf, clear_flag, stream);
 }
 
 }  // extern "C"

@@ -25,7 +25,7 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_pack_planned": (_i32, [_vp, _vp, _f32, _i32, _vp, _vp]),
     "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
+    "mdx_pack_allreduce_unpack_planned_noalloc": (_i32, [_vp, _f32, _vp, _vp, _vp]),
     "mdx_strerror": (ctypes.c_char_p, [_i32]),
     "mdx_abi_version": (_i32, []),
 }
@@ -262,7 +263,10 @@ def reduce_scatter_share(
     check(rc, "mdx_reduce_scatter_share")
 
 
+MDX_EALIAS = -4
 MDX_ESIZE = -5
+MDX_ESCRATCH = -6
+NOALLOC_SCRATCH_BYTES = 256 * 1024
 
 
 class Plan:
@@ -349,6 +353,15 @@ def pack_allreduce_unpack_planned(
     rc = lib().mdx_pack_allreduce_unpack_planned(plan.host_ptr, plan.device_ptr, inv_scale, found_inf, clear_flag,
                                                  stream)
     check(rc, "mdx_pack_allreduce_unpack_planned")
+
+
+def pack_allreduce_unpack_planned_noalloc(
+    plan: Plan, inv_scale: float, found_inf: int | None, clear_flag: int | None, stream: int
+) -> None:
+    """The same launch as :func:`pack_allreduce_unpack_planned` from the plan's host bytes only:
+    the library uploads them into its own per-GPU buffer (no device memory is allocated)."""
+    rc = lib().mdx_pack_allreduce_unpack_planned_noalloc(plan.host_ptr, inv_scale, found_inf, clear_flag, stream)
+    check(rc, "mdx_pack_allreduce_unpack_planned_noalloc")
 
 
 def pack_planned(plan: Plan, scale: float, divide: bool, stream: int, clear_flag: int | None = None) -> None:

@@ -28,7 +28,9 @@
  *     caller zeroes; a kernel stores 1 into it if it produced any inf or NaN,
  *     and never stores 0.
  *   - No global mutable state: calls are thread-safe; calls that write the
- *     same memory must be ordered by the caller (same stream or events).
+ *     same memory must be ordered by the caller (same stream or events).  The
+ *     one exception is mdx_pack_allreduce_unpack_planned_noalloc, whose
+ *     per-GPU buffer every call on that GPU shares (see there).
  */
 #ifndef MDX_H_
 #define MDX_H_
@@ -39,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 5
+#define MDX_ABI_VERSION 6
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -62,6 +64,9 @@ enum {
   MDX_EWORLD = -3,    /* world outside [1, MDX_MAX_WORLD] or rank >= world */
   MDX_EALIAS = -4,    /* an output overlaps an input it must not overlap  */
   MDX_ESIZE = -5,     /* plan buffer missing or too small                 */
+  MDX_ESCRATCH = -6,  /* plan larger than MDX_NOALLOC_SCRATCH_BYTES, or the
+                         stream is not on the current device (allocation-free
+                         entry point only)                                  */
 };
 
 #define MDX_MAX_WORLD 16
@@ -309,6 +314,30 @@ MDX_API int mdx_unpack_planned(const void* plan, const void* d_plan, float inv_s
 /* mdx_allreduce_unpack (or _wide, by the plan) over a plan: one dispatch. */
 MDX_API int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale,
                                          int32_t* found_inf, void* stream);
+
+/* mdx_pack_allreduce_unpack_planned without a caller-allocated device copy
+ * of the plan: the library uploads `plan` (host bytes from
+ * mdx_plan_pack_allreduce_unpack) into a device buffer of its own and launches
+ * the same kernel on it, with the same results.
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc); it calls no hipMalloc, hipFree or
+ * other allocating routine.
+ *   - The buffer is a fixed array of MDX_NOALLOC_SCRATCH_BYTES per GPU, held
+ *     until the process ends; a plan whose size (`*plan_bytes` returned by the
+ *     plan builder) exceeds it is rejected with MDX_ESCRATCH before anything
+ *     is launched.  `stream` must belong to the current device (else
+ *     MDX_ESCRATCH).
+ *   - The plan travels in the kernel arguments of small upload dispatches
+ *     (3 KB each) enqueued on `stream` ahead of the kernel, so `plan` may be
+ *     reused or freed as soon as the call returns.
+ *   - Every call on one GPU shares that GPU's buffer: calls on one stream are
+ *     ordered, but calls that overlap in time on one GPU (different streams
+ *     without events between them, or several threads) race and must not be
+ *     made. */
+#define MDX_NOALLOC_SCRATCH_BYTES (256 * 1024)
+MDX_API int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float inv_scale, int32_t* found_inf,
+                                                      int32_t* clear_flag, void* stream);
 
 /* Static description of a status code. */
 MDX_API const char* mdx_strerror(int code);
