@@ -492,12 +492,23 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     around them, so the step's dispatches are enqueued behind a spin kernel and
     the step is timed on the GPU (first to last dispatch, HIP events): the
     number is the dispatch sequence's own throughput, as when FSDP's launches
-    overlap forward/backward compute.  By default the wrapper runs with
-    ``comm_streams=True``: every gather cast goes to its gather stream and
-    every reduce-scatter share to its reduce stream, so a cast overlaps the
-    shares around it (``--serial``: everything on one stream).  The per-kernel
-    times of the roofline come from a separate pass with the dispatches on one
-    stream and HIP events around each."""
+    overlap forward/backward compute.
+
+    ``--fsdp-mode`` picks how the 48 units' work is issued:
+
+    * ``batched`` (default): as FSDP issues it for units that are ready
+      together -- the gather casts of all units in one dispatch (the batched
+      unshard of ``summon_full_params``, without the peers' gather copies,
+      which are the all-gather's own traffic) and the reduce-scatter shares
+      of all units in one multi-unit dispatch (``finish_gradient_sync``
+      flushing units whose gradients are ready);
+    * ``per-unit``: per unit its cast and its share, as the forward and
+      backward hooks issue them, on the caller's stream;
+    * ``per-unit-streams``: the same with ``comm_streams=True`` (casts on the
+      gather stream, shares on the reduce stream).
+
+    The per-kernel times of the roofline come from a separate pass with the
+    step's dispatches on one stream and HIP events around each."""
     import torch
     from torch import nn
 
@@ -527,9 +538,12 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     name = "cfg3" if param_dtype_name == "bf16" else f"cfg3-{param_dtype_name}"
     pdt = getattr(torch, TORCH_DTYPE_NAMES[param_dtype_name])
     policy = MixedPrecisionPolicy(param_dtype=pdt, reduce_dtype=torch.float32)
-    streams = not args.serial
+    mode = args.fsdp_mode
+    streams = mode == "per-unit-streams"
+    # reshard_after_forward=False: the gather buffers stay allocated (the step re-casts into them),
+    # and finish_gradient_sync's flush does not free them
     fsdp = FSDP(model, unit_types=(Block,), process_group=ResidentGroup(W, 0, dev), mixed_precision=policy,
-                comm_streams=streams)
+                reshard_after_forward=False, comm_streams=streams)
     units = fsdp._units
     assert len(units) == n_units
     own_grads = []
@@ -543,6 +557,20 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     S = units[0].shard_numel
 
     def step(events=None):
+        if mode == "batched":
+            if events is not None:
+                events[0][0].record()
+            fsdp._cast_own_slots(units)
+            if events is not None:
+                events[0][1].record()
+            for i, u in enumerate(units):
+                u.flat_shard.grad = None  # the shard gradient is set, not accumulated
+                for p, g in zip(u.params, own_grads[i], strict=True):
+                    p.grad = g
+            fsdp.finish_gradient_sync()  # every unit holds gradients: one multi-unit share
+            if events is not None:
+                events[0][2].record()
+            return
         for i, u in enumerate(units):
             if events is not None:
                 events[i][0].record()
@@ -587,20 +615,22 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     # Kernel pass: the same steps on one stream with events around every dispatch.
     cast_ms, share_ms = [], []
     one_stream(True)
+    n_ev = 1 if mode == "batched" else len(units)
     for _ in range(min(steps, 5)):
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in units]
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
         torch.cuda._sleep(hold_cycles)
         step(ev)
         torch.cuda.synchronize()
         cast_ms += [e[0].elapsed_time(e[1]) for e in ev]
         share_ms += [e[1].elapsed_time(e[2]) for e in ev]
     one_stream(False)
+    per_launch = n_units if mode == "batched" else 1  # units one timed launch covers
     ms_per_step = sorted(per_step)[len(per_step) // 2]
     alg_bytes = n_units * 26 * S  # cast 6S (fp32 read, bf16 write) + share 20S (8 bf16 reads, fp32 write)
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
     share_avg = sum(share_ms) / len(share_ms)
     cast_avg = sum(cast_ms) / len(cast_ms)
-    share_gbs = 20 * S / (share_avg * 1e-3) / 1e9
+    share_gbs = 20 * S * per_launch / (share_avg * 1e-3) / 1e9
     return {
         "metric": f"FSDP unit gather-cast + reduce-scatter share HBM GB/s (% of 8 TB/s) {name}; ms/step",
         "value": round(value, 2),
@@ -617,11 +647,18 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                 "in HBM)",
         "config": {
             "workload": f"{name}: 48 FSDP units of GPT-2-XL blocks (12 tensors, 30,740,800 elements each, shard "
-                        f"S=3,842,600), W=8, param {param_dtype_name} / reduce fp32; per unit the gather cast ("
-                        + ("mdx_cast_f32_bf16" if param_dtype_name == "bf16" else "mdx_pack, fp32 -> fp16")
-                        + ") + mdx_reduce_scatter_share; GPU time of the step's dispatches",
-            "streams": "comm_streams=True: casts on the gather stream, shares on the reduce stream" if streams
-                       else "one stream (--serial)",
+                        f"S=3,842,600), W=8, param {param_dtype_name} / reduce fp32; per unit the gather cast and "
+                        "the reduce-scatter share ("
+                        + ("mdx_pack over the 48 units' master shards + mdx_reduce_scatter_share_multi_planned"
+                           if mode == "batched" else
+                           ("mdx_cast_f32_bf16" if param_dtype_name == "bf16" else "mdx_pack, fp32 -> fp16")
+                           + " + mdx_reduce_scatter_share per unit")
+                        + "); GPU time of the step's dispatches",
+            "issue": {"batched": "all units' casts in one dispatch, all units' shares in one multi-unit dispatch "
+                                 "(finish_gradient_sync's flush)",
+                      "per-unit": "per unit a cast and a share dispatch (the hooks' order), one stream",
+                      "per-unit-streams": "per unit a cast on the gather stream and a share on the reduce stream "
+                                          "(comm_streams=True)"}[mode],
             "ms_per_step_stat": f"median of {steps} steps",
             "world": W,
             "units": n_units,
@@ -629,19 +666,22 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
             "alg_bytes_per_step": alg_bytes,
             "alg_bytes_formula": "per unit 6*S (cast) + 20*S (share: W*S*2 read, S*4 written)",
             "cast_avg_ms": round(cast_avg, 5),
-            "cast_gbs": round(6 * S / (cast_avg * 1e-3) / 1e9, 1),
+            "cast_gbs": round(6 * S * per_launch / (cast_avg * 1e-3) / 1e9, 1),
             "alg_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"share_kernel_few<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
-                      "(mdx_reduce_scatter_share; rank 0's shard is 3 parameter pieces)",
+            "kernel": (f"share_kernel_dev<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
+                       "(mdx_reduce_scatter_share_multi_planned: 48 units' shares, ~150 pieces, one dispatch)")
+                      if mode == "batched" else
+                      (f"share_kernel_few<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
+                       "(mdx_reduce_scatter_share; rank 0's shard is 3 parameter pieces)"),
             "achieved": round(share_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(share_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(name),
-            "bytes_per_launch": 20 * S,
+            "traffic": measured_traffic(name) if mode != "batched" else None,
+            "bytes_per_launch": 20 * S * per_launch,
             "avg_launch_ms": round(share_avg, 5),
         },
         "cpu_baseline": None,
@@ -822,8 +862,8 @@ def main() -> int:
                          "unscale_ runs its own pass over the gradients")
     ap.add_argument("--misaligned", action="store_true",
                     help="DDP workloads: every gradient a view one element into its allocation")
-    ap.add_argument("--serial", action="store_true",
-                    help="cfg3: run every unit's cast and share on one stream (default: FSDP comm_streams=True)")
+    ap.add_argument("--fsdp-mode", default="batched", choices=["batched", "per-unit", "per-unit-streams"],
+                    help="cfg3: how the units' casts and shares are issued (see bench_fsdp)")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument(
         "--calibrate-copy", action="store_true",

@@ -501,6 +501,70 @@ int for_each_pack_run(const mdx_pack_run* runs, int n_runs, const FusedArgs& f, 
   return MDX_OK;
 }
 
+// The pre-scale / accumulate / unscale flags of a reduce-scatter share.
+void share_flags(int world, int divide, int accumulate, float inv_scale, ReduceParams* p) {
+  int32_t flags = 0;
+  p->pre = 1.0f;
+  if (divide && world > 1) {
+    // x / W and x * (1/W) are the same correctly rounded value when 1/W is
+    // exact, i.e. for power-of-two W; the multiply is the cheaper instruction.
+    if (is_pow2(world)) {
+      flags |= kRedPreMul;
+      p->pre = 1.0f / float(world);
+    } else {
+      flags |= kRedPreDiv;
+      p->pre = float(world);
+    }
+  }
+  if (accumulate) flags |= kRedAccumulate;
+  if (inv_scale != 1.0f) flags |= kRedUnscale;
+  p->flags = flags;
+  p->inv_scale = inv_scale;
+}
+
+// Arguments of a multi-unit share, validated: pieces at absolute positions of
+// the contribution rows `peers`, each with a destination of its own.
+int check_share_multi(const mdx_piece* pieces, void* const* outs, int n, const void* const* peers, int world,
+                      int rank, int in_dtype, int reduce_dtype, int shard_dtype, ReduceParams* p, bool* any) {
+  if (!valid_dtype(in_dtype) || !valid_dtype(reduce_dtype) || !valid_dtype(shard_dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD || rank < 0 || rank >= world) return MDX_EWORLD;
+  if (n < 0 || (n > 0 && (pieces == nullptr || outs == nullptr))) return MDX_EINVAL;
+  if (world > 1 && peers == nullptr) return MDX_EINVAL;
+  const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
+  int64_t extent = 0;
+  *any = false;
+  for (int i = 0; i < n; ++i) {
+    if (pieces[i].numel < 0 || pieces[i].pos < 0) return MDX_EINVAL;
+    if (pieces[i].numel == 0) continue;
+    if (outs[i] == nullptr) return MDX_EINVAL;
+    *any = true;
+    extent = std::max<int64_t>(extent, pieces[i].pos + pieces[i].numel);
+  }
+  memset(p, 0, sizeof(*p));
+  p->rank = rank;
+  p->world = world;
+  if (!*any) return MDX_OK;
+  for (int r = 0; r < world; ++r) {
+    if (r == rank) continue;
+    if (peers[r] == nullptr) return MDX_EINVAL;
+    p->peer[r] = peers[r];
+  }
+  // Every destination must be clear of the rows, of every piece's own data and
+  // of every other destination (workgroups of different pieces run unordered).
+  for (int i = 0; i < n; ++i) {
+    const int64_t ob = pieces[i].numel * os;
+    if (ob == 0) continue;
+    for (int r = 0; r < world; ++r) {
+      if (r != rank && any_overlap(peers[r], extent * is, outs[i], ob)) return MDX_EALIAS;
+    }
+    for (int j = 0; j < n; ++j) {
+      if (pieces[j].own && any_overlap(pieces[j].own, pieces[j].numel * is, outs[i], ob)) return MDX_EALIAS;
+      if (j != i && any_overlap(outs[j], pieces[j].numel * os, outs[i], ob)) return MDX_EALIAS;
+    }
+  }
+  return MDX_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Allocation-free plan launch (mdx_pack_allreduce_unpack_planned_noalloc)
 // ---------------------------------------------------------------------------
@@ -811,24 +875,8 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
   p.out = shard;
   p.rank = rank;
   p.world = world;
-  p.inv_scale = inv_scale;
   p.found_inf = found_inf;
-  p.pre = 1.0f;
-  int32_t flags = 0;
-  if (divide && world > 1) {
-    // x / W and x * (1/W) are the same correctly rounded value when 1/W is
-    // exact, i.e. for power-of-two W; the multiply is the cheaper instruction.
-    if (is_pow2(world)) {
-      flags |= kRedPreMul;
-      p.pre = 1.0f / float(world);
-    } else {
-      flags |= kRedPreDiv;
-      p.pre = float(world);
-    }
-  }
-  if (accumulate) flags |= kRedAccumulate;
-  if (inv_scale != 1.0f) flags |= kRedUnscale;
-  p.flags = flags;
+  share_flags(world, divide, accumulate, inv_scale, &p);
   const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
   const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
   const int E = reduce_frag_elems(is, os, os);  // as the kernel's compile-time fragment
@@ -838,6 +886,73 @@ int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void* const*
     return launch_share(in_dtype, reduce_dtype, shard_dtype, wmax, b, p, st);
   };
   return run_pieces(own, nullptr, n_own, p, is, os, 0, E, U, launch);
+}
+
+int mdx_reduce_scatter_share_multi(const mdx_piece* pieces, void* const* outs, int n_pieces,
+                                   const void* const* peers, int world, int rank, int in_dtype, int reduce_dtype,
+                                   int divide, int shard_dtype, int accumulate, float inv_scale, int32_t* found_inf,
+                                   void* stream) {
+  ReduceParams p;
+  bool any = false;
+  const int rc = check_share_multi(pieces, outs, n_pieces, peers, world, rank, in_dtype, reduce_dtype, shard_dtype,
+                                   &p, &any);
+  if (rc != MDX_OK || !any) return rc;
+  p.found_inf = found_inf;
+  share_flags(world, divide, accumulate, inv_scale, &p);
+  const int is = dtype_size(in_dtype), os = dtype_size(shard_dtype);
+  const int wmax = share_wmax(in_dtype, reduce_dtype, shard_dtype, world);
+  const int E = reduce_frag_elems(is, os, os);  // as the kernel's compile-time fragment
+  const int U = share_unroll(wmax, E * is);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](const PieceBatch& b) {
+    return launch_share(in_dtype, reduce_dtype, shard_dtype, wmax, b, p, st);
+  };
+  return run_pieces(pieces, outs, n_pieces, p, is, os, os, E, U, launch);
+}
+
+int mdx_plan_reduce_scatter_share_multi(const mdx_piece* pieces, void* const* outs, int n_pieces,
+                                        const void* const* peers, int world, int rank, int in_dtype, void* plan,
+                                        int64_t* plan_bytes) {
+  if (plan_bytes == nullptr) return MDX_EINVAL;
+  ReduceParams p;
+  bool any = false;
+  const int rc = check_share_multi(pieces, outs, n_pieces, peers, world, rank, in_dtype, MDX_F32, MDX_F32, &p, &any);
+  if (rc != MDX_OK) return rc;
+  PlanHeader proto;
+  memset(&proto, 0, sizeof(proto));
+  proto.kind = kPlanSharePieces;
+  proto.dtype_a = in_dtype;
+  proto.dtype_b = MDX_F32;
+  proto.reduce_dtype = MDX_F32;
+  proto.world = world;
+  proto.rank = rank;
+  for (int r = 0; r < world; ++r) proto.replicas[r] = addr(p.peer[r]);
+  const int is = dtype_size(in_dtype), os = 4;
+  const int wmax = share_wmax(in_dtype, MDX_F32, MDX_F32, world);
+  const int E = reduce_frag_elems(is, os, os);
+  const int U = share_unroll(wmax, E * is);
+  auto gen = [&](auto&& emit) {
+    return any ? for_each_piece_run(pieces, outs, n_pieces, p, is, os, os, E, U, emit) : MDX_OK;
+  };
+  return build_plan(proto, gen, plan, plan_bytes);
+}
+
+int mdx_reduce_scatter_share_multi_planned(const void* plan, const void* d_plan, int divide, int accumulate,
+                                           float inv_scale, int32_t* found_inf, void* stream) {
+  const PlanHeader* h;
+  DevTable t;
+  const int rc = plan_view(plan, d_plan, kPlanSharePieces, &h, &t);
+  if (rc != MDX_OK) return rc;
+  if (h->count == 0) return MDX_OK;
+  ReduceParams p;
+  memset(&p, 0, sizeof(p));
+  for (int r = 0; r < h->world; ++r) p.peer[r] = reinterpret_cast<const void*>(h->replicas[r]);
+  p.world = h->world;
+  p.rank = h->rank;
+  p.found_inf = found_inf;
+  share_flags(h->world, divide, accumulate, inv_scale, &p);
+  const int wmax = share_wmax(h->dtype_a, MDX_F32, MDX_F32, h->world);
+  return status(launch_share_fast_dev(h->dtype_a, wmax, t, h->blocks, p, static_cast<hipStream_t>(stream)));
 }
 
 // -- device plans -------------------------------------------------------------

@@ -557,7 +557,7 @@ struct DevView {
 // byte offsets.  The same bytes live on the host (read at launch for the grid
 // size and kernel arguments) and in device memory (read by the kernel).
 constexpr uint32_t kPlanMagic = 0x5058444du;  // "MDXP"
-enum : int32_t { kPlanSpans = 1, kPlanGradRuns = 2, kPlanPackRuns = 3 };
+enum : int32_t { kPlanSpans = 1, kPlanGradRuns = 2, kPlanPackRuns = 3, kPlanSharePieces = 4 };
 
 struct PlanHeader {
   uint32_t magic;
@@ -592,6 +592,9 @@ hipError_t launch_pack_allreduce(int wire_dtype, int reduce_dtype, int world, co
                                  const ReduceParams& p, hipStream_t stream);
 hipError_t launch_pack_allreduce_dev(int wire_dtype, int reduce_dtype, int world, const DevTable& t, int blocks,
                                      const ReduceParams& p, hipStream_t stream);
+// Multi-unit reduce-scatter share over a plan (fp32 reduction into fp32 shards).
+hipError_t launch_share_fast_dev(int in_dtype, int wmax, const DevTable& t, int blocks, const ReduceParams& p,
+                                 hipStream_t stream);
 
 inline int dtype_size(int dt) { return dt == MDX_F32 ? 4 : 2; }
 

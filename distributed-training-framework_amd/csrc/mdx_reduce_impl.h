@@ -466,7 +466,9 @@ __device__ __forceinline__ void share_body(const PieceRun& run, const ReducePara
   for (int r = 0; r < WMAX; ++r) {
     src[r] = (r == rank) ? static_cast<const In*>(run.own) : static_cast<const In*>(p.peer[r]) + pos;
   }
-  Out* out = static_cast<Out*>(p.out) + pos;
+  // A piece of a multi-unit share carries its own destination (each unit's
+  // shard gradient is a tensor of its own); otherwise the shard is p.out.
+  Out* out = run.grad ? static_cast<Out*>(run.grad) : static_cast<Out*>(p.out) + pos;
   bool bad = false;
 
   auto widen = [&](In x) -> Acc {
@@ -595,6 +597,20 @@ __global__ void __launch_bounds__(kBlock) share_kernel_one(PieceOne b, ReducePar
 template <typename In, typename Acc, typename Out, int WMAX>
 __global__ void __launch_bounds__(kBlock) share_kernel_few(PieceFew b, ReduceParams p) {
   share_run<In, Acc, Out, WMAX>(PieceFewView{b}.piece_run(int(blockIdx.x)), p);
+}
+
+// Pieces of a device plan: the shares of many FSDP units in one dispatch.
+template <typename In, typename Acc, typename Out, int WMAX>
+__global__ void __launch_bounds__(kBlock) share_kernel_dev(DevTable t, ReduceParams p) {
+  const DevView v{t};
+  share_run<In, Acc, Out, WMAX>(v.piece_run(v.block()), p);
+}
+
+template <typename In, typename Acc, typename Out, int WMAX>
+hipError_t launch_share_dev_w(const DevTable& t, int blocks, const ReduceParams& p, hipStream_t stream) {
+  return launch_plan_slices(t, blocks, [&](const DevTable& slice, int grid) {
+    hipLaunchKernelGGL((share_kernel_dev<In, Acc, Out, WMAX>), dim3(grid), dim3(kBlock), 0, stream, slice, p);
+  });
 }
 
 template <typename In, typename Acc, typename Out, int WMAX>

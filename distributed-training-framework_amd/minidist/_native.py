@@ -25,7 +25,7 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -57,6 +57,11 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_planned": (_i32, [_vp, _vp, _f32, _vp, _vp]),
     "mdx_pack_allreduce_unpack_planned_noalloc": (_i32, [_vp, _f32, _vp, _vp, _vp]),
+    "mdx_reduce_scatter_share_multi": (
+        _i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _vp],
+    ),
+    "mdx_plan_reduce_scatter_share_multi": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "mdx_reduce_scatter_share_multi_planned": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp]),
     "mdx_strerror": (ctypes.c_char_p, [_i32]),
     "mdx_abi_version": (_i32, []),
 }
@@ -263,6 +268,7 @@ def reduce_scatter_share(
     check(rc, "mdx_reduce_scatter_share")
 
 
+MDX_EDTYPE = -2
 MDX_EALIAS = -4
 MDX_ESIZE = -5
 MDX_ESCRATCH = -6
@@ -353,6 +359,40 @@ def pack_allreduce_unpack_planned(
     rc = lib().mdx_pack_allreduce_unpack_planned(plan.host_ptr, plan.device_ptr, inv_scale, found_inf, clear_flag,
                                                  stream)
     check(rc, "mdx_pack_allreduce_unpack_planned")
+
+
+def reduce_scatter_share_multi(
+    own: np.ndarray, outs: list[int], peers: list[int], rank: int, in_dtype: int, reduce_dtype: int, divide: bool,
+    shard_dtype: int, accumulate: bool, inv_scale: float, found_inf: int | None, stream: int,
+) -> None:
+    """Several units' reduce-scatter shares: piece k of ``own`` (absolute row positions) lands in ``outs[k]``."""
+    rc = lib().mdx_reduce_scatter_share_multi(
+        _ptr(own), _ptrs(outs) if outs else None, len(own), _ptrs(peers), len(peers), rank, in_dtype, reduce_dtype,
+        int(divide), shard_dtype, int(accumulate), inv_scale, found_inf, stream,
+    )
+    check(rc, "mdx_reduce_scatter_share_multi")
+
+
+def plan_reduce_scatter_share_multi(
+    own: np.ndarray, outs: list[int], peers: list[int], rank: int, in_dtype: int, device
+) -> Plan:
+    out_ptrs = _ptrs(outs) if outs else None
+    reps = _ptrs(peers)
+    return _build_plan(
+        lambda buf, size: lib().mdx_plan_reduce_scatter_share_multi(
+            _ptr(own), out_ptrs, len(own), reps, len(peers), rank, in_dtype, buf, size
+        ),
+        "mdx_plan_reduce_scatter_share_multi", device,
+    )
+
+
+def reduce_scatter_share_multi_planned(
+    plan: Plan, divide: bool, accumulate: bool, inv_scale: float, found_inf: int | None, stream: int
+) -> None:
+    rc = lib().mdx_reduce_scatter_share_multi_planned(
+        plan.host_ptr, plan.device_ptr, int(divide), int(accumulate), inv_scale, found_inf, stream
+    )
+    check(rc, "mdx_reduce_scatter_share_multi_planned")
 
 
 def pack_allreduce_unpack_planned_noalloc(

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 6
+#define MDX_ABI_VERSION 7
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -245,6 +245,25 @@ MDX_API int mdx_reduce_scatter_share(const mdx_piece* own, int n_own, const void
                              int shard_dtype, int accumulate, float inv_scale, int32_t* found_inf,
                              void* stream);
 
+/* The reduce-scatter shares of several FSDP units in one call.
+ * Replaces, for every unit whose gradients are ready at the same time,
+ * _FSDPUnit.reduce_scatter_grads (minidist/fsdp.py:215-237) -- the units
+ * FullyShardedDataParallel.finish_gradient_sync flushes after a no_sync
+ * accumulation (fsdp.py:462-470) -- with the arithmetic of
+ * mdx_reduce_scatter_share.  The units' contributions live in one set of
+ * rows: `peers[r]` is the base of rank r's row (peers[rank] is ignored) and
+ * piece k covers elements [pos, pos + numel) of every row; this rank's data
+ * for it comes from pieces[k].own (NULL = zeros) and its result goes to
+ * outs[k] (numel elements of shard_dtype), which may be any tensor -- each
+ * unit's shard gradient is its own.  Destinations must not overlap the rows,
+ * any piece's own data or each other.  divide / accumulate / inv_scale /
+ * found_inf apply to every piece as in mdx_reduce_scatter_share.  One
+ * dispatch per 48 pieces; the planned form below takes any number. */
+MDX_API int mdx_reduce_scatter_share_multi(const mdx_piece* pieces, void* const* outs, int n_pieces,
+                                           const void* const* peers, int world, int rank, int in_dtype,
+                                           int reduce_dtype, int divide, int shard_dtype, int accumulate,
+                                           float inv_scale, int32_t* found_inf, void* stream);
+
 /* fp32 -> bf16 round-to-nearest-even cast (NaN -> 0xFFFF), written straight
  * into this rank's slot of the FSDP gather buffer.
  * Replaces `src = flat_shard.to(param_dtype)` in _FSDPUnit.unshard
@@ -298,6 +317,17 @@ MDX_API int mdx_plan_allreduce_unpack_wide(const void* const* replicas, int worl
 MDX_API int mdx_plan_pack_allreduce_unpack(const void* const* replicas, int world, int rank, int wire_dtype,
                                            const mdx_pack_run* runs, int n_runs, void* out, int reduce_dtype,
                                            float scale, void* plan, int64_t* plan_bytes);
+
+/* Plan for mdx_reduce_scatter_share_multi_planned (arguments as
+ * mdx_reduce_scatter_share_multi, with reduce and shard dtype MDX_F32 -- the
+ * FSDP default -- which is what the planned form supports). */
+MDX_API int mdx_plan_reduce_scatter_share_multi(const mdx_piece* pieces, void* const* outs, int n_pieces,
+                                                const void* const* peers, int world, int rank, int in_dtype,
+                                                void* plan, int64_t* plan_bytes);
+
+/* mdx_reduce_scatter_share_multi over a plan: every unit's share in one dispatch. */
+MDX_API int mdx_reduce_scatter_share_multi_planned(const void* plan, const void* d_plan, int divide, int accumulate,
+                                                   float inv_scale, int32_t* found_inf, void* stream);
 
 /* mdx_pack_allreduce_unpack over a plan: one dispatch. */
 MDX_API int mdx_pack_allreduce_unpack_planned(const void* plan, const void* d_plan, float inv_scale,

@@ -341,3 +341,82 @@ def test_dropped_fsdp_frees_its_buffers():
     assert all(r() is None for r in refs)
     assert torch.cuda.memory_allocated(DEV) == base
 
+
+
+class _Blk(torch.nn.Module):
+    def __init__(self, k: int, gen: torch.Generator):
+        super().__init__()
+        self.w = torch.nn.Parameter(torch.randn(17 + k % 7, 9, generator=gen) * 0.02)
+        self.b = torch.nn.Parameter(torch.randn(5 + k % 3, generator=gen) * 0.02)
+
+
+class _Stack(torch.nn.Module):
+    def __init__(self, n: int, seed: int = 5):
+        super().__init__()
+        gen = torch.Generator().manual_seed(seed)
+        self.blocks = torch.nn.ModuleList([_Blk(k, gen) for k in range(n)])
+
+
+def _grad_bits(rng, n, dt):
+    return o.from_f32((rng.standard_normal(n) * 1e-3).astype(np.float32), dt)
+
+
+def _dev_from_bits(bits, dtype):
+    if dtype == torch.bfloat16:
+        return torch.from_numpy(bits.view(np.int16).copy()).to(DEV).view(torch.bfloat16)
+    return torch.from_numpy(bits.copy()).to(DEV)
+
+
+@pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n_blocks", [3, 60])
+@pytest.mark.parametrize("comm_streams", [False, True])
+def test_flush_of_many_units_matches_per_unit_and_oracle(param_dtype, n_blocks, comm_streams):
+    """finish_gradient_sync with gradients on every unit sends all units' shares out together (one
+    multi-unit dispatch; a device plan beyond 48 pieces).  Every shard gradient equals the per-unit
+    reduce_scatter_grads result and the oracle bit for bit; a second flush accumulates into them."""
+    W, rank = 4, 2
+    dt = o.BF16 if param_dtype == torch.bfloat16 else o.F32
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    wraps = [FSDP(_Stack(n_blocks).to(DEV), unit_types=(_Blk,), process_group=ResidentGroup(W, rank, DEV),
+                  mixed_precision=policy, comm_streams=comm_streams and i == 0) for i in range(2)]
+    batched, per_unit = wraps
+    assert len(batched._units) == n_blocks
+    rng = np.random.default_rng(77 + n_blocks)
+    existing = [None] * n_blocks
+    for flush in range(2):
+        for u, (ua, ub) in enumerate(zip(batched._units, per_unit._units, strict=True)):
+            grads = [[_grad_bits(rng, n, dt) for n in ua.numels] for _ in range(W)]
+            for fs in (ua, ub):
+                peers = fs.peer_grad_contributions()
+                for r in range(W):
+                    if r != rank:
+                        peers[r].copy_(_dev_from_bits(o.fsdp_flatten(grads[r], dt, fs.numels, fs.padded_numel, dt),
+                                                      param_dtype))
+                for p, g in zip(fs.params, grads[rank], strict=True):
+                    p.grad = _dev_from_bits(g, param_dtype).view(p.shape)
+            existing[u] = o.fsdp_reduce_scatter_share(grads, dt, ua.numels, rank, o.F32, o.F32, existing=existing[u])
+        batched.finish_gradient_sync()
+        for ub in per_unit._units:
+            ub.reduce_scatter_grads()
+        for u, (ua, ub) in enumerate(zip(batched._units, per_unit._units, strict=True)):
+            got, ref = host_bits(ua.flat_shard.grad), host_bits(ub.flat_shard.grad)
+            assert same_bits(got, ref), f"flush {flush} unit {u}: " + first_mismatch(got, ref)
+            assert same_bits(got, existing[u]), f"flush {flush} unit {u}: " + first_mismatch(got, existing[u])
+            assert all(p.grad is None for p in ua.params)
+
+
+@pytest.mark.parametrize("comm_streams", [False, True])
+def test_summon_of_many_units_gathers_every_parameter(comm_streams):
+    """summon_full_params over 60 units: the casts and the peers' gather copies go out batched (device
+    plans beyond 48 spans); every gathered parameter is the bf16 cast of its initial value, and the
+    units are freed again afterwards."""
+    W, rank = 4, 1
+    model = _Stack(60).to(DEV)
+    init = {n: p.detach().clone() for n, p in model.named_parameters()}
+    fsdp = FSDP(model, unit_types=(_Blk,), process_group=ResidentGroup(W, rank, DEV),
+                mixed_precision=MixedPrecisionPolicy(param_dtype=torch.bfloat16), comm_streams=comm_streams)
+    with fsdp.summon_full_params():
+        for n, p in model.named_parameters():
+            want = o.bf16_from_f32(init[n].cpu().numpy().reshape(-1))
+            assert np.array_equal(host_bits(p), want), n
+    assert not any(u.is_unsharded for u in fsdp._units)

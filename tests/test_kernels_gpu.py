@@ -822,3 +822,114 @@ def test_pack_clears_the_flag(rng, n_spans, planned):
         assert same_bits(got[off : off + n], o.mul_scalar(to_host(s), o.F32, 0.25))
         off += n
     assert same_bits(got[off:], np.full(len(got) - off, SENTINEL_F32, dtype=np.float32))
+
+
+# ---------------------------------------------------------------------------
+# multi-unit reduce-scatter share (finish_gradient_sync's flush of many units)
+# ---------------------------------------------------------------------------
+
+
+def _multi_share_case(rng, units, idt, W, rank, accumulate, sdt=o.F32, rdt=o.F32):
+    """Units laid out one after another in shared contribution rows; each unit's shard result
+    goes to a tensor of its own.  Returns the pieces, destinations, rows and the expected shards."""
+    layouts, base = [], 0
+    for numels in units:
+        total = sum(numels)
+        S = (total + W - 1) // W
+        layouts.append((numels, S, S * W, base))
+        base += S * W + int(rng.integers(0, 5))  # units need not be packed back to back
+    rows_host = [o.zeros(base, idt) for _ in range(W)]
+    grads_all, pieces, outs, shards, wants, prevs, own_keep = [], [], [], [], [], [], []
+    for u, (numels, S, P, off0) in enumerate(layouts):
+        grads = [[None if (r + i + u) % 5 == 3 else values(rng, n, idt, scale=1e-3) for i, n in enumerate(numels)]
+                 for r in range(W)]
+        grads_all.append(grads)
+        for r in range(W):
+            rows_host[r][off0 : off0 + P] = o.fsdp_flatten(grads[r], idt, numels, P, idt)
+        own_devs = [None if g is None else to_dev(g) for g in grads[rank]]
+        own_keep.append(own_devs)
+        prev = values(rng, S, sdt, specials=False, scale=1e-3)
+        shard = to_dev(prev) if accumulate else empty_dev(S, sdt)
+        shards.append(shard)
+        prevs.append(prev)
+        lo, hi = rank * S, rank * S + S
+        off, cursor = 0, lo
+        for t, n in zip(own_devs, numels, strict=True):
+            a, b = max(off, lo), min(off + n, hi)
+            if a < b:
+                ptr = 0 if t is None else t.data_ptr() + (a - off) * esize(idt)
+                pieces.append((ptr, off0 + a, b - a))
+                outs.append(shard.data_ptr() + (a - lo) * esize(sdt))
+                cursor = b
+            off += n
+        if cursor < hi:
+            pieces.append((0, off0 + cursor, hi - cursor))
+            outs.append(shard.data_ptr() + (cursor - lo) * esize(sdt))
+        wants.append(o.fsdp_reduce_scatter_share(grads, idt, numels, rank, rdt, sdt,
+                                                 existing=prev if accumulate else None))
+    row_devs = [to_dev(h) for h in rows_host]
+    return dict(pieces=nat.pieces_array(pieces), outs=outs, rows=row_devs, shards=shards, wants=wants,
+                prevs=prevs, keep=own_keep)
+
+
+@pytest.mark.parametrize("planned", [False, True])
+@pytest.mark.parametrize("idt", [o.BF16, o.F32, o.F16])
+@pytest.mark.parametrize("W,rank", [(2, 1), (3, 0), (8, 5), (16, 9)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_reduce_scatter_share_multi_matches_oracle(rng, planned, idt, W, rank, accumulate):
+    """Sixty units of 1-8 parameters (at least one piece each: more than one kernel-argument table)
+    reduced in one call, each unit's shard against the oracle; the plan form does it in one dispatch
+    and is launched twice (the second launch must give the same bits again, from fresh inputs)."""
+    units = [[int(x) for x in rng.integers(1, 3000, int(rng.integers(1, 9)))] for _ in range(60)]
+    c = _multi_share_case(rng, units, idt, W, rank, accumulate)
+    peers = [r.data_ptr() for r in c["rows"]]
+    assert len(c["pieces"]) > 48
+    if planned:
+        plan = nat.plan_reduce_scatter_share_multi(c["pieces"], c["outs"], peers, rank, code(idt), DEV)
+        for launch in range(2):
+            if launch:  # restore the shards and launch the same plan again
+                for sh, prev in zip(c["shards"], c["prevs"], strict=True):
+                    sh.copy_(to_dev(prev) if accumulate else empty_dev(sh.numel(), o.F32))
+            nat.reduce_scatter_share_multi_planned(plan, True, accumulate, 1.0, None, stream())
+            for u, (sh, want) in enumerate(zip(c["shards"], c["wants"], strict=True)):
+                got = to_host(sh)
+                assert same_bits(got, want), f"launch {launch} unit {u}: " + first_mismatch(got, want)
+    else:
+        nat.reduce_scatter_share_multi(c["pieces"], c["outs"], peers, rank, code(idt), nat.MDX_F32, True,
+                                       nat.MDX_F32, accumulate, 1.0, None, stream())
+        for u, (sh, want) in enumerate(zip(c["shards"], c["wants"], strict=True)):
+            got = to_host(sh)
+            assert same_bits(got, want), f"unit {u}: " + first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("sdt,rdt", [(o.BF16, o.F32), (o.F16, o.F32), (o.F32, o.BF16)])
+def test_reduce_scatter_share_multi_other_dtypes(rng, sdt, rdt):
+    """Low-precision shards (keep_low_precision_shard) and a bf16 reduction go through the
+    kernel-argument form of the multi-unit share, against the oracle."""
+    units = [[int(x) for x in rng.integers(1, 2000, int(rng.integers(1, 6)))] for _ in range(6)]
+    W, rank = 4, 3
+    c = _multi_share_case(rng, units, o.BF16, W, rank, False, sdt=sdt, rdt=rdt)
+    peers = [r.data_ptr() for r in c["rows"]]
+    nat.reduce_scatter_share_multi(c["pieces"], c["outs"], peers, rank, nat.MDX_BF16, code(rdt), True, code(sdt),
+                                   False, 1.0, None, stream())
+    for u, (sh, want) in enumerate(zip(c["shards"], c["wants"], strict=True)):
+        got = to_host(sh)
+        assert same_bits(got, want), f"unit {u}: " + first_mismatch(got, want)
+
+
+def test_reduce_scatter_share_multi_rejects_overlaps():
+    """A destination over a contribution row, over a piece's own data or over another
+    destination is refused before anything is launched; the plan rejects non-fp32 shards."""
+    rows = [torch.zeros(4096, device=DEV) for _ in range(2)]
+    own = torch.zeros(1024, device=DEV)
+    out = torch.zeros(2048, device=DEV)
+    peers = [r.data_ptr() for r in rows]
+    pieces = nat.pieces_array([(own.data_ptr(), 0, 512), (0, 512, 512)])
+    for outs in ([rows[0].data_ptr(), out.data_ptr()], [out.data_ptr(), own.data_ptr()],
+                 [out.data_ptr(), out.data_ptr() + 4 * 100]):
+        rc = nat.lib().mdx_reduce_scatter_share_multi(
+            nat._ptr(pieces), nat._ptrs(outs), 2, nat._ptrs(peers), 2, 1, nat.MDX_F32, nat.MDX_F32, 1,
+            nat.MDX_F32, 0, 1.0, None, stream())
+        assert rc == nat.MDX_EALIAS, nat.strerror(rc)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
