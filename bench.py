@@ -178,6 +178,7 @@ TRAFFIC_FILES = {
     ("cfg2", False): "allreduce_unpack_gpt2_medium_w4_traffic.json",
     ("cfg4", False): "allreduce_wide_llama7b_w8_traffic.json",
     ("cfg3", False): "share_cast_gpt2_xl_fsdp_w8_traffic.json",
+    ("cfg3", True): "share_multi_cast_batch_gpt2_xl_fsdp_w8_traffic.json",
 }
 
 
@@ -680,7 +681,7 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(share_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(name) if mode != "batched" else None,
+            "traffic": measured_traffic(name, mode == "batched"),
             "bytes_per_launch": 20 * S * per_launch,
             "avg_launch_ms": round(share_avg, 5),
         },
