@@ -1108,4 +1108,35 @@ int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float inv_scale,
   return mdx_pack_allreduce_unpack_planned(plan, d_plan, inv_scale, found_inf, clear_flag, stream);
 }
 
+int mdx_ipc_export(const void* ptr, mdx_ipc_handle* out) {
+  if (ptr == nullptr || out == nullptr) return MDX_EINVAL;
+  static_assert(sizeof(hipIpcMemHandle_t) == MDX_IPC_HANDLE_BYTES, "IPC handle size");
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  hipError_t e = hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(const_cast<void*>(ptr)));
+  if (e != hipSuccess) return int(e);
+  if (int64_t(size) >= MDX_IPC_MAX_ALLOC_BYTES) return MDX_ESIZE;
+  hipIpcMemHandle_t h;
+  e = hipIpcGetMemHandle(&h, reinterpret_cast<void*>(base));
+  if (e != hipSuccess) return int(e);
+  memcpy(out->bytes, &h, sizeof(h));
+  out->offset = int64_t(addr(ptr) - addr(reinterpret_cast<const void*>(base)));
+  out->alloc_bytes = int64_t(size);
+  return MDX_OK;
+}
+
+int mdx_ipc_open(const mdx_ipc_handle* h, void** base) {
+  if (h == nullptr || base == nullptr) return MDX_EINVAL;
+  if (h->alloc_bytes <= 0 || h->alloc_bytes >= MDX_IPC_MAX_ALLOC_BYTES) return MDX_ESIZE;
+  if (h->offset < 0 || h->offset >= h->alloc_bytes) return MDX_EINVAL;
+  hipIpcMemHandle_t mh;
+  memcpy(&mh, h->bytes, sizeof(mh));
+  return status(hipIpcOpenMemHandle(base, mh, hipIpcMemLazyEnablePeerAccess));
+}
+
+int mdx_ipc_close(void* base) {
+  if (base == nullptr) return MDX_EINVAL;
+  return status(hipIpcCloseMemHandle(base));
+}
+
 }  // extern "C"

@@ -15,6 +15,7 @@ that says so.
 
 from .amp import DistributedGradScaler, PrecisionConfig, resolve_precision
 from .comm import (
+    IpcGroup,
     ResidentGroup,
     barrier,
     comm_stats,
@@ -63,6 +64,7 @@ __all__ = [
     "DistributedGradScaler",
     "PrecisionConfig",
     "ResidentGroup",
+    "IpcGroup",
     "resolve_precision",
     "init_distributed",
     "shutdown_distributed",

@@ -25,7 +25,7 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mdx_plan_reduce_scatter_share_multi": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp]),
     "mdx_reduce_scatter_share_multi_planned": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp]),
+    "mdx_ipc_export": (_i32, [_vp, _vp]),
+    "mdx_ipc_open": (_i32, [_vp, _vp]),
+    "mdx_ipc_close": (_i32, [_vp]),
     "mdx_strerror": (ctypes.c_char_p, [_i32]),
     "mdx_abi_version": (_i32, []),
 }
@@ -393,6 +396,42 @@ def reduce_scatter_share_multi_planned(
         plan.host_ptr, plan.device_ptr, int(divide), int(accumulate), inv_scale, found_inf, stream
     )
     check(rc, "mdx_reduce_scatter_share_multi_planned")
+
+
+IPC_HANDLE_BYTES = 64
+IPC_MAX_ALLOC_BYTES = 1 << 31
+
+
+class IpcHandle(ctypes.Structure):
+    """``mdx_ipc_handle``: the runtime's handle of a device allocation, the exported pointer's
+    offset in it, and the allocation's size."""
+
+    _fields_ = [("bytes", ctypes.c_ubyte * IPC_HANDLE_BYTES), ("offset", ctypes.c_int64),
+                ("alloc_bytes", ctypes.c_int64)]
+
+    def to_bytes(self) -> bytes:
+        return bytes(memoryview(self))
+
+    @classmethod
+    def from_bytes(cls, raw: bytes) -> IpcHandle:
+        return cls.from_buffer_copy(raw)
+
+
+def ipc_export(ptr: int) -> IpcHandle:
+    h = IpcHandle()
+    check(lib().mdx_ipc_export(ptr, ctypes.byref(h)), "mdx_ipc_export")
+    return h
+
+
+def ipc_open(h: IpcHandle) -> int:
+    """Maps a peer's exported allocation; returns the exported pointer in this process."""
+    base = ctypes.c_void_p()
+    check(lib().mdx_ipc_open(ctypes.byref(h), ctypes.byref(base)), "mdx_ipc_open")
+    return int(base.value) + int(h.offset)
+
+
+def ipc_close(ptr: int, h: IpcHandle) -> None:
+    check(lib().mdx_ipc_close(ptr - int(h.offset)), "mdx_ipc_close")
 
 
 def pack_allreduce_unpack_planned_noalloc(

@@ -49,6 +49,7 @@ __all__ = [
     "broadcast",
     "print_rank0",
     "ResidentGroup",
+    "IpcGroup",
     "StreamWork",
     "zeros_for_collective",
     "record_all_reduce",
@@ -606,6 +607,153 @@ class ResidentGroup:
         stream = torch.cuda.current_stream(input_.device)
         _native.pack(_native.spans_array(rows), code, code, 1.0, False, stream.cuda_stream)
         return StreamWork(stream) if async_op else None
+
+
+class _IpcArena:
+    """One symmetric buffer of an :class:`IpcGroup`: this rank's row is an allocation of its
+    own; the peers' rows are their allocations, mapped into this process over IPC."""
+
+    __slots__ = ("own", "numel", "dtype", "esize", "own_base", "row_ptrs", "target", "handles")
+
+    def __init__(self, own: torch.Tensor, numel: int, row_ptrs: list[int], handles: list):
+        self.own = own
+        self.numel = numel
+        self.dtype = own.dtype
+        self.esize = own.element_size()
+        self.own_base = own.data_ptr()
+        self.row_ptrs = row_ptrs
+        self.target: torch.Tensor | None = None
+        self.handles = handles  # (mapped pointer, handle) of each peer row, None for this rank's
+
+    def offset_of(self, t: torch.Tensor) -> int | None:
+        p = t.data_ptr()
+        off, rem = divmod(p - self.own_base, self.esize)
+        if rem or off < 0 or off + t.numel() > self.numel or t.dtype != self.dtype:
+            return None
+        return off
+
+
+class IpcGroup(ResidentGroup):
+    """W processes of a real process group whose contribution rows are mapped into each other.
+
+    The multi-GPU design of this path, runnable here with W processes sharing
+    the one GPU: each rank allocates its row of every symmetric buffer
+    (:meth:`zeros`, each row an allocation below 2 GiB), exports it over IPC,
+    and maps its peers' rows, so every collective is a *one-shot* reduction:
+    each rank reads all W rows with the same rank-ordered kernels a
+    :class:`ResidentGroup` uses and computes the full result itself,
+    bit-identical on every rank.  The reference hands each bucket to
+    ``dist.all_reduce`` instead (minidist/comm.py:223-234).
+
+    Ordering is the host's: before a reduction every rank has finished
+    writing its row (stream synchronisation, then a barrier over
+    ``process_group``), and after it every rank has finished reading its
+    peers' rows (the same again) before anyone writes a row again.  No kernel
+    waits on a flag a peer sets.  The pack cannot be fused into the reduction
+    (a rank's row must be complete before its peers read it), so DDP runs the
+    two-dispatch pipeline over this group (``fuses_pack`` is False).
+    ``process_group`` carries only host traffic: the handles and the barriers
+    (gloo is enough).
+    """
+
+    fuses_pack = False
+
+    def __init__(self, process_group=None, device: torch.device | str | None = None):
+        self.process_group = process_group
+        super().__init__(dist.get_world_size(process_group), dist.get_rank(process_group), device)
+
+    def __repr__(self) -> str:
+        return f"IpcGroup(world_size={self._world}, rank={self._rank}, device={self.device})"
+
+    # -- symmetric memory ---------------------------------------------------
+
+    def zeros(self, numel: int, dtype: torch.dtype) -> torch.Tensor:
+        """This rank's row of a new zero-filled symmetric buffer; every rank calls it in the
+        same order with the same sizes (the rows are exchanged collectively)."""
+        esize = torch.empty((), dtype=dtype).element_size()
+        align = _ROW_ALIGN_BYTES // esize
+        row_elems = max(align, (numel + align - 1) // align * align)
+        own = torch.zeros(row_elems, dtype=dtype, device=self.device)
+        torch.cuda.current_stream(self.device).synchronize()  # the zeros are in place before a peer maps the row
+        handle = _native.ipc_export(own.data_ptr())
+        raw: list = [None] * self._world
+        dist.all_gather_object(raw, (handle.to_bytes(), row_elems, str(dtype)), group=self.process_group)
+        # every kernel reads all W rows over this rank's extent: the rows must agree
+        if any((n, d) != (row_elems, str(dtype)) for _, n, d in raw):
+            raise RuntimeError(f"IpcGroup.zeros: the ranks asked for different buffers {[(n, d) for _, n, d in raw]}")
+        row_ptrs, handles = [], []
+        for r in range(self._world):
+            if r == self._rank:
+                row_ptrs.append(own.data_ptr())
+                handles.append(None)
+                continue
+            h = _native.IpcHandle.from_bytes(raw[r][0])
+            if h.offset + row_elems * esize > h.alloc_bytes:
+                raise RuntimeError(f"IpcGroup.zeros: rank {r}'s row is not inside the allocation it exported")
+            ptr = _native.ipc_open(h)
+            row_ptrs.append(ptr)
+            handles.append((ptr, h))
+        arena = _IpcArena(own, numel, row_ptrs, handles)
+        self._arenas.append(arena)
+        return own[:numel]
+
+    def replicas(self, t: torch.Tensor) -> list[torch.Tensor]:
+        raise NotImplementedError("an IpcGroup's peer rows belong to other processes (only addresses are mapped)")
+
+    def release(self) -> None:
+        """Unmap every peer row (collective: no rank still reads a row when it is released)."""
+        torch.cuda.current_stream(self.device).synchronize()
+        dist.barrier(group=self.process_group)
+        for arena in self._arenas:
+            for entry in arena.handles:
+                if entry is not None:
+                    _native.ipc_close(*entry)
+        self._arenas.clear()
+
+    # -- the one-shot protocol ----------------------------------------------
+
+    def _rows_written(self) -> None:
+        """Every rank's writes to its rows are complete (this one's: its stream is drained)."""
+        torch.cuda.current_stream(self.device).synchronize()
+        dist.barrier(group=self.process_group)
+
+    def _rows_read(self) -> None:
+        """Every rank has finished reading its peers' rows."""
+        torch.cuda.current_stream(self.device).synchronize()
+        dist.barrier(group=self.process_group)
+
+    def _one_shot(self, launch, async_op: bool):
+        self._rows_written()
+        launch()
+        self._rows_read()
+        return _CompletedWork() if async_op else None
+
+    def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
+        return self._one_shot(lambda: ResidentGroup.all_reduce_sum(self, tensors), async_op)
+
+    def all_reduce_unpack(self, buffer, runs, grad_dtype, inv_scale=1.0, found_inf=None, async_op=False,
+                          bucket=None):
+        return self._one_shot(lambda: ResidentGroup.all_reduce_unpack(
+            self, buffer, runs, grad_dtype, inv_scale, found_inf, bucket=bucket), async_op)
+
+    def all_reduce_unpack_wide(self, wire, bucket, runs, grad_dtype, prescale, inv_scale=1.0, found_inf=None,
+                               async_op=False):
+        return self._one_shot(lambda: ResidentGroup.all_reduce_unpack_wide(
+            self, wire, bucket, runs, grad_dtype, prescale, inv_scale, found_inf), async_op)
+
+    def all_reduce_unpack_planned(self, plan, device, inv_scale=1.0, found_inf=None, async_op=False):
+        return self._one_shot(lambda: ResidentGroup.all_reduce_unpack_planned(
+            self, plan, device, inv_scale, found_inf), async_op)
+
+    def pack_all_reduce_unpack(self, *args, **kwargs):
+        raise NotImplementedError("IpcGroup: a rank's row must be complete before its peers read it (no fused pack)")
+
+    pack_all_reduce_unpack_planned = pack_all_reduce_unpack
+
+    def reduce_scatter_sum(self, output, input_, async_op: bool = False):
+        raise NotImplementedError("IpcGroup implements the DDP all-reduce; FSDP runs over the process group itself")
+
+    all_gather_into = reduce_scatter_sum
 
 
 def zeros_for_collective(numel: int, dtype: torch.dtype, device: torch.device, group=None) -> torch.Tensor:

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 7
+#define MDX_ABI_VERSION 8
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -368,6 +368,41 @@ MDX_API int mdx_allreduce_unpack_planned(const void* plan, const void* d_plan, f
 #define MDX_NOALLOC_SCRATCH_BYTES (256 * 1024)
 MDX_API int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float inv_scale, int32_t* found_inf,
                                                       int32_t* clear_flag, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Peer rows over IPC: the transport of the one-shot all-reduce.
+ *
+ * No counterpart in the reference, which hands every bucket to
+ * dist.all_reduce (minidist/comm.py:223-234, called from ddp.py:243-247):
+ * these calls let W processes map each other's contribution rows, so that each
+ * rank runs the same rank-ordered fused reduction (mdx_allreduce_unpack[_planned])
+ * over the peers' rows -- the one-shot all-reduce.  The caller orders the ranks
+ * (every rank's pack complete before any rank reads it, every read complete
+ * before a rank overwrites its row).
+ * ------------------------------------------------------------------------- */
+
+#define MDX_IPC_HANDLE_BYTES 64
+/* Each exported allocation stays below this size (larger shared allocations
+ * have not opened reliably on this platform). */
+#define MDX_IPC_MAX_ALLOC_BYTES ((int64_t)1 << 31)
+
+typedef struct mdx_ipc_handle {
+  unsigned char bytes[MDX_IPC_HANDLE_BYTES]; /* the runtime's IPC memory handle */
+  int64_t offset;                            /* of the exported pointer in its allocation */
+  int64_t alloc_bytes;                       /* size of that allocation */
+} mdx_ipc_handle;
+
+/* The IPC handle of the device allocation that contains `ptr`.  Returns
+ * MDX_ESIZE (nothing exported) when that allocation is MDX_IPC_MAX_ALLOC_BYTES
+ * or larger. */
+MDX_API int mdx_ipc_export(const void* ptr, mdx_ipc_handle* out);
+
+/* Maps another process's exported allocation into this one; *base receives
+ * the allocation's base here (the exported pointer is *base + h->offset). */
+MDX_API int mdx_ipc_open(const mdx_ipc_handle* h, void** base);
+
+/* Unmaps a base mdx_ipc_open returned. */
+MDX_API int mdx_ipc_close(void* base);
 
 /* Static description of a status code. */
 MDX_API const char* mdx_strerror(int code);

@@ -1,0 +1,110 @@
+"""The one-shot all-reduce over IPC-mapped rows: W processes on the one GPU (comm.IpcGroup).
+
+W processes (2, 3 or 4, all on ``cuda:0``) meet in a gloo group, which carries
+only host traffic: the IPC handles of each rank's contribution rows and the
+barriers of the one-shot protocol.  DDP over an ``IpcGroup`` packs each rank's
+gradients into its own row (``mdx_pack``, x 1/W), and after every rank's pack
+is done each rank runs the fused rank-ordered reduction + unpack + unscale +
+found-inf over all W rows -- its peers' rows read through their IPC mappings
+-- so every rank computes the whole average itself.  The reference hands each
+bucket to ``dist.all_reduce`` (minidist/comm.py:223-234, ddp.py:243-274).
+
+Every rank's gradients are checked bit for bit against the oracle's
+rank-ordered pipeline over all ranks' seeded gradients, for two steps: the
+second with an inf in one rank's gradients, which every rank must flag.
+"""
+
+from __future__ import annotations
+
+import os
+import time
+from datetime import timedelta
+
+import numpy as np
+import pytest
+import torch
+import torch.distributed as dist
+import torch.multiprocessing as mp
+
+from conftest import first_mismatch, same_bits
+from minidist import DDP, DistributedGradScaler, IpcGroup
+from minidist import workloads as wl
+from oracle import gradpath as o
+
+pytestmark = pytest.mark.gpu
+SCALE = 2.0**16
+CAP_MB = 1.0
+CFG = dict(n_layer=4, n_embd=256, vocab=1024, ctx=128)  # 52 gradients: one device plan
+INF_AT = (1, 3, 17)  # (rank, parameter, element) that overflows in step 1
+
+
+def _grads(rank: int, specs) -> list[torch.Tensor]:
+    g = torch.Generator().manual_seed(1234 + 7919 * rank)
+    return [torch.randn(s.numel, generator=g) * (1e-2 * SCALE) for s in specs]
+
+
+def _worker(rank: int, world: int, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        group = IpcGroup(dist.group.WORLD, dev)
+        specs = wl.gpt_specs(**CFG)
+        model = wl.SpecModule(specs, dev)
+        params = list(model.parameters())
+        scaler = DistributedGradScaler(init_scale=SCALE, process_group=group)
+        ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+
+        class _Opt:
+            param_groups = [{"params": params}]
+
+        host = _grads(rank, specs)
+        out = {"buckets": np.array(len(ddp._buckets))}
+        for step in range(2):
+            for i, (p, g) in enumerate(zip(params, host, strict=True)):
+                t = g.clone()
+                if step == 1 and (rank, i) == INF_AT[:2]:
+                    t[INF_AT[2]] = float("inf")
+                p.grad = t.to(dev).view(p.shape)
+            t0 = time.perf_counter()
+            ddp.finish_gradient_sync()
+            found = scaler.unscale_(_Opt())
+            out[f"ms_{step}"] = np.array((time.perf_counter() - t0) * 1e3)
+            scaler.update()
+            out[f"found_{step}"] = np.array(found)
+            for i, p in enumerate(params):
+                out[f"grad_{step}_{i}"] = p.grad.detach().reshape(-1).cpu().numpy()
+        group.release()
+        np.savez(os.path.join(out_dir, f"ipc_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("world", [2, 3, 4])
+def test_ipc_one_shot_all_reduce_bitwise(tmp_path, world):
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup one-shot all-reduce)", flush=True)
+    mp.spawn(_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    res = []
+    for r in range(world):
+        with np.load(tmp_path / f"ipc_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    specs = wl.gpt_specs(**CFG)
+    numels = [s.numel for s in specs]
+    n = len(specs)
+    assert int(res[0]["buckets"]) > 2
+    for step in range(2):
+        replica = [[g.numpy() for g in _grads(r, specs)] for r in range(world)]
+        if step == 1:
+            rr, i, k = INF_AT
+            replica[rr][i] = replica[rr][i].copy()
+            replica[rr][i][k] = np.inf
+        for rank in range(world):
+            want = o.ddp_pipeline(replica, [o.F32] * n, numels, CAP_MB, rank, 1.0 / SCALE)
+            assert bool(res[rank][f"found_{step}"]) == want["found_inf"] == (step == 1)
+            for i in range(n):
+                got = res[rank][f"grad_{step}_{i}"]
+                assert same_bits(got, want["grads"][i]), (
+                    f"step {step} rank {rank} param {i}: " + first_mismatch(got, want["grads"][i]))
+    print("step ms per rank:", [[float(res[r][f"ms_{s}"]) for s in range(2)] for r in range(world)], flush=True)
