@@ -25,18 +25,27 @@ inline int status(hipError_t e) { return e == hipSuccess ? MDX_OK : int(e); }
 
 inline uintptr_t addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }
 
-// Smallest h in [0, kHeadRange) such that every (pointer, element size)
-// advanced by h elements is 16-byte aligned; -1 if none exists or the run has
-// no full fragment of E elements after it.
-int aligned_head(const uintptr_t* ptrs, const int* sizes, int count, int E, int64_t n) {
+// The run's head: the h in [0, kHeadRange) after which the most pointers --
+// each (pointer, element size, weight), stored streams weighing double --
+// are 16-byte aligned (the smallest such h on a tie); -1 if the run has no
+// full fragment of E elements after it.  The vector body accesses every
+// stream with 16-byte (or 8-byte) vector instructions whatever its alignment
+// (the memory pipeline splits an unaligned access); the head picks which
+// streams get the aligned ones, so a gradient view that shares no alignment
+// with its bucket rows still moves in vectors.
+int aligned_head(const uintptr_t* ptrs, const int* sizes, const int* weights, int count, int E, int64_t n) {
+  int best = 0, best_score = -1;
   for (int h = 0; h < kHeadRange; ++h) {
-    bool ok = true;
-    for (int k = 0; k < count && ok; ++k) {
-      ok = ((ptrs[k] + uintptr_t(h) * uintptr_t(sizes[k])) & 15u) == 0;
+    int score = 0;
+    for (int k = 0; k < count; ++k) {
+      if (((ptrs[k] + uintptr_t(h) * uintptr_t(sizes[k])) & 15u) == 0) score += weights[k];
     }
-    if (ok) return (n >= int64_t(h) + E) ? h : -1;
+    if (score > best_score) {
+      best = h;
+      best_score = score;
+    }
   }
-  return -1;
+  return (n >= int64_t(best) + E) ? best : -1;
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -80,7 +89,7 @@ int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool
       const void* rs = src ? src + done * ss : nullptr;
       void* rd = dst + done * ds;
       uintptr_t ptrs[2];
-      int sizes[2];
+      int sizes[2], weights[2] = {2, 1};  // the destination (stored) first
       int np = 0;
       ptrs[np] = addr(rd);
       sizes[np++] = ds;
@@ -88,7 +97,7 @@ int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool
         ptrs[np] = addr(rs);
         sizes[np++] = ss;
       }
-      const int head = aligned_head(ptrs, sizes, np, E, n);
+      const int head = aligned_head(ptrs, sizes, weights, np, E, n);
       const int rc = emit(Rec{rs, rd, 0, n, head, run_blocks(n, head, E, VPB, EPB)});
       if (rc != MDX_OK) return rc;
     }
@@ -113,28 +122,32 @@ int for_each_piece_run(const mdx_piece* pieces, void* const* grads, int n_pieces
       const int64_t n = std::min<int64_t>(kMaxRunElems, pc.numel - done);
       const int64_t pos = pc.pos + done;
       uintptr_t ptrs[MDX_MAX_WORLD + 3];
-      int sizes[MDX_MAX_WORLD + 3];
+      int sizes[MDX_MAX_WORLD + 3], weights[MDX_MAX_WORLD + 3];
       int np = 0;
       const void* ro = own ? own + done * in_size : nullptr;
       void* rg = grad ? grad + done * grad_size : nullptr;
       if (ro) {
         ptrs[np] = addr(ro);
+        weights[np] = 1;
         sizes[np++] = in_size;
       }
       for (int r = 0; r < params.world; ++r) {
         if (r == params.rank && !own_row) continue;
         ptrs[np] = addr(params.peer[r]) + uintptr_t(pos) * uintptr_t(in_size);
+        weights[np] = (r == params.rank) ? 2 : 1;  // the fused pack stores this rank's row
         sizes[np++] = in_size;
       }
       if (params.out) {
         ptrs[np] = addr(params.out) + uintptr_t(pos) * uintptr_t(out_size);
+        weights[np] = 2;
         sizes[np++] = out_size;
       }
       if (rg) {
         ptrs[np] = addr(rg);
+        weights[np] = 2;
         sizes[np++] = grad_size;
       }
-      const int head = aligned_head(ptrs, sizes, np, E, n);
+      const int head = aligned_head(ptrs, sizes, weights, np, E, n);
       const int rc = emit(Rec{ro, rg, pos, n, head, run_blocks(n, head, E, VPB, EPB)});
       if (rc != MDX_OK) return rc;
     }

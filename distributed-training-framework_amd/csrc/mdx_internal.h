@@ -35,10 +35,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // The same vector in the global address space.  Every buffer this library
 // touches is device memory, but pointers read from a work table are generic
 // (flat) pointers; casting them makes the compiler emit global_load/store
-// instead of flat_load/store (no aperture check, no LDS counter).
-typedef __attribute__((address_space(1))) u32x4 gu32x4;
+// instead of flat_load/store (no aperture check, no LDS counter).  The views
+// assume no alignment beyond 2 bytes: every vector access of the kernels goes
+// through them, so a stream that the run's head leaves unaligned still moves
+// in one dwordx4 / dwordx2 instruction per lane (the target runs in
+// unaligned-access mode; for an aligned address the instruction is the same).
+typedef u32x4 u32x4_any __attribute__((aligned(2)));
+typedef __attribute__((address_space(1))) u32x4_any gu32x4;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(1))) u32x2 gu32x2;
+typedef u32x2 u32x2_any __attribute__((aligned(2)));
+typedef __attribute__((address_space(1))) u32x2_any gu32x2;
 
 // ----------------------------------------------------------------------------
 // Element conversions (IEEE, round to nearest even; NaN -> 0xFFFF for bf16,
