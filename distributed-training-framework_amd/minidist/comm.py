@@ -660,6 +660,7 @@ class IpcGroup(ResidentGroup):
 
     def __init__(self, process_group=None, device: torch.device | str | None = None):
         self.process_group = process_group
+        self._released = False
         super().__init__(dist.get_world_size(process_group), dist.get_rank(process_group), device)
 
     def __repr__(self) -> str:
@@ -670,6 +671,8 @@ class IpcGroup(ResidentGroup):
     def zeros(self, numel: int, dtype: torch.dtype) -> torch.Tensor:
         """This rank's row of a new zero-filled symmetric buffer; every rank calls it in the
         same order with the same sizes (the rows are exchanged collectively)."""
+        if self._released:
+            raise RuntimeError("IpcGroup: released")
         esize = torch.empty((), dtype=dtype).element_size()
         align = _ROW_ALIGN_BYTES // esize
         row_elems = max(align, (numel + align - 1) // align * align)
@@ -709,6 +712,8 @@ class IpcGroup(ResidentGroup):
                 if entry is not None:
                     _native.ipc_close(*entry)
         self._arenas.clear()
+        # plans built over this group still hold the peers' (now unmapped) addresses
+        self._released = True
 
     # -- the one-shot protocol ----------------------------------------------
 
@@ -723,6 +728,8 @@ class IpcGroup(ResidentGroup):
         dist.barrier(group=self.process_group)
 
     def _one_shot(self, launch, async_op: bool):
+        if self._released:
+            raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
         self._rows_written()
         launch()
         self._rows_read()
