@@ -1121,6 +1121,11 @@ int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float inv_scale,
   return mdx_pack_allreduce_unpack_planned(plan, d_plan, inv_scale, found_inf, clear_flag, stream);
 }
 
+int mdx_host_device_address(void* host_ptr, void** device_ptr) {
+  if (host_ptr == nullptr || device_ptr == nullptr) return MDX_EINVAL;
+  return status(hipHostGetDevicePointer(device_ptr, host_ptr, 0));
+}
+
 int mdx_ipc_export(const void* ptr, mdx_ipc_handle* out) {
   if (ptr == nullptr || out == nullptr) return MDX_EINVAL;
   static_assert(sizeof(hipIpcMemHandle_t) == MDX_IPC_HANDLE_BYTES, "IPC handle size");

@@ -25,7 +25,7 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mdx_plan_reduce_scatter_share_multi": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp]),
     "mdx_reduce_scatter_share_multi_planned": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp]),
+    "mdx_host_device_address": (_i32, [_vp, _vp]),
     "mdx_ipc_export": (_i32, [_vp, _vp]),
     "mdx_ipc_open": (_i32, [_vp, _vp]),
     "mdx_ipc_close": (_i32, [_vp]),
@@ -396,6 +397,19 @@ def reduce_scatter_share_multi_planned(
         plan.host_ptr, plan.device_ptr, int(divide), int(accumulate), inv_scale, found_inf, stream
     )
     check(rc, "mdx_reduce_scatter_share_multi_planned")
+
+
+def host_device_address(host_ptr: int) -> int:
+    """The address kernels use for pinned host memory at ``host_ptr``."""
+    out = ctypes.c_void_p()
+    check(lib().mdx_host_device_address(host_ptr, ctypes.byref(out)), "mdx_host_device_address")
+    return int(out.value)
+
+
+def clear_flag(flag_address: int, stream: int) -> None:
+    """Set one int32 found-inf flag to 0 in stream order (a one-lane dispatch; works for device
+    memory and for pinned host memory at its device address)."""
+    check(lib().mdx_pack(None, 0, MDX_F32, MDX_F32, 1.0, 0, flag_address, stream), "mdx_pack (flag clear)")
 
 
 IPC_HANDLE_BYTES = 64

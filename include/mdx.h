@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 8
+#define MDX_ABI_VERSION 9
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -403,6 +403,14 @@ MDX_API int mdx_ipc_open(const mdx_ipc_handle* h, void** base);
 
 /* Unmaps a base mdx_ipc_open returned. */
 MDX_API int mdx_ipc_close(void* base);
+
+/* The address kernels use for pinned host memory at `host_ptr` (allocated with
+ * hipHostMalloc, e.g. torch's pin_memory), so that a kernel can store a
+ * found-inf flag straight into memory the host reads after a stream
+ * synchronisation, without a device-to-host copy.  No counterpart in the
+ * reference; it serves DistributedGradScaler.unscale_'s flag read
+ * (minidist/amp.py:219). */
+MDX_API int mdx_host_device_address(void* host_ptr, void** device_ptr);
 
 /* Static description of a status code. */
 MDX_API const char* mdx_strerror(int code);
