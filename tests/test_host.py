@@ -429,3 +429,67 @@ def test_host_grad_ptrs_helper_matches_python():
         _hostptrs.grad_ptrs([ps[0], 3])
     with pytest.raises(TypeError):
         _hostptrs.grad_ptrs(tuple(ps))
+
+
+def test_new_entry_points_check_arguments_before_any_launch():
+    """The multi-unit share, its plan, the allocation-free launch, the IPC calls and the host-flag
+    address refuse bad arguments with their MDX_E* codes before touching a device."""
+    L = nat.lib()
+    P = ctypes.c_void_p
+    pieces = nat.pieces_array([(4096, 0, 8), (0, 8, 8)])
+    outs = (ctypes.c_void_p * 2)(1 << 20, (1 << 20) + 32)
+    peers = (ctypes.c_void_p * 2)(1 << 24, 1 << 25)
+    args = (pieces.ctypes.data, outs, 2, peers)
+    assert L.mdx_reduce_scatter_share_multi(*args, 2, 0, 7, 0, 1, 0, 0, 1.0, None, None) == -2  # dtype
+    assert L.mdx_reduce_scatter_share_multi(*args, 2, 2, 0, 0, 1, 0, 0, 1.0, None, None) == -3  # rank
+    bad_outs = (ctypes.c_void_p * 2)(1 << 20, 0)
+    assert L.mdx_reduce_scatter_share_multi(pieces.ctypes.data, bad_outs, 2, peers, 2, 0, 0, 0, 1, 0, 0, 1.0, None,
+                                            None) == -1  # NULL destination
+    over_row = (ctypes.c_void_p * 2)(1 << 20, (1 << 25) + 8)
+    assert L.mdx_reduce_scatter_share_multi(pieces.ctypes.data, over_row, 2, peers, 2, 0, 0, 0, 1, 0, 0, 1.0, None,
+                                            None) == -4  # a destination over peer 1's row
+    over_each_other = (ctypes.c_void_p * 2)(1 << 20, (1 << 20) + 16)
+    assert L.mdx_reduce_scatter_share_multi(pieces.ctypes.data, over_each_other, 2, peers, 2, 0, 0, 0, 1, 0, 0, 1.0,
+                                            None, None) == -4
+    assert L.mdx_reduce_scatter_share_multi(None, None, 0, peers, 2, 0, 0, 0, 1, 0, 0, 1.0, None, None) == 0
+    size = ctypes.c_int64(0)
+    assert L.mdx_plan_reduce_scatter_share_multi(*args, 2, 0, 9, None, ctypes.byref(size)) == -2
+    assert L.mdx_plan_reduce_scatter_share_multi(*args, 2, 0, 1, None, ctypes.byref(size)) == nat.MDX_ESIZE
+    assert size.value > 0
+    assert L.mdx_reduce_scatter_share_multi_planned(None, None, 1, 0, 1.0, None, None) == -1
+    assert L.mdx_pack_allreduce_unpack_planned_noalloc(None, 1.0, None, None, None) == -1
+    junk = np.zeros(64, dtype=np.uint64)  # not a plan
+    assert L.mdx_pack_allreduce_unpack_planned_noalloc(junk.ctypes.data, 1.0, None, None, None) == -1
+    assert L.mdx_ipc_export(None, None) == -1
+    assert L.mdx_ipc_open(None, None) == -1
+    assert L.mdx_ipc_close(None) == -1
+    h = nat.IpcHandle()
+    h.alloc_bytes = 1 << 31  # a shared allocation of 2 GiB or more is refused
+    assert L.mdx_ipc_open(ctypes.byref(h), ctypes.byref(P())) == nat.MDX_ESIZE
+    assert L.mdx_host_device_address(None, ctypes.byref(P())) == -1
+    assert "256 KiB" in nat.strerror(nat.MDX_ESCRATCH)
+
+
+def test_cfg1_plan_fits_the_allocation_free_buffer():
+    """The fused plan of GPT-2-124M's 148 gradients in 18 buckets (the headline step) is well under
+    MDX_NOALLOC_SCRATCH_BYTES; the plan is built on the host from addresses alone."""
+    specs = w.gpt_specs(**w.GPT2_SMALL)
+    layout = o.build_buckets([s.nbytes for s in specs[::-1]], 25.0)
+    rows, off = [], 0
+    base = 1 << 40
+    rev = specs[::-1]
+    for idx in layout:
+        for i in idx:
+            n = rev[i].numel
+            rows.append((off, n, base + (1 << 36) + 4 * off, base + (1 << 37) + 4 * off))
+            off += n
+        off = (off + 63) // 64 * 64
+    runs = nat.pack_runs_array(rows)
+    reps = (ctypes.c_void_p * 8)(*[base + r * (1 << 31) for r in range(8)])
+    size = ctypes.c_int64(0)
+    rc = nat.lib().mdx_plan_pack_allreduce_unpack(reps, 8, 0, nat.MDX_F32, runs.ctypes.data, len(rows),
+                                                  ctypes.c_void_p(base + (1 << 38)), nat.MDX_F32, 0.125, None,
+                                                  ctypes.byref(size))
+    assert rc == nat.MDX_ESIZE
+    assert 8 * 1024 < size.value < nat.NOALLOC_SCRATCH_BYTES // 4
+    print(f"cfg1 fused plan: {size.value} bytes")
