@@ -27,7 +27,7 @@ import torch.distributed as dist
 import torch.multiprocessing as mp
 
 from conftest import first_mismatch, same_bits
-from minidist import DDP, DistributedGradScaler, IpcGroup
+from minidist import DDP, DistributedGradScaler, IpcGroup, comm
 from minidist import workloads as wl
 from oracle import gradpath as o
 
@@ -38,28 +38,39 @@ CFG = dict(n_layer=4, n_embd=256, vocab=1024, ctx=128)  # 52 gradients: one devi
 INF_AT = (1, 3, 17)  # (rank, parameter, element) that overflows in step 1
 
 
-def _grads(rank: int, specs) -> list[torch.Tensor]:
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _grads(rank: int, specs, dtype: torch.dtype = torch.float32) -> list[torch.Tensor]:
     g = torch.Generator().manual_seed(1234 + 7919 * rank)
-    return [torch.randn(s.numel, generator=g) * (1e-2 * SCALE) for s in specs]
+    return [(torch.randn(s.numel, generator=g) * (1e-2 * SCALE)).to(dtype) for s in specs]
 
 
-def _worker(rank: int, world: int, store: str, out_dir: str) -> None:
+def _host_bits(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().reshape(-1).cpu()
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
+    dtype = DTYPES[dtype_name]
     try:
         group = IpcGroup(dist.group.WORLD, dev)
-        specs = wl.gpt_specs(**CFG)
+        specs = wl.gpt_specs(**CFG, dtype=dtype)
         model = wl.SpecModule(specs, dev)
         params = list(model.parameters())
         scaler = DistributedGradScaler(init_scale=SCALE, process_group=group)
-        ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler)
+        # bf16 parameters: fp32 buckets, with the contributions travelling as bf16 (widening)
+        ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler,
+                  reduce_dtype=torch.float32 if dtype != torch.float32 else None)
 
         class _Opt:
             param_groups = [{"params": params}]
 
-        host = _grads(rank, specs)
+        host = _grads(rank, specs, dtype)
         out = {"buckets": np.array(len(ddp._buckets))}
         for step in range(2):
             for i, (p, g) in enumerate(zip(params, host, strict=True)):
@@ -74,37 +85,58 @@ def _worker(rank: int, world: int, store: str, out_dir: str) -> None:
             scaler.update()
             out[f"found_{step}"] = np.array(found)
             for i, p in enumerate(params):
-                out[f"grad_{step}_{i}"] = p.grad.detach().reshape(-1).cpu().numpy()
+                out[f"grad_{step}_{i}"] = _host_bits(p.grad)
+        if dtype == torch.float32:
+            # the reference's own per-bucket sequence over the same group: gather_into_buffer,
+            # comm.all_reduce (one-shot SUM of the rows into the bucket), scatter_from_buffer
+            for p, g in zip(params, host, strict=True):
+                p.grad = g.clone().to(dev).view(p.shape)
+            for b in ddp._buckets:
+                row = b.gather_into_buffer(1.0 / world)
+                comm.all_reduce(row, group=group)
+                b.scatter_from_buffer()
+            for i, p in enumerate(params):
+                out[f"grad_ref_{i}"] = _host_bits(p.grad)
         group.release()
         np.savez(os.path.join(out_dir, f"ipc_r{rank}.npz"), **out)
     finally:
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world", [2, 3, 4])
-def test_ipc_one_shot_all_reduce_bitwise(tmp_path, world):
+@pytest.mark.parametrize("world,dtype", [(2, "f32"), (3, "f32"), (4, "f32"), (2, "bf16"), (4, "bf16")])
+def test_ipc_one_shot_all_reduce_bitwise(tmp_path, world, dtype):
+    """fp32 gradients into fp32 buckets, or bf16 gradients into fp32 buckets with bf16 rows; in fp32
+    also the reference's per-bucket sequence through comm.all_reduce over the group."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (IpcGroup one-shot all-reduce)", flush=True)
-    mp.spawn(_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup one-shot all-reduce, {dtype})", flush=True)
+    mp.spawn(_worker, args=(world, store, str(tmp_path), dtype), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_r{r}.npz", allow_pickle=False) as d:
             res.append({k: d[k] for k in d.files})
-    specs = wl.gpt_specs(**CFG)
+    tdt = DTYPES[dtype]
+    odt = o.F32 if dtype == "f32" else o.BF16
+    specs = wl.gpt_specs(**CFG, dtype=tdt)
     numels = [s.numel for s in specs]
     n = len(specs)
     assert int(res[0]["buckets"]) > 2
     for step in range(2):
-        replica = [[g.numpy() for g in _grads(r, specs)] for r in range(world)]
+        replica = [[_host_bits(g) for g in _grads(r, specs, tdt)] for r in range(world)]
         if step == 1:
             rr, i, k = INF_AT
             replica[rr][i] = replica[rr][i].copy()
-            replica[rr][i][k] = np.inf
+            replica[rr][i][k] = np.inf if odt == o.F32 else np.uint16(0x7F80)
         for rank in range(world):
-            want = o.ddp_pipeline(replica, [o.F32] * n, numels, CAP_MB, rank, 1.0 / SCALE)
+            want = o.ddp_pipeline(replica, [odt] * n, numels, CAP_MB, rank, 1.0 / SCALE,
+                                  bucket_dtype=o.F32)
             assert bool(res[rank][f"found_{step}"]) == want["found_inf"] == (step == 1)
             for i in range(n):
                 got = res[rank][f"grad_{step}_{i}"]
                 assert same_bits(got, want["grads"][i]), (
                     f"step {step} rank {rank} param {i}: " + first_mismatch(got, want["grads"][i]))
+            if step == 0 and dtype == "f32":
+                for i in range(n):  # the reference's sequence: the unscaled average, not unscaled
+                    want_ref = o.ddp_pipeline(replica, [odt] * n, numels, CAP_MB, rank, None)["grads"][i]
+                    got = res[rank][f"grad_ref_{i}"]
+                    assert same_bits(got, want_ref), f"reference sequence rank {rank} param {i}"
     print("step ms per rank:", [[float(res[r][f"ms_{s}"]) for s in range(2)] for r in range(world)], flush=True)
