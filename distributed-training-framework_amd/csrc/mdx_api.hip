@@ -78,7 +78,7 @@ template <typename Emit>
 int for_each_span_run(const mdx_span* spans, int n_spans, int sdt, int ddt, bool in_place, Emit&& emit) {
   const int E = copy_frag_elems(sdt, ddt);
   const int ss = dtype_size(sdt), ds = dtype_size(ddt);
-  const int64_t VPB = int64_t(kBlock) * copy_unroll(E * ss);
+  const int64_t VPB = int64_t(kBlock) * copy_unroll_of(ss, ds);
   const int64_t EPB = VPB * E;
   for (int i = 0; i < n_spans; ++i) {
     const mdx_span& sp = spans[i];

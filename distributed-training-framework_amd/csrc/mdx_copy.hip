@@ -9,13 +9,19 @@
 // plain pack or unpack carries no dead arithmetic.
 //
 // Layout of the work: each span is cut into chunks of kBlock * U fragments
-// (a fragment = E elements = one or two 16-byte vectors).  Lane t of chunk c
-// handles fragments c*VPB + u*kBlock + t, so every vector instruction of a
-// wave touches 64 consecutive 16-byte vectors; all U fragments are loaded
-// (non-temporal: each byte is read once per step) before the first store,
-// and stored non-temporally (the next reader is a later pipeline stage).
-// A span whose src and dst cannot both be brought to 16-byte alignment by the
-// same element offset is processed with coalesced scalar accesses instead.
+// (a fragment = E elements = one 16-byte vector of the wider of the two
+// types, so 8 or 16 bytes of the other).  Lane t of chunk c handles
+// fragments c*VPB + u*kBlock + t, so every vector instruction of a wave
+// touches 64 consecutive fragments; all U fragments are loaded (non-temporal:
+// each byte is read once per step) before the first store, and stored
+// non-temporally (the next reader is a later pipeline stage).  The body
+// starts at the run's head, the element offset that 16-byte aligns the most
+// streams (the destination first); a stream it leaves unaligned still moves
+// in vectors.  The head before the body and the tail after it go one element
+// per lane, and a run shorter than its head plus one fragment goes entirely
+// that way.
+#include <type_traits>
+
 #include "mdx_internal.h"
 
 namespace mdx {
@@ -37,14 +43,19 @@ struct CopyOp {
 
 template <typename S, typename D, int SCALE, bool CHECK, typename View>
 __device__ __forceinline__ void copy_body(const View& tab, const CopyParams& p) {
-  constexpr int E = store_frag_elems(int(sizeof(D)));
-  constexpr int U = copy_unroll(E * int(sizeof(S)));
+  constexpr int E = copy_frag_elems_of(int(sizeof(S)), int(sizeof(D)));
+  constexpr int U = copy_unroll_of(int(sizeof(S)), int(sizeof(D)));
   constexpr int VPB = kBlock * U;
   constexpr int EPT = U * E;
   constexpr int EPB = kBlock * EPT;
 
   const int blk = tab.block();
-  const SpanRun run = tab.span_run(blk);
+  SpanRun run;
+  if constexpr (sizeof(S) > sizeof(D) && std::is_same_v<View, SpanArgView>) {
+    run = tab.span_run_wave(blk);
+  } else {
+    run = tab.span_run(blk);
+  }
   const int c = run.c;
   const int nblk = run.nblk;
   const S* src = static_cast<const S*>(run.src);
@@ -197,8 +208,7 @@ hipError_t launch_clear_flag(int32_t* flag, hipStream_t stream) {
 }
 
 int copy_frag_elems(int src_dtype, int dst_dtype) {
-  (void)src_dtype;
-  return store_frag_elems(dtype_size(dst_dtype));
+  return copy_frag_elems_of(dtype_size(src_dtype), dtype_size(dst_dtype));
 }
 
 hipError_t launch_copy(int src_dtype, int dst_dtype, const SpanBatch& b, const CopyParams& p,
