@@ -445,7 +445,13 @@ def ipc_open(h: IpcHandle) -> int:
 
 
 def ipc_close(ptr: int, h: IpcHandle) -> None:
-    check(lib().mdx_ipc_close(ptr - int(h.offset)), "mdx_ipc_close")
+    """Unmaps what :func:`ipc_open` mapped (``ptr`` is the pointer it returned)."""
+    ipc_close_base(ptr - int(h.offset))
+
+
+def ipc_close_base(base: int) -> None:
+    """Unmaps a peer allocation by its mapped base address."""
+    check(lib().mdx_ipc_close(base), "mdx_ipc_close")
 
 
 def pack_allreduce_unpack_planned_noalloc(

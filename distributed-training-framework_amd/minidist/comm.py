@@ -610,12 +610,12 @@ class ResidentGroup:
 
 
 class _IpcArena:
-    """One symmetric buffer of an :class:`IpcGroup`: this rank's row is an allocation of its
-    own; the peers' rows are their allocations, mapped into this process over IPC."""
+    """One symmetric buffer of an :class:`IpcGroup`: this rank's row is a tensor of its own;
+    the peers' rows are inside their allocations, mapped into this process over IPC."""
 
-    __slots__ = ("own", "numel", "dtype", "esize", "own_base", "row_ptrs", "target", "handles")
+    __slots__ = ("own", "numel", "dtype", "esize", "own_base", "row_ptrs", "target")
 
-    def __init__(self, own: torch.Tensor, numel: int, row_ptrs: list[int], handles: list):
+    def __init__(self, own: torch.Tensor, numel: int, row_ptrs: list[int]):
         self.own = own
         self.numel = numel
         self.dtype = own.dtype
@@ -623,7 +623,6 @@ class _IpcArena:
         self.own_base = own.data_ptr()
         self.row_ptrs = row_ptrs
         self.target: torch.Tensor | None = None
-        self.handles = handles  # (mapped pointer, handle) of each peer row, None for this rank's
 
     def offset_of(self, t: torch.Tensor) -> int | None:
         p = t.data_ptr()
@@ -661,6 +660,10 @@ class IpcGroup(ResidentGroup):
     def __init__(self, process_group=None, device: torch.device | str | None = None):
         self.process_group = process_group
         self._released = False
+        # A peer's allocation mapped into this process, by (rank, handle bytes): the
+        # caching allocator may carve two small rows out of one allocation, whose
+        # exports then name the same memory; it is mapped once and unmapped once.
+        self._mapped: dict[tuple[int, bytes], int] = {}
         super().__init__(dist.get_world_size(process_group), dist.get_rank(process_group), device)
 
     def __repr__(self) -> str:
@@ -684,19 +687,21 @@ class IpcGroup(ResidentGroup):
         # every kernel reads all W rows over this rank's extent: the rows must agree
         if any((n, d) != (row_elems, str(dtype)) for _, n, d in raw):
             raise RuntimeError(f"IpcGroup.zeros: the ranks asked for different buffers {[(n, d) for _, n, d in raw]}")
-        row_ptrs, handles = [], []
+        row_ptrs = []
         for r in range(self._world):
             if r == self._rank:
                 row_ptrs.append(own.data_ptr())
-                handles.append(None)
                 continue
             h = _native.IpcHandle.from_bytes(raw[r][0])
             if h.offset + row_elems * esize > h.alloc_bytes:
                 raise RuntimeError(f"IpcGroup.zeros: rank {r}'s row is not inside the allocation it exported")
-            ptr = _native.ipc_open(h)
-            row_ptrs.append(ptr)
-            handles.append((ptr, h))
-        arena = _IpcArena(own, numel, row_ptrs, handles)
+            key = (r, bytes(h.bytes))
+            base = self._mapped.get(key)
+            if base is None:
+                base = _native.ipc_open(h) - int(h.offset)
+                self._mapped[key] = base
+            row_ptrs.append(base + int(h.offset))
+        arena = _IpcArena(own, numel, row_ptrs)
         self._arenas.append(arena)
         return own[:numel]
 
@@ -707,10 +712,9 @@ class IpcGroup(ResidentGroup):
         """Unmap every peer row (collective: no rank still reads a row when it is released)."""
         torch.cuda.current_stream(self.device).synchronize()
         dist.barrier(group=self.process_group)
-        for arena in self._arenas:
-            for entry in arena.handles:
-                if entry is not None:
-                    _native.ipc_close(*entry)
+        for base in self._mapped.values():
+            _native.ipc_close_base(base)
+        self._mapped.clear()
         self._arenas.clear()
         # plans built over this group still hold the peers' (now unmapped) addresses
         self._released = True
@@ -736,7 +740,26 @@ class IpcGroup(ResidentGroup):
         return _CompletedWork() if async_op else None
 
     def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
-        return self._one_shot(lambda: ResidentGroup.all_reduce_sum(self, tensors), async_op)
+        """SUM over the W ranks' rows, rank order 0..W-1, into the buffer's reduce target.
+
+        Without a target the sum replaces the rows' contents, as the reference's
+        in-place ``dist.all_reduce`` does; over IPC a rank's row is still read by
+        its peers while its own reduction runs, so the sums go to a private
+        buffer first and are copied into the rows once every rank has read them."""
+        arenas = {id(a): a for a in (self._locate(t)[0] for t in tensors)}
+        staged = [a for a in arenas.values() if a.target is None]
+        for arena in staged:
+            arena.target = torch.empty_like(arena.own)
+        try:
+            work = self._one_shot(lambda: ResidentGroup.all_reduce_sum(self, tensors), async_op)
+            for t in tensors:
+                arena, off = self._locate(t)
+                if arena in staged:
+                    t.copy_(arena.target[off : off + t.numel()].view(t.shape))
+        finally:
+            for arena in staged:
+                arena.target = None
+        return work
 
     def all_reduce_unpack(self, buffer, runs, grad_dtype, inv_scale=1.0, found_inf=None, async_op=False,
                           bucket=None):

@@ -140,3 +140,54 @@ def test_ipc_one_shot_all_reduce_bitwise(tmp_path, world, dtype):
                     got = res[rank][f"grad_ref_{i}"]
                     assert same_bits(got, want_ref), f"reference sequence rank {rank} param {i}"
     print("step ms per rank:", [[float(res[r][f"ms_{s}"]) for s in range(2)] for r in range(world)], flush=True)
+
+
+SMALL = (1000, 3000)  # two small symmetric buffers: the caching allocator may carve both out of one segment
+
+
+def _small_rows(rank: int, step: int) -> list[np.ndarray]:
+    g = np.random.default_rng(77 + 1009 * rank + 31 * step)
+    return [(g.standard_normal(n) * 1e3).astype(np.float32) for n in SMALL]
+
+
+def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        group = IpcGroup(dist.group.WORLD, dev)
+        rows = [group.zeros(n, torch.float32) for n in SMALL]
+        out = {"mapped": np.array(len(group._mapped))}
+        for step in range(2):
+            for row, host in zip(rows, _small_rows(rank, step), strict=True):
+                row.copy_(torch.from_numpy(host).to(dev))
+            comm.all_reduce(rows[0], group=group)  # in place, one buffer
+            comm.all_reduce_coalesced([rows[1][:1500], rows[1][1500:]], group=group)  # two views of the other
+            for k, row in enumerate(rows):
+                out[f"sum_{step}_{k}"] = row.cpu().numpy()
+        group.release()
+        np.savez(os.path.join(out_dir, f"inplace_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("world", [2, 3])
+def test_ipc_in_place_all_reduce(tmp_path, world):
+    """``comm.all_reduce`` in place on rows of an IpcGroup buffer with no reduce target: every rank
+    ends with the rank-ordered sum while its peers read its row concurrently; a peer allocation
+    that holds two rows is mapped once."""
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup in-place all-reduce)", flush=True)
+    mp.spawn(_in_place_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    for step in range(2):
+        hosts = [_small_rows(r, step) for r in range(world)]
+        for k in range(len(SMALL)):
+            want = hosts[0][k].copy()
+            for r in range(1, world):
+                want = want + hosts[r][k]  # float32, rank order 0..W-1
+            for rank in range(world):
+                with np.load(tmp_path / f"inplace_r{rank}.npz", allow_pickle=False) as d:
+                    got = d[f"sum_{step}_{k}"]
+                    assert int(d["mapped"]) <= len(SMALL) * (world - 1)
+                assert same_bits(got, want), f"step {step} buffer {k} rank {rank}: " + first_mismatch(got, want)
