@@ -437,6 +437,19 @@ def test_no_sync_accumulation_then_sync():
         assert rel <= 2e-5
 
 
+def test_non_contiguous_gradient_is_rejected():
+    """The pack kernels read each gradient as one flat span: a strided gradient is refused with an
+    error before anything is launched."""
+    model = Flat([(64, 32), (32,)])
+    ddp = DDP(model, process_group=ResidentGroup(2, 0, DEV))
+    w, b = list(model.parameters())
+    w.grad = torch.zeros(32, 64, device=DEV).t()
+    b.grad = torch.zeros(32, device=DEV)
+    assert not w.grad.is_contiguous()
+    with pytest.raises(RuntimeError, match="not a dense"):
+        ddp.finish_gradient_sync()
+
+
 def test_bucket_layout_matches_reference_invariants():
     c = tiny_gpt.Config()
     ddp = DDP(tiny_gpt.GPT(c).to(DEV), process_group=ResidentGroup(2, 0, DEV), bucket_cap_mb=0.05)

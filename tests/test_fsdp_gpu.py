@@ -176,6 +176,25 @@ def test_no_sync_accumulates_then_flushes(comm_streams):
         assert rel <= 2e-5
 
 
+def test_non_contiguous_gradient_is_rejected():
+    """The shard kernels read each full-size gradient as one flat span: a strided gradient is refused
+    with an error before anything is launched, and the unit's gradients are left as they were."""
+    c = tiny_gpt.Config(n_layer=1)
+    fsdp = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(2, 0, DEV))
+    unit = next(u for u in fsdp._units if any(p.dim() == 2 for p in u.params))
+    unit.unshard()
+    for p in unit.params:
+        if p.dim() == 2:
+            p.grad = torch.zeros(p.shape[::-1], dtype=p.dtype, device=DEV).t()  # right shape, transposed strides
+            assert not p.grad.is_contiguous()
+        else:
+            p.grad = torch.zeros_like(p)
+    with pytest.raises(RuntimeError, match="not contiguous"):
+        unit.reduce_scatter_grads()
+    assert all(p.grad is not None for p in unit.params)
+    assert unit.flat_shard.grad is None
+
+
 def test_second_backward_accumulates_into_shard_grad():
     c = tiny_gpt.Config()
     W, rank = 2, 0
