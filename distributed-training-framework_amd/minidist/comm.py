@@ -845,6 +845,18 @@ def dist_broadcast(tensor: torch.Tensor, src: int, group=None, async_op: bool = 
     return dist.broadcast(tensor, src=src, group=group, async_op=async_op)
 
 
+def broadcast_module_state(module: torch.nn.Module, group=None, src: int = 0, buffer_filter=None) -> None:
+    """A wrapper's construction-time sync: every parameter, then every buffer that
+    ``buffer_filter`` accepts (all of them when it is None), from rank ``src`` of ``group``
+    (of the default group: always rank 0).  ``dist.broadcast`` takes the source's global
+    rank, so a group rank is translated first."""
+    root = 0 if group is None else dist.get_global_rank(group, src)
+    buffers = [b for b in module.buffers() if buffer_filter is None or buffer_filter(b)]
+    with torch.no_grad():
+        for t in (*module.parameters(), *buffers):
+            dist_broadcast(t.data, src=root, group=group)
+
+
 def dist_all_gather_into_tensor(output: torch.Tensor, input_: torch.Tensor, group=None, async_op: bool = False):
     if _via_host(output, group):
         host_out = torch.empty(output.shape, dtype=output.dtype)

@@ -256,6 +256,23 @@ def test_ddp_layout_matches_oracle_at_real_shapes(cfg, W, cap):
     assert ddp.world_size == W
 
 
+def test_bucket_spans_are_the_oracle_partition():
+    """DDP's partition (index ranges over the reversed parameters) against the oracle's restatement
+    of ddp.py:175-190, over every list of up to 5 sizes from a small alphabet and several caps."""
+    import itertools
+
+    from minidist.ddp import bucket_spans
+
+    for k in range(6):
+        for sizes in itertools.product((0, 1, 3, 4, 9), repeat=k):
+            for cap_mb in (0.0, 2 / 2**20, 4 / 2**20, 9 / 2**20, 1.0):
+                nbytes = list(sizes)
+                want = o.build_buckets(nbytes, cap_mb)
+                n = len(nbytes)
+                spans = bucket_spans(nbytes[::-1], int(cap_mb * 1024 * 1024))
+                assert [[n - 1 - j for j in range(a, b)] for a, b in spans] == want, (sizes, cap_mb)
+
+
 def test_out_of_scope_names_say_so():
     import minidist
 
