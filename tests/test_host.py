@@ -385,6 +385,74 @@ def test_plan_run_hints_resolve_every_workgroup(seed):
     assert np.array_equal(got, brute)
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_plan_builders_on_random_tables(seed):
+    """Every plan builder on random tables (fake device addresses, aligned or not, runs from empty to
+    past the 2^26-element run limit, bad dtypes and worlds): each call returns a documented code; a
+    size query followed by a build into exactly that many bytes succeeds, and one 8 bytes short is
+    refused with MDX_ESIZE.  (The same tables also ran against a build with the host code under
+    AddressSanitizer and UndefinedBehaviorSanitizer, clean.)"""
+    import random
+
+    L = nat.lib()
+    rng = random.Random(seed)
+    codes = {0, -2, -3, -4, -5}
+    base = 1 << 40
+
+    def ptr(aligned=True):
+        return base + rng.randrange(1 << 30) * 256 + (0 if aligned else rng.choice([2, 4, 8, 12]))
+
+    def numel():
+        return rng.choice([0, 1, 63, 64, 4096, 100_003, (1 << 26) - 1, (1 << 26) + 5])
+
+    def dt():
+        return rng.choice([0, 1, 2, 0, 1, 2, 7])
+
+    def check(fn, *args):
+        size = ctypes.c_int64(0)
+        rc = fn(*args, None, ctypes.byref(size))
+        assert rc in codes, rc
+        if rc != nat.MDX_ESIZE:
+            return
+        buf = np.zeros((size.value + 7) // 8 + 1, dtype=np.uint64)
+        short = ctypes.c_int64(size.value - 8)
+        assert fn(*args, buf.ctypes.data, ctypes.byref(short)) == nat.MDX_ESIZE
+        exact = ctypes.c_int64(size.value)
+        assert fn(*args, buf.ctypes.data, ctypes.byref(exact)) == 0
+
+    for _ in range(400):
+        kind = rng.randrange(4)
+        k = rng.randrange(0, 60)
+        if kind == 0:
+            spans = np.array([(ptr(rng.random() > 0.2), ptr(rng.random() > 0.2), numel()) for _ in range(k)],
+                             dtype=nat.SPAN_DTYPE)
+            check(L.mdx_plan_spans, nat._ptr(spans), k, dt(), dt())
+            continue
+        if kind == 3:
+            W = rng.choice([1, 2, 4, 8, 16])
+            pieces = np.array([(ptr() if rng.random() > 0.1 else 0, rng.randrange(1 << 20) * 8,
+                                rng.choice([0, 1, 5000, 1 << 20])) for _ in range(k)], dtype=nat.PIECE_DTYPE)
+            outs = nat._ptrs([ptr() for _ in range(k)]) if k else None
+            check(L.mdx_plan_reduce_scatter_share_multi, nat._ptr(pieces), outs, k,
+                  nat._ptrs([ptr() for _ in range(W)]), W, rng.randrange(W), dt())
+            continue
+        W = rng.choice([0, 1, 2, 3, 8, 16, 17])
+        reps = nat._ptrs([ptr() for _ in range(max(W, 1))])
+        off, rows = 0, []
+        for _ in range(k):
+            m = numel() if rng.random() < 0.3 else rng.randrange(5000)
+            rows.append((off, m, ptr(rng.random() > 0.2)))
+            off += m + rng.choice([0, 128])
+        out = ptr() if rng.random() < 0.7 else None
+        if kind == 1:
+            runs = np.array(rows, dtype=nat.GRAD_RUN_DTYPE)
+            check(L.mdx_plan_allreduce_unpack, reps, W, dt(), nat._ptr(runs), k, out, dt())
+        else:
+            runs = np.array([(a, m, ptr(rng.random() > 0.2), g) for a, m, g in rows], dtype=nat.PACK_RUN_DTYPE)
+            check(L.mdx_plan_pack_allreduce_unpack, reps, W, rng.randrange(max(W, 1)), dt(), nat._ptr(runs), k,
+                  out, dt(), ctypes.c_float(0.125))
+
+
 def test_plan_allreduce_unpack_builds_and_rejects_overlap():
     L = nat.lib()
     reps = (ctypes.c_void_p * 8)(*[0x100000000 + r * (1 << 24) for r in range(8)])
