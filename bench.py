@@ -506,7 +506,12 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     * ``per-unit``: per unit its cast and its share, as the forward and
       backward hooks issue them, on the caller's stream;
     * ``per-unit-streams``: the same with ``comm_streams=True`` (casts on the
-      gather stream, shares on the reduce stream).
+      gather stream, shares on the reduce stream);
+    * ``unit-batch``: as the hooks issue it with ``unit_batch=K``
+      (``--unit-batch``, default 8): the forward gathers K units per batched
+      unshard (cast dispatch), the backward holds reduce-scatters until K
+      units are ready and sends them as one multi-unit share, last units
+      first.
 
     The per-kernel times of the roofline come from a separate pass with the
     step's dispatches on one stream and HIP events around each."""
@@ -540,6 +545,7 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     pdt = getattr(torch, TORCH_DTYPE_NAMES[param_dtype_name])
     policy = MixedPrecisionPolicy(param_dtype=pdt, reduce_dtype=torch.float32)
     mode = args.fsdp_mode
+    K = args.unit_batch
     streams = mode == "per-unit-streams"
     # reshard_after_forward=False: the gather buffers stay allocated (the step re-casts into them),
     # and finish_gradient_sync's flush does not free them
@@ -557,33 +563,44 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                           for p in u.params])
     S = units[0].shard_numel
 
-    def step(events=None):
-        if mode == "batched":
-            if events is not None:
-                events[0][0].record()
-            fsdp._cast_own_slots(units)
-            if events is not None:
-                events[0][1].record()
-            for i, u in enumerate(units):
-                u.flat_shard.grad = None  # the shard gradient is set, not accumulated
-                for p, g in zip(u.params, own_grads[i], strict=True):
-                    p.grad = g
-            fsdp.finish_gradient_sync()  # every unit holds gradients: one multi-unit share
-            if events is not None:
-                events[0][2].record()
+    def timed(events, kind, work):
+        """``work()``, between two events appended to ``events[kind]`` when events are taken."""
+        if events is None:
+            work()
             return
-        for i, u in enumerate(units):
-            if events is not None:
-                events[i][0].record()
-            u._cast_into_own_slot()
-            if events is not None:
-                events[i][1].record()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        work()
+        e1.record()
+        events[kind].append((e0, e1))
+
+    def give_grads(group):
+        for u in group:
+            i = units.index(u)
             u.flat_shard.grad = None  # the shard gradient is set, not accumulated
             for p, g in zip(u.params, own_grads[i], strict=True):
                 p.grad = g
-            u.reduce_scatter_grads()
-            if events is not None:
-                events[i][2].record()
+
+    def step(events=None):
+        if mode == "batched":
+            timed(events, "cast", lambda: fsdp._cast_own_slots(units))
+            give_grads(units)
+            # every unit holds gradients: one multi-unit share
+            timed(events, "share", fsdp.finish_gradient_sync)
+            return
+        if mode == "unit-batch":
+            for g0 in range(0, n_units, K):  # forward: K units per batched unshard
+                timed(events, "cast", lambda g0=g0: fsdp._cast_own_slots(units[g0 : g0 + K]))
+            for g1 in range(n_units, 0, -K):  # backward: K held reduce-scatters at a time, last units first
+                group = units[max(0, g1 - K) : g1][::-1]
+                give_grads(group)
+                fsdp._held_reductions = list(group)
+                timed(events, "share", fsdp._reduce_held)
+            return
+        for u in units:
+            timed(events, "cast", u._cast_into_own_slot)
+            give_grads([u])
+            timed(events, "share", u.reduce_scatter_grads)
         fsdp.finish_gradient_sync()  # with side streams: the caller's stream joins both
 
     def one_stream(on: bool) -> None:
@@ -616,16 +633,16 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     # Kernel pass: the same steps on one stream with events around every dispatch.
     cast_ms, share_ms = [], []
     one_stream(True)
-    n_ev = 1 if mode == "batched" else len(units)
     for _ in range(min(steps, 5)):
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_ev)]
+        ev = {"cast": [], "share": []}
         torch.cuda._sleep(hold_cycles)
         step(ev)
         torch.cuda.synchronize()
-        cast_ms += [e[0].elapsed_time(e[1]) for e in ev]
-        share_ms += [e[1].elapsed_time(e[2]) for e in ev]
+        cast_ms += [e0.elapsed_time(e1) for e0, e1 in ev["cast"]]
+        share_ms += [e0.elapsed_time(e1) for e0, e1 in ev["share"]]
     one_stream(False)
-    per_launch = n_units if mode == "batched" else 1  # units one timed launch covers
+    # units one timed launch covers (unit-batch: the mean over its groups)
+    per_launch = {"batched": n_units, "unit-batch": n_units / -(-n_units // K)}.get(mode, 1)
     ms_per_step = sorted(per_step)[len(per_step) // 2]
     alg_bytes = n_units * 26 * S  # cast 6S (fp32 read, bf16 write) + share 20S (8 bf16 reads, fp32 write)
     value = alg_bytes / (ms_per_step * 1e-3) / 1e9
@@ -652,6 +669,8 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                         "the reduce-scatter share ("
                         + ("mdx_pack over the 48 units' master shards + mdx_reduce_scatter_share_multi_planned"
                            if mode == "batched" else
+                           f"mdx_pack over {K} units' master shards + mdx_reduce_scatter_share_multi over {K} units"
+                           if mode == "unit-batch" else
                            ("mdx_cast_f32_bf16" if param_dtype_name == "bf16" else "mdx_pack, fp32 -> fp16")
                            + " + mdx_reduce_scatter_share per unit")
                         + "); GPU time of the step's dispatches",
@@ -659,7 +678,9 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                                  "(finish_gradient_sync's flush)",
                       "per-unit": "per unit a cast and a share dispatch (the hooks' order), one stream",
                       "per-unit-streams": "per unit a cast on the gather stream and a share on the reduce stream "
-                                          "(comm_streams=True)"}[mode],
+                                          "(comm_streams=True)",
+                      "unit-batch": f"unit_batch={K}: a cast dispatch per {K} units in forward order, a multi-unit "
+                                    f"share per {K} units in backward order"}[mode],
             "ms_per_step_stat": f"median of {steps} steps",
             "world": W,
             "units": n_units,
@@ -675,13 +696,16 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
             "kernel": (f"share_kernel_dev<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
                        "(mdx_reduce_scatter_share_multi_planned: 48 units' shares, ~150 pieces, one dispatch)")
                       if mode == "batched" else
+                      (f"share_kernel<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
+                       f"(mdx_reduce_scatter_share_multi: {K} units' shares, {3 * K} pieces, one dispatch)")
+                      if mode == "unit-batch" else
                       (f"share_kernel_few<{KERNEL_TYPE_NAMES[param_dtype_name]}, float, float, 8> "
                        "(mdx_reduce_scatter_share; rank 0's shard is 3 parameter pieces)"),
             "achieved": round(share_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(share_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(name, mode == "batched"),
+            "traffic": (measured_traffic(name, mode == "batched") if mode != "unit-batch" else None),
             "bytes_per_launch": 20 * S * per_launch,
             "avg_launch_ms": round(share_avg, 5),
         },
@@ -863,7 +887,10 @@ def main() -> int:
                          "unscale_ runs its own pass over the gradients")
     ap.add_argument("--misaligned", action="store_true",
                     help="DDP workloads: every gradient a view one element into its allocation")
-    ap.add_argument("--fsdp-mode", default="batched", choices=["batched", "per-unit", "per-unit-streams"],
+    ap.add_argument("--unit-batch", type=int, default=8,
+                    help="cfg3 --fsdp-mode unit-batch: units per batched gather and per multi-unit share")
+    ap.add_argument("--fsdp-mode", default="batched",
+                    choices=["batched", "per-unit", "per-unit-streams", "unit-batch"],
                     help="cfg3: how the units' casts and shares are issued (see bench_fsdp)")
     ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument(

@@ -61,8 +61,11 @@ def _capture(store):
 @pytest.mark.parametrize("W", [2, 4, 3])
 @pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("comm_streams", [False, True])
-def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams):
-    """With ``comm_streams`` the gathers and reduce-scatters run on side streams: the same bits."""
+@pytest.mark.parametrize("unit_batch", [1, 2, 8])
+def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams, unit_batch):
+    """With ``comm_streams`` the gathers and reduce-scatters run on side streams, and with
+    ``unit_batch`` they go out for several units at once (2: the 4 units in pairs; 8: every unit's
+    reduce-scatter held to the end of backward): the same bits."""
     c = tiny_gpt.Config(n_layer=3)
     ids, tgt = tiny_gpt.batch(c, 12 if W == 3 else 8, seed=1234)
     rank = W - 1
@@ -73,7 +76,7 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams):
         p.register_post_accumulate_grad_hook(_capture(captured))
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
     fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
-                comm_streams=comm_streams)
+                comm_streams=comm_streams, unit_batch=unit_batch)
     # peers' gradients are computed by replicas whose parameters are the gathered (param_dtype) values
     replica = []
     for r in range(W):
@@ -150,8 +153,8 @@ def test_sharding_is_real_and_unit_count():
         assert s["fsdp_state_MB"] < s["ddp_state_MB"]
 
 
-@pytest.mark.parametrize("comm_streams", [False, True])
-def test_no_sync_accumulates_then_flushes(comm_streams):
+@pytest.mark.parametrize("comm_streams,unit_batch", [(False, 1), (True, 1), (False, 3), (True, 3)])
+def test_no_sync_accumulates_then_flushes(comm_streams, unit_batch):
     """Reference tests/test_fsdp.py:214-238 on one GPU (world emulated, peers zero)."""
     c = tiny_gpt.Config()
     W, rank = 2, 1
@@ -159,13 +162,13 @@ def test_no_sync_accumulates_then_flushes(comm_streams):
     my_ids, my_tgt = ids.chunk(W)[rank].to(DEV), tgt.chunk(W)[rank].to(DEV)
 
     single = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV),
-                  comm_streams=comm_streams)
+                  comm_streams=comm_streams, unit_batch=unit_batch)
     _, loss = single(my_ids, my_tgt)
     loss.backward()
     expected = [p.grad.clone() for p in single.parameters()]
 
     accum = FSDP(tiny_gpt.GPT(c).to(DEV), unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV),
-                 comm_streams=comm_streams)
+                 comm_streams=comm_streams, unit_batch=unit_batch)
     with accum.no_sync():
         for h_ids, h_tgt in zip(my_ids.chunk(2), my_tgt.chunk(2), strict=True):
             _, l = accum(h_ids, h_tgt)
@@ -212,7 +215,7 @@ def test_second_backward_accumulates_into_shard_grad():
         assert rel <= 1e-6
 
 
-def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1, comm_streams=False):
+def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1, comm_streams=False, unit_batch=1):
     """FSDP on rank ``rank`` of a ResidentGroup next to a full-batch reference, both SGD.
 
     Every step the emulated peers get what they would hold: their shard of the
@@ -225,7 +228,7 @@ def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1, comm_streams=False):
     names_by_id = {id(p): n for n, p in model.named_parameters()}
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
     fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
-                comm_streams=comm_streams)
+                comm_streams=comm_streams, unit_batch=unit_batch)
     opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
     opt_ref = torch.optim.SGD(ref.parameters(), lr=lr)
     out = []
@@ -264,12 +267,14 @@ def _sgd_run(W, rank, param_dtype, steps=4, lr=0.1, comm_streams=False):
     return fsdp, ref, names_by_id, out
 
 
-@pytest.mark.parametrize("W,rank,comm_streams", [(2, 1, False), (4, 2, False), (4, 2, True)])
-def test_sgd_steps_track_full_batch(W, rank, comm_streams):
+@pytest.mark.parametrize("W,rank,comm_streams,unit_batch",
+                         [(2, 1, False, 1), (4, 2, False, 1), (4, 2, True, 1), (4, 2, False, 2), (4, 1, True, 3)])
+def test_sgd_steps_track_full_batch(W, rank, comm_streams, unit_batch):
     """Reference tests/test_fsdp.py:92-127: after 4 SGD steps this rank's shard equals its slice of
     the full-batch model's weights (the reference compares with DDP; both equal the full batch).
-    With ``comm_streams`` the optimizer must see the side streams' shard gradients."""
-    fsdp, ref, names_by_id, _ = _sgd_run(W, rank, torch.float32, comm_streams=comm_streams)
+    With ``comm_streams`` the optimizer must see the side streams' shard gradients, and with
+    ``unit_batch`` the reduce-scatters held to the end of backward."""
+    fsdp, ref, names_by_id, _ = _sgd_run(W, rank, torch.float32, comm_streams=comm_streams, unit_batch=unit_batch)
     final = {n: p.detach() for n, p in ref.named_parameters()}
     for unit in fsdp._units:
         flat = torch.cat([final[names_by_id[id(p)]].reshape(-1) for p in unit.params])
