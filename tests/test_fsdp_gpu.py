@@ -66,6 +66,19 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams, u
     """With ``comm_streams`` the gathers and reduce-scatters run on side streams, and with
     ``unit_batch`` they go out for several units at once (2: the 4 units in pairs; 8: every unit's
     reduce-scatter held to the end of backward): the same bits."""
+    _check_shard_grads(W, param_dtype, comm_streams, unit_batch, reshard_after_forward=True)
+
+
+@pytest.mark.parametrize("W,param_dtype,comm_streams,unit_batch",
+                         [(2, torch.float32, False, 1), (4, torch.bfloat16, False, 2), (3, torch.float32, True, 3),
+                          (4, torch.float16, True, 8)])
+def test_shard_grads_without_reshard_after_forward(W, param_dtype, comm_streams, unit_batch):
+    """``reshard_after_forward=False``: the units stay gathered from forward to backward (no backward
+    gathers), and are freed after their reduce-scatter as with the default: the same bits."""
+    _check_shard_grads(W, param_dtype, comm_streams, unit_batch, reshard_after_forward=False)
+
+
+def _check_shard_grads(W, param_dtype, comm_streams, unit_batch, reshard_after_forward):
     c = tiny_gpt.Config(n_layer=3)
     ids, tgt = tiny_gpt.batch(c, 12 if W == 3 else 8, seed=1234)
     rank = W - 1
@@ -76,7 +89,7 @@ def test_shard_grads_match_oracle_and_full_batch(W, param_dtype, comm_streams, u
         p.register_post_accumulate_grad_hook(_capture(captured))
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
     fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
-                comm_streams=comm_streams, unit_batch=unit_batch)
+                comm_streams=comm_streams, unit_batch=unit_batch, reshard_after_forward=reshard_after_forward)
     # peers' gradients are computed by replicas whose parameters are the gathered (param_dtype) values
     replica = []
     for r in range(W):
