@@ -390,6 +390,72 @@ def test_cfg3_fsdp_gpt2_xl_block_unit(rank):
     assert same_bits(got2, want2), first_mismatch(got2, want2)
 
 
+class _XLStack(torch.nn.Module):
+    def __init__(self, specs, n_blocks, seed):
+        super().__init__()
+        self.blocks = torch.nn.ModuleList([_Block(specs) for _ in range(n_blocks)])
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, device=DEV, generator=g) * 0.02)
+
+
+def test_cfg3_all_48_units_batched_full_size():
+    """cfg3 as the bench issues it: the 48 units' gather casts in one dispatch and their reduce-scatter
+    shares in one multi-unit dispatch (144 pieces, a device plan), at full size (23.6 GB of peer
+    contributions).  Every unit's slot against the oracle's RNE cast, every unit's shard gradient
+    against the per-unit reduce_scatter_grads of the same inputs, and three units' against the oracle."""
+    specs = wl.gpt_block_specs(0, wl.GPT2_XL["n_embd"])
+    W, rank, n = 8, 5, wl.GPT2_XL["n_layer"]
+    m = _XLStack(specs, n, seed=78)
+    masters = [torch.cat([p.detach().reshape(-1) for p in b.parameters()]) for b in m.blocks]
+    policy = MixedPrecisionPolicy(param_dtype=torch.bfloat16, reduce_dtype=torch.float32)
+    f = FSDP(m, unit_types=(_Block,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
+             reshard_after_forward=False)
+    units = f._units
+    assert len(units) == n
+    S, P = units[0].shard_numel, units[0].padded_numel
+    for u in units:
+        u.unshard()
+    f._cast_own_slots(units)
+    for k, u in enumerate(units):
+        want = o.fsdp_gather_cast(bits(masters[k][rank * S : (rank + 1) * S]), o.BF16)
+        got = bits(u._full[rank * S : (rank + 1) * S])
+        assert same_bits(got, want), f"unit {k}: " + first_mismatch(got, want)
+    gen = torch.Generator(device=DEV).manual_seed(200)
+    own = []
+    for u in units:
+        peers = u.peer_grad_contributions()
+        for r in range(W):
+            if r != rank:
+                peers[r].copy_((torch.randn(P, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16))
+        own.append((torch.randn(P, device=DEV, generator=gen) * 1e-3).to(torch.bfloat16))
+
+    def give(u, k):
+        off = 0
+        for p in u.params:
+            p.grad = own[k][off : off + p.numel()].view(p.shape).clone()
+            off += p.numel()
+
+    for k, u in enumerate(units):
+        give(u, k)
+    f.finish_gradient_sync()  # every unit holds gradients: one multi-unit share
+    batched = [u.flat_shard.grad.clone() for u in units]
+    assert all(p.grad is None for u in units for p in u.params)
+    for k, u in enumerate(units):
+        u.flat_shard.grad = None
+        give(u, k)
+        u.reduce_scatter_grads()
+        assert torch.equal(batched[k].view(torch.int32), u.flat_shard.grad.view(torch.int32)), f"unit {k}"
+    lo = rank * S
+    for k in (0, 23, 47):
+        peers = units[k].peer_grad_contributions()
+        slices = [bits(own[k][lo : lo + S]) if r == rank else bits(peers[r, lo : lo + S]) for r in range(W)]
+        want = o.allreduce_sum([o.div_scalar(o.convert(x, o.BF16, o.F32), o.F32, W) for x in slices], o.F32)
+        got = bits(batched[k])
+        assert same_bits(got, want), f"unit {k}: " + first_mismatch(got, want)
+
+
 # ---------------------------------------------------------------------------
 # cfg4: Llama-7B bf16 grads randn * 1e-3 * 2^12, W = 8 (~108 GB of contributions), fp32 buckets
 # ---------------------------------------------------------------------------
