@@ -274,13 +274,12 @@ def test_bucket_spans_are_the_oracle_partition():
 
 
 def test_fsdp_unit_batch_is_checked():
-    """unit_batch must be a positive int, and above 1 needs a ResidentGroup (rejected before any work)."""
+    """unit_batch must be a positive int (rejected before any work)."""
     from minidist import FSDP
 
-    with pytest.raises(ValueError, match="positive int"):
-        FSDP(nn.Linear(2, 2), unit_batch=0)
-    with pytest.raises(ValueError, match="ResidentGroup"):
-        FSDP(nn.Linear(2, 2), unit_batch=2)
+    for bad in (0, -1, 2.0):
+        with pytest.raises(ValueError, match="positive int"):
+            FSDP(nn.Linear(2, 2), unit_batch=bad)
 
 
 def test_out_of_scope_names_say_so():

@@ -61,7 +61,7 @@ def _worker(rank: int, kind: str, store: str, out_dir: str) -> None:
         elif kind == "fsdp-vs-ddp":
             _fsdp_vs_ddp_rank(rank, out_dir)
         else:
-            _fsdp_rank(rank, DTYPES[kind.split("-")[1]], out_dir)
+            _fsdp_rank(rank, DTYPES[kind.split("-")[1]], out_dir, unit_batch=2 if kind.endswith("-ub2") else 1)
     finally:
         dist.destroy_process_group()
 
@@ -104,7 +104,7 @@ def _ddp_rank(rank: int, out_dir: str, comm_stream: bool) -> None:
     np.savez(os.path.join(out_dir, f"ddp_r{rank}.npz"), **out)
 
 
-def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str) -> None:
+def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str, unit_batch: int = 1) -> None:
     dev = torch.device("cuda", 0)
     c = tiny_gpt.Config(n_layer=2)
     model = tiny_gpt.GPT(c, seed=rank).to(dev)
@@ -118,7 +118,7 @@ def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str) -> None:
     for p in params:
         p.register_post_accumulate_grad_hook(capture)
     policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
-    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), mixed_precision=policy)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), mixed_precision=policy, unit_batch=unit_batch)
     out = {}
     for u, unit in enumerate(fsdp._units):
         out[f"unit_{u}_params"] = np.array([index[id(p)] for p in unit.params])
@@ -229,9 +229,12 @@ def test_ddp_two_processes_bitwise(tmp_path, comm_stream):
     assert all(float(res[r]["scale_after"]) == SCALE / 2 for r in range(W))
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16", "bf16-ub2"])
 def test_fsdp_two_processes_bitwise(tmp_path, dtype):
+    """bf16-ub2: ``unit_batch=2``, the two blocks gathered together and their reduce-scatters held
+    until both are ready (each still its own collective over the real group)."""
     res = _run(f"fsdp-{dtype}", tmp_path)
+    dtype = dtype.split("-")[0]
     c = tiny_gpt.Config(n_layer=2)
     init0 = _rank0_init(c)
     pdt = {"f32": o.F32, "bf16": o.BF16, "f16": o.F16}[dtype]
