@@ -196,20 +196,26 @@ class DistributedGradScaler:
             flag = pair[self._parity]
         return flag, pending
 
-    def _exchanges_flag(self) -> bool:
-        """Whether unscale_ takes the MAX of the flag over a real process group."""
-        return (
-            not isinstance(self.process_group, comm.ResidentGroup)
-            and comm.is_distributed()
-            and comm.get_world_size(self.process_group) > 1
-        )
+    def _flag_exchange(self) -> tuple[bool, object]:
+        """Whether unscale_ takes the MAX of the flag over a process group, and the group
+        (None: the default group).
+
+        Not under a ResidentGroup (this process saw every value there is).  An
+        IpcGroup's ranks are processes: DDP's one-shot reduction gives each the
+        same flag, but FSDP's ranks check different shards, so the flag is
+        exchanged over the group's host process group (4 bytes)."""
+        group = self.process_group
+        if isinstance(group, comm.IpcGroup):
+            return group.size() > 1, group.process_group
+        if isinstance(group, comm.ResidentGroup):
+            return False, None
+        return comm.is_distributed() and comm.get_world_size(group) > 1, group
 
     def _new_flag_pair(self, device: torch.device):
         """Both flags, zeroed: in pinned host memory on a GPU (unless an RCCL group must
         exchange them, which needs device memory), else in ``device``'s memory."""
-        if device.type == "cuda" and (
-            not self._exchanges_flag() or dist.get_backend(self.process_group) == "gloo"
-        ):
+        exchange, group = self._flag_exchange()
+        if device.type == "cuda" and (not exchange or dist.get_backend(group) == "gloo"):
             storage = torch.zeros(2, dtype=torch.int32, pin_memory=True)
             base = _native.host_device_address(storage.data_ptr())
             return (_HostFlag(storage[0:1], base, device), _HostFlag(storage[1:2], base + 4, device))
@@ -296,8 +302,9 @@ class DistributedGradScaler:
             flag.settle()
             flag = flag.host
         # The collective that makes the decision unanimous under FSDP / TP.
-        if self._exchanges_flag():
-            comm.dist_all_reduce(flag, op=dist.ReduceOp.MAX, group=self.process_group)
+        exchange, group = self._flag_exchange()
+        if exchange:
+            comm.dist_all_reduce(flag, op=dist.ReduceOp.MAX, group=group)
 
         self._found_inf_this_step = bool(flag.item() > 0)
         self._unscaled = True

@@ -309,6 +309,13 @@ class ResidentGroup:
         self._arenas.append(arena)
         return arena.row(self._rank)
 
+    def row_addresses(self, row: torch.Tensor) -> list[int]:
+        """Every rank's address of the row that :meth:`zeros` returned as ``row`` (rank order)."""
+        arena, off = self._locate(row)
+        if off != 0:
+            raise ValueError("row_addresses takes the row that zeros() returned")
+        return list(arena.row_ptrs)
+
     def _locate(self, t: torch.Tensor) -> tuple[_Arena, int]:
         for arena in self._arenas:
             off = arena.offset_of(t)
@@ -721,12 +728,14 @@ class IpcGroup(ResidentGroup):
 
     # -- the one-shot protocol ----------------------------------------------
 
-    def _rows_written(self) -> None:
+    def rows_written(self) -> None:
         """Every rank's writes to its rows are complete (this one's: its stream is drained)."""
+        if self._released:
+            raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
         torch.cuda.current_stream(self.device).synchronize()
         dist.barrier(group=self.process_group)
 
-    def _rows_read(self) -> None:
+    def rows_read(self) -> None:
         """Every rank has finished reading its peers' rows."""
         torch.cuda.current_stream(self.device).synchronize()
         dist.barrier(group=self.process_group)
@@ -734,9 +743,9 @@ class IpcGroup(ResidentGroup):
     def _one_shot(self, launch, async_op: bool):
         if self._released:
             raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
-        self._rows_written()
+        self.rows_written()
         launch()
-        self._rows_read()
+        self.rows_read()
         return _CompletedWork() if async_op else None
 
     def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
@@ -781,7 +790,8 @@ class IpcGroup(ResidentGroup):
     pack_all_reduce_unpack_planned = pack_all_reduce_unpack
 
     def reduce_scatter_sum(self, output, input_, async_op: bool = False):
-        raise NotImplementedError("IpcGroup implements the DDP all-reduce; FSDP runs over the process group itself")
+        raise NotImplementedError("IpcGroup: FSDP publishes and reads its units' rows itself "
+                                  "(FullyShardedDataParallel over an IpcGroup); no reduce-scatter of other tensors")
 
     all_gather_into = reduce_scatter_sum
 

@@ -26,8 +26,9 @@ import torch
 import torch.distributed as dist
 import torch.multiprocessing as mp
 
+import tiny_gpt
 from conftest import first_mismatch, same_bits
-from minidist import DDP, DistributedGradScaler, IpcGroup, comm
+from minidist import DDP, FSDP, DistributedGradScaler, IpcGroup, MixedPrecisionPolicy, comm
 from minidist import workloads as wl
 from oracle import gradpath as o
 
@@ -191,3 +192,91 @@ def test_ipc_in_place_all_reduce(tmp_path, world):
                     got = d[f"sum_{step}_{k}"]
                     assert int(d["mapped"]) <= len(SMALL) * (world - 1)
                 assert same_bits(got, want), f"step {step} buffer {k} rank {rank}: " + first_mismatch(got, want)
+
+
+FSDP_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, unit_batch: int) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        group = IpcGroup(dist.group.WORLD, dev)
+        c = tiny_gpt.Config(n_layer=2)
+        model = tiny_gpt.GPT(c, seed=rank).to(dev)  # the construction broadcast makes them rank 0's
+        params = list(model.parameters())
+        index = {id(p): i for i, p in enumerate(params)}
+        local: dict[int, torch.Tensor] = {}
+
+        def capture(p):
+            local[id(p)] = p.grad.detach().clone()
+
+        for p in params:
+            p.register_post_accumulate_grad_hook(capture)
+        policy = MixedPrecisionPolicy(param_dtype=FSDP_DTYPES[dtype_name], reduce_dtype=torch.float32)
+        fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=group, mixed_precision=policy,
+                    unit_batch=unit_batch)
+        scaler = DistributedGradScaler(init_scale=16.0, process_group=group)
+        out = {"units": np.array(len(fsdp._units))}
+        for u, unit in enumerate(fsdp._units):
+            out[f"unit_{u}_params"] = np.array([index[id(p)] for p in unit.params])
+        with fsdp.summon_full_params():
+            for u, unit in enumerate(fsdp._units):
+                out[f"full_{u}"] = _host_bits(unit._full)
+        ids, tgt = tiny_gpt.batch(c, 12, seed=6)
+        _, loss = fsdp(ids.chunk(world)[rank].to(dev), tgt.chunk(world)[rank].to(dev))
+        loss.backward()
+        for i, p in enumerate(params):
+            out[f"local_{i}"] = _host_bits(local[id(p)])
+        for u, unit in enumerate(fsdp._units):
+            out[f"shard_grad_{u}"] = _host_bits(unit.flat_shard.grad)
+            assert not unit.is_unsharded and all(p.grad is None for p in unit.params)
+
+        class _Opt:
+            param_groups = [{"params": list(fsdp.parameters())}]
+
+        if rank == world - 1:  # one rank's shard overflows: every rank must skip
+            with torch.no_grad():
+                fsdp._units[0].flat_shard.grad[0] = float("inf")
+        out["found"] = np.array(scaler.unscale_(_Opt()))
+        group.release()
+        np.savez(os.path.join(out_dir, f"ipc_fsdp_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("world,dtype,unit_batch", [(2, "f32", 1), (3, "bf16", 1), (4, "bf16", 2), (2, "f16", 3)])
+def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch):
+    """FSDP over an IpcGroup: each unit's all-gather is its ranks' published shards copied from the
+    mapped rows, its reduce-scatter the share kernel over every rank's published full-size gradient
+    (the reference's fsdp.py:172-241 with comm.all_gather_into_tensor / reduce_scatter_tensor).
+    Gathered parameters, every rank's shard gradient (against the oracle on the ranks' captured
+    local gradients) and the found-inf flag exchanged over the host group."""
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (FSDP over an IpcGroup, {dtype}, unit_batch={unit_batch})", flush=True)
+    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch), nprocs=world, join=True)
+    res = []
+    for r in range(world):
+        with np.load(tmp_path / f"ipc_fsdp_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    c = tiny_gpt.Config(n_layer=2)
+    init0 = [p.detach().reshape(-1).numpy().copy() for p in tiny_gpt.GPT(c, seed=0).parameters()]
+    pdt = {"f32": o.F32, "bf16": o.BF16, "f16": o.F16}[dtype]
+    n_units = int(res[0]["units"])
+    assert n_units == c.n_layer + 1
+    for u in range(n_units):
+        idx = [int(i) for i in res[0][f"unit_{u}_params"]]
+        numels = [init0[i].size for i in idx]
+        _, S, P = o.fsdp_layout(numels, world)
+        flat = np.zeros(P, np.float32)
+        flat[: sum(numels)] = np.concatenate([init0[i] for i in idx])
+        gathered = o.fsdp_gather_cast(flat, pdt)
+        grads = [[res[r][f"local_{i}"] for i in idx] for r in range(world)]
+        for rank in range(world):
+            assert same_bits(res[rank][f"full_{u}"], gathered), f"unit {u} rank {rank}: all-gather"
+            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, o.F32)
+            got = res[rank][f"shard_grad_{u}"]
+            assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)
+    assert all(bool(res[r]["found"]) for r in range(world))
