@@ -280,3 +280,79 @@ def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch):
             got = res[rank][f"shard_grad_{u}"]
             assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)
     assert all(bool(res[r]["found"]) for r in range(world))
+
+
+BACKWARD_CAP_MB = 0.01  # several bucket runs, launched while backward runs
+
+
+def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        group = IpcGroup(dist.group.WORLD, dev)
+        c = tiny_gpt.Config(n_layer=2)
+        model = tiny_gpt.GPT(c, seed=rank).to(dev)  # the construction broadcast makes them rank 0's
+        params = list(model.parameters())
+        local: dict[int, torch.Tensor] = {}
+        state = {"inject": False}
+
+        def capture(p):
+            if state["inject"] and rank == 1 and p is params[3]:
+                p.grad.view(-1)[5] = float("inf")  # this rank's backward overflowed
+            local[id(p)] = p.grad.detach().clone()
+
+        for p in params:
+            p.register_post_accumulate_grad_hook(capture)
+        scaler = DistributedGradScaler(init_scale=SCALE, process_group=group)
+        ddp = DDP(model, process_group=group, bucket_cap_mb=BACKWARD_CAP_MB, grad_scaler=scaler)
+        out = {"buckets": np.array(len(ddp._buckets))}
+
+        class _Opt:
+            param_groups = [{"params": params}]
+
+        ids, tgt = tiny_gpt.batch(c, 12, seed=5)
+        for step in range(2):
+            state["inject"] = step == 1
+            for p in params:
+                p.grad = None
+            _, loss = ddp(ids.chunk(world)[rank].to(dev), tgt.chunk(world)[rank].to(dev))
+            scaler.scale_loss(loss).backward()
+            out[f"found_{step}"] = np.array(scaler.unscale_(_Opt()))
+            scaler.update()
+            for i, p in enumerate(params):
+                out[f"local_{step}_{i}"] = _host_bits(local[id(p)])
+                out[f"final_{step}_{i}"] = _host_bits(p.grad)
+        group.release()
+        np.savez(os.path.join(out_dir, f"ipc_bwd_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("world", [2, 3])
+def test_ipc_ddp_during_backward_bitwise(tmp_path, world):
+    """DDP over an IpcGroup inside a real backward: bucket runs launch from the autograd hooks as
+    they fill (pack, fences, the one-shot reduction over the mapped rows), two steps, the second
+    with an overflow on one rank that every rank must skip.  Every rank's gradients against the
+    oracle's pipeline over all ranks' captured local gradients."""
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (DDP over an IpcGroup, real backward)", flush=True)
+    mp.spawn(_ddp_backward_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    res = []
+    for r in range(world):
+        with np.load(tmp_path / f"ipc_bwd_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    assert int(res[0]["buckets"]) > 2
+    c = tiny_gpt.Config(n_layer=2)
+    numels = [p.numel() for p in tiny_gpt.GPT(c, seed=0).parameters()]
+    n = len(numels)
+    for step in range(2):
+        grads = [[res[r][f"local_{step}_{i}"] for i in range(n)] for r in range(world)]
+        for rank in range(world):
+            want = o.ddp_pipeline(grads, [o.F32] * n, numels, BACKWARD_CAP_MB, rank, 1.0 / SCALE)
+            assert bool(res[rank][f"found_{step}"]) == want["found_inf"] == (step == 1)
+            for i in range(n):
+                got = res[rank][f"final_{step}_{i}"]
+                assert same_bits(got, want["grads"][i]), (
+                    f"step {step} rank {rank} param {i}: " + first_mismatch(got, want["grads"][i]))
