@@ -282,6 +282,53 @@ def test_fsdp_unit_batch_is_checked():
             FSDP(nn.Linear(2, 2), unit_batch=bad)
 
 
+def _broadcast_worker(rank: int, store: str, out_dir: str) -> None:
+    import os
+
+    import torch.distributed as dist
+
+    from minidist.ddp import _broadcasts_buffer
+
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=2)
+    try:
+        def module():
+            m = nn.Linear(3, 2)
+            with torch.no_grad():
+                for p in m.parameters():
+                    p.fill_(10 + rank)
+            m.register_buffer("f", torch.full((2,), 20.0 + rank))
+            m.register_buffer("i", torch.full((2,), 30 + rank, dtype=torch.int64))
+            m.register_buffer("u", torch.full((2,), 40 + rank, dtype=torch.uint8))
+            return m
+
+        out = {}
+        sub = dist.new_group([0, 1])
+        for tag, group, src, flt in (("ddp_default", None, 1, _broadcasts_buffer),
+                                     ("ddp_sub", sub, 1, _broadcasts_buffer),
+                                     ("fsdp_sub", sub, 0, None)):
+            m = module()
+            comm.broadcast_module_state(m, group, src, buffer_filter=flt)
+            out[tag] = np.array([m.weight[0, 0].item(), m.bias[0].item(), m.f[0].item(), m.i[0].item(), m.u[0].item()])
+        np.savez(os.path.join(out_dir, f"bcast_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+def test_module_state_broadcast_rules(tmp_path):
+    """The construction-time sync over a real two-rank gloo group: DDP broadcasts parameters and
+    floating-point / int32 / int64 / bool buffers from group rank ``src`` (from rank 0 on the
+    default group, whatever ``src``), ddp.py:160-173; FSDP every parameter and buffer from group
+    rank 0, fsdp.py:307-313."""
+    import torch.multiprocessing as mp
+
+    mp.spawn(_broadcast_worker, args=(str(tmp_path / "store"), str(tmp_path)), nprocs=2, join=True)
+    for r in range(2):
+        with np.load(tmp_path / f"bcast_r{r}.npz", allow_pickle=False) as d:
+            assert list(d["ddp_default"]) == [10, 10, 20, 30, 40 + r]  # rank 0's; uint8 buffer untouched
+            assert list(d["ddp_sub"]) == [11, 11, 21, 31, 40 + r]  # group rank 1's
+            assert list(d["fsdp_sub"]) == [10, 10, 20, 30, 40]  # every buffer, group rank 0's
+
+
 def test_out_of_scope_names_say_so():
     import minidist
 
