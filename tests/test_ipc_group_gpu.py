@@ -197,7 +197,8 @@ def test_ipc_in_place_all_reduce(tmp_path, world):
 FSDP_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
-def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, unit_batch: int) -> None:
+def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, unit_batch: int,
+                 accumulate: bool = False) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
@@ -226,8 +227,17 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
             for u, unit in enumerate(fsdp._units):
                 out[f"full_{u}"] = _host_bits(unit._full)
         ids, tgt = tiny_gpt.batch(c, 12, seed=6)
-        _, loss = fsdp(ids.chunk(world)[rank].to(dev), tgt.chunk(world)[rank].to(dev))
-        loss.backward()
+        my_ids, my_tgt = ids.chunk(world)[rank].to(dev), tgt.chunk(world)[rank].to(dev)
+        if accumulate:
+            # two halves under no_sync, then the flush: every unit's share in one multi-unit exchange
+            with fsdp.no_sync():
+                for h_ids, h_tgt in zip(my_ids.chunk(2), my_tgt.chunk(2), strict=True):
+                    _, loss = fsdp(h_ids, h_tgt)
+                    (loss / 2).backward()
+            fsdp.finish_gradient_sync()
+        else:
+            _, loss = fsdp(my_ids, my_tgt)
+            loss.backward()
         for i, p in enumerate(params):
             out[f"local_{i}"] = _host_bits(local[id(p)])
         for u, unit in enumerate(fsdp._units):
@@ -247,16 +257,19 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world,dtype,unit_batch", [(2, "f32", 1), (3, "bf16", 1), (4, "bf16", 2), (2, "f16", 3)])
-def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch):
+@pytest.mark.parametrize("world,dtype,unit_batch,accumulate",
+                         [(2, "f32", 1, False), (3, "bf16", 1, False), (4, "bf16", 2, False), (2, "f16", 3, False),
+                          (3, "f32", 1, True), (2, "bf16", 2, True)])
+def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulate):
     """FSDP over an IpcGroup: each unit's all-gather is its ranks' published shards copied from the
     mapped rows, its reduce-scatter the share kernel over every rank's published full-size gradient
     (the reference's fsdp.py:172-241 with comm.all_gather_into_tensor / reduce_scatter_tensor).
     Gathered parameters, every rank's shard gradient (against the oracle on the ranks' captured
-    local gradients) and the found-inf flag exchanged over the host group."""
+    local gradients) and the found-inf flag exchanged over the host group.  ``accumulate``: two
+    half-batch backwards under ``no_sync`` and the flush of every unit at once."""
     store = str(tmp_path / "store")
     print(f"spawning {world} ranks on cuda:0 (FSDP over an IpcGroup, {dtype}, unit_batch={unit_batch})", flush=True)
-    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch), nprocs=world, join=True)
+    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch, accumulate), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_fsdp_r{r}.npz", allow_pickle=False) as d:
