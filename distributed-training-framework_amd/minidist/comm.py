@@ -681,8 +681,7 @@ class IpcGroup(ResidentGroup):
     def zeros(self, numel: int, dtype: torch.dtype) -> torch.Tensor:
         """This rank's row of a new zero-filled symmetric buffer; every rank calls it in the
         same order with the same sizes (the rows are exchanged collectively)."""
-        if self._released:
-            raise RuntimeError("IpcGroup: released")
+        self._check_open()
         esize = torch.empty((), dtype=dtype).element_size()
         align = _ROW_ALIGN_BYTES // esize
         row_elems = max(align, (numel + align - 1) // align * align)
@@ -728,10 +727,13 @@ class IpcGroup(ResidentGroup):
 
     # -- the one-shot protocol ----------------------------------------------
 
-    def rows_written(self) -> None:
-        """Every rank's writes to its rows are complete (this one's: its stream is drained)."""
+    def _check_open(self) -> None:
         if self._released:
             raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
+
+    def rows_written(self) -> None:
+        """Every rank's writes to its rows are complete (this one's: its stream is drained)."""
+        self._check_open()
         torch.cuda.current_stream(self.device).synchronize()
         dist.barrier(group=self.process_group)
 
@@ -741,8 +743,6 @@ class IpcGroup(ResidentGroup):
         dist.barrier(group=self.process_group)
 
     def _one_shot(self, launch, async_op: bool):
-        if self._released:
-            raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
         self.rows_written()
         launch()
         self.rows_read()
@@ -755,6 +755,7 @@ class IpcGroup(ResidentGroup):
         in-place ``dist.all_reduce`` does; over IPC a rank's row is still read by
         its peers while its own reduction runs, so the sums go to a private
         buffer first and are copied into the rows once every rank has read them."""
+        self._check_open()
         arenas = {id(a): a for a in (self._locate(t)[0] for t in tensors)}
         staged = [a for a in arenas.values() if a.target is None]
         for arena in staged:

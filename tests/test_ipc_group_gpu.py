@@ -168,6 +168,15 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
             for k, row in enumerate(rows):
                 out[f"sum_{step}_{k}"] = row.cpu().numpy()
         group.release()
+        # a released group maps nothing: every further use is refused, nothing is launched
+        for use in (lambda: comm.all_reduce(rows[0], group=group), lambda: group.zeros(16, torch.float32),
+                    group.rows_written):
+            try:
+                use()
+            except RuntimeError as e:
+                assert "released" in str(e)
+            else:
+                raise AssertionError("a released IpcGroup accepted a collective")
         np.savez(os.path.join(out_dir, f"inplace_r{rank}.npz"), **out)
     finally:
         dist.destroy_process_group()
