@@ -444,13 +444,9 @@ def ipc_open(h: IpcHandle) -> int:
     return int(base.value) + int(h.offset)
 
 
-def ipc_close(ptr: int, h: IpcHandle) -> None:
-    """Unmaps what :func:`ipc_open` mapped (``ptr`` is the pointer it returned)."""
-    ipc_close_base(ptr - int(h.offset))
-
-
 def ipc_close_base(base: int) -> None:
-    """Unmaps a peer allocation by its mapped base address."""
+    """Unmaps a peer allocation by its mapped base address (what :func:`ipc_open` returned, minus
+    the handle's offset)."""
     check(lib().mdx_ipc_close(base), "mdx_ipc_close")
 
 
