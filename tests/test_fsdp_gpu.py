@@ -153,6 +153,37 @@ def test_unshard_casts_into_own_slot_and_gathers_peers(comm_streams):
         assert not u.is_unsharded
 
 
+@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
+def test_unit_and_memory_summaries(param_dtype):
+    """unit_summary() and memory_summary() (fsdp.py:472-492) from their definitions: per unit
+    (name, full elements, shard elements); per rank, MiB of the shards and of the replicated model,
+    four shard-dtype copies (parameters, gradients, Adam's two moments) sharded or whole, and the
+    largest unit gathered in param_dtype."""
+    c = tiny_gpt.Config(n_layer=3)
+    W = 4
+    model = tiny_gpt.GPT(c).to(DEV)
+    sizes = {n: p.numel() for n, p in model.named_parameters()}
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, 1, DEV),
+                mixed_precision=MixedPrecisionPolicy(param_dtype=param_dtype))
+    rows = fsdp.unit_summary()
+    assert [r[0] for r in rows] == ["blocks.0", "blocks.1", "blocks.2", "<root>"]
+    block = sum(v for n, v in sizes.items() if n.startswith("blocks.0."))
+    root = sum(v for n, v in sizes.items() if not n.startswith("blocks."))
+    assert [r[1] for r in rows] == [block, block, block, root]
+    assert [r[2] for r in rows] == [-(-n // W) for n in (block, block, block, root)]
+    total, shard = sum(r[1] for r in rows), sum(r[2] for r in rows)
+    mib, gather = 2.0**20, torch.empty((), dtype=param_dtype).element_size()
+    assert fsdp.memory_summary() == {
+        "params_total_M": total / 1e6,
+        "shard_params_MB": shard * 4 / mib,
+        "replicated_params_MB": total * 4 / mib,
+        "fsdp_state_MB": shard * 4 * 4 / mib,
+        "ddp_state_MB": total * 4 * 4 / mib,
+        "transient_gather_MB": max(block, root) * gather / mib,
+        "num_units": 4,
+    }
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):

@@ -235,6 +235,35 @@ def test_scaler_state_machine_matches_oracle(init, interval, found, final):
     assert set(s.state_dict()) == {"scale", "good_steps", "num_skipped", "num_steps"}
 
 
+def test_scaler_checkpoint_round_trip_and_summary():
+    """state_dict / load_state_dict carry the state machine across a restart (amp.py:164-176): a
+    scaler restored mid-history continues exactly as the uninterrupted one; summary() is the
+    reference's line, and an old checkpoint without the counters loads with them at zero."""
+    history = [True, False, False, False, True, False, False, False, False]
+    whole = DistributedGradScaler(init_scale=2.0**10, growth_interval=3)
+    first = DistributedGradScaler(init_scale=2.0**10, growth_interval=3)
+
+    def run(s, found):
+        s.num_steps += 1  # what step() counts
+        s.num_skipped += int(found)
+        s._found_inf_this_step, s._unscaled = found, True  # what unscale_ would have decided
+        s.update()
+
+    for f in history[:4]:
+        run(whole, f)
+        run(first, f)
+    resumed = DistributedGradScaler(init_scale=1.0, growth_interval=3)
+    resumed.load_state_dict(first.state_dict())
+    for f in history[4:]:
+        run(whole, f)
+        run(resumed, f)
+        assert resumed.state_dict() == whole.state_dict()
+    assert whole.summary() == f"scale={whole.scale:g}  skipped=2/9 (22.2%)"
+    old = DistributedGradScaler()
+    old.load_state_dict({"scale": 256.0, "good_steps": 1})
+    assert old.state_dict() == {"scale": 256.0, "good_steps": 1, "num_skipped": 0, "num_steps": 0}
+
+
 # ---------------------------------------------------------------------------
 # DDP layout (meta tensors: real GPT-2 shapes without allocating them)
 # ---------------------------------------------------------------------------
