@@ -285,6 +285,20 @@ def test_ddp_layout_matches_oracle_at_real_shapes(cfg, W, cap):
     assert ddp.world_size == W
 
 
+def test_ddp_bucket_summary_and_passthrough():
+    """bucket_summary() (ddp.py:296-302): (index, parameters, MiB of their bytes) per bucket in launch
+    order; attributes the wrapper does not have come from the wrapped module (ddp.py:304-313)."""
+    specs = w.gpt_specs(**w.TINY_GPT)
+    module = MetaParams(specs)
+    module.vocab_size = 1024
+    ddp = DistributedDataParallel(module, process_group=comm.ResidentGroup(4, 0, "meta"), bucket_cap_mb=0.5)
+    layout = o.build_buckets([sp.nbytes for sp in specs], 0.5)
+    assert ddp.bucket_summary() == [(k, len(b), sum(specs[i].nbytes for i in b) / 2**20) for k, b in enumerate(layout)]
+    assert ddp.vocab_size == 1024 and ddp.ps is module.ps
+    with pytest.raises(AttributeError):
+        ddp.no_such_attribute
+
+
 def test_bucket_spans_are_the_oracle_partition():
     """DDP's partition (index ranges over the reversed parameters) against the oracle's restatement
     of ddp.py:175-190, over every list of up to 5 sizes from a small alphabet and several caps."""
