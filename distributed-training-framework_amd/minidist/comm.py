@@ -309,6 +309,13 @@ class ResidentGroup:
         self._arenas.append(arena)
         return arena.row(self._rank)
 
+    def _rows_of(self, t: torch.Tensor) -> list[int]:
+        """Every rank's address of ``t``'s elements in its row (``t`` lies in a symmetric buffer)."""
+        if not t.is_contiguous():
+            raise RuntimeError("a collective's symmetric-buffer operand must be contiguous")
+        arena, off = self._locate(t)
+        return [p + off * arena.esize for p in arena.row_ptrs]
+
     def row_addresses(self, row: torch.Tensor) -> list[int]:
         """Every rank's address of the row that :meth:`zeros` returned as ``row`` (rank order)."""
         arena, off = self._locate(row)
@@ -581,17 +588,16 @@ class ResidentGroup:
     def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
         _native.require_device_tensor(input_, "reduce_scatter input")
-        reps = self.replicas(input_)
+        rows = self._rows_of(input_)
         S = output.numel()
         if input_.numel() != S * self._world:
             raise ValueError(f"reduce_scatter: input has {input_.numel()} elements, expected {S * self._world}")
         if output.dtype != input_.dtype:
             raise TypeError("reduce_scatter: output and input dtypes differ")
         _native.require_dense(output, "reduce_scatter output")
-        lo = self._rank * S
-        flat = [r.reshape(-1) for r in reps]
-        own = _native.pieces_array([(flat[self._rank][lo:].data_ptr(), 0, S)])
-        peers = [f[lo:].data_ptr() for f in flat]
+        lo = self._rank * S * input_.element_size()
+        peers = [r + lo for r in rows]
+        own = _native.pieces_array([(peers[self._rank], 0, S)])
         code = _native.dtype_code(input_.dtype)
         stream = torch.cuda.current_stream(input_.device)
         _native.reduce_scatter_share(
@@ -604,15 +610,15 @@ class ResidentGroup:
         """``output[r*S:(r+1)*S] = replicas(input_)[r]`` for every rank r."""
         _native.require_device_tensor(input_, "all_gather input")
         _native.require_dense(output, "all_gather output")
-        reps = self.replicas(input_)
+        rows = self._rows_of(input_)
         S = input_.numel()
         if output.numel() != S * self._world or output.dtype != input_.dtype:
             raise ValueError("all_gather: output must hold world_size inputs of the same dtype")
-        out = output.view(-1)
-        rows = [(reps[r].data_ptr(), out[r * S :].data_ptr(), S) for r in range(self._world)]
+        es, base = input_.element_size(), output.data_ptr()
+        spans = [(rows[r], base + r * S * es, S) for r in range(self._world)]
         code = _native.dtype_code(input_.dtype)
         stream = torch.cuda.current_stream(input_.device)
-        _native.pack(_native.spans_array(rows), code, code, 1.0, False, stream.cuda_stream)
+        _native.pack(_native.spans_array(spans), code, code, 1.0, False, stream.cuda_stream)
         return StreamWork(stream) if async_op else None
 
 
@@ -791,10 +797,16 @@ class IpcGroup(ResidentGroup):
     pack_all_reduce_unpack_planned = pack_all_reduce_unpack
 
     def reduce_scatter_sum(self, output, input_, async_op: bool = False):
-        raise NotImplementedError("IpcGroup: FSDP publishes and reads its units' rows itself "
-                                  "(FullyShardedDataParallel over an IpcGroup); no reduce-scatter of other tensors")
+        """``output`` = this rank's slice of the rank-ordered SUM of every rank's ``input_`` (a row
+        of a symmetric buffer), read one-shot from the mapped rows."""
+        self._check_open()
+        return self._one_shot(lambda: ResidentGroup.reduce_scatter_sum(self, output, input_), async_op)
 
-    all_gather_into = reduce_scatter_sum
+    def all_gather_into(self, output, input_, async_op: bool = False):
+        """``output[r*S:(r+1)*S]`` = rank r's ``input_`` (a row of a symmetric buffer), copied
+        one-shot from the mapped rows."""
+        self._check_open()
+        return self._one_shot(lambda: ResidentGroup.all_gather_into(self, output, input_), async_op)
 
 
 def zeros_for_collective(numel: int, dtype: torch.dtype, device: torch.device, group=None) -> torch.Tensor:

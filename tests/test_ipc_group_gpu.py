@@ -151,6 +151,13 @@ def _small_rows(rank: int, step: int) -> list[np.ndarray]:
     return [(g.standard_normal(n) * 1e3).astype(np.float32) for n in SMALL]
 
 
+RS_S = 777  # elements of a reduce-scatter output / an all-gather input
+
+
+def _rs_rows(rank: int, world: int) -> np.ndarray:
+    return (np.random.default_rng(991 + rank).standard_normal(RS_S * world) * 1e2).astype(np.float32)
+
+
 def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
@@ -167,6 +174,15 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
             comm.all_reduce_coalesced([rows[1][:1500], rows[1][1500:]], group=group)  # two views of the other
             for k, row in enumerate(rows):
                 out[f"sum_{step}_{k}"] = row.cpu().numpy()
+        # comm.reduce_scatter_tensor / all_gather_into_tensor (reference comm.py:237-265) over the rows
+        rs_in, ag_in = group.zeros(RS_S * world, torch.float32), group.zeros(RS_S, torch.float32)
+        rs_in.copy_(torch.from_numpy(_rs_rows(rank, world)).to(dev))
+        ag_in.copy_(torch.from_numpy(_rs_rows(rank, world)[:RS_S]).to(dev))
+        rs_out = torch.empty(RS_S, device=dev)
+        ag_out = torch.empty(RS_S * world, device=dev)
+        comm.reduce_scatter_tensor(rs_out, rs_in, group=group)
+        comm.all_gather_into_tensor(ag_out, ag_in, group=group)
+        out["rs"], out["ag"] = rs_out.cpu().numpy(), ag_out.cpu().numpy()
         group.release()
         # a released group maps nothing: every further use is refused, nothing is launched
         for use in (lambda: comm.all_reduce(rows[0], group=group), lambda: group.zeros(16, torch.float32),
@@ -186,7 +202,8 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
 def test_ipc_in_place_all_reduce(tmp_path, world):
     """``comm.all_reduce`` in place on rows of an IpcGroup buffer with no reduce target: every rank
     ends with the rank-ordered sum while its peers read its row concurrently; a peer allocation
-    that holds two rows is mapped once."""
+    that holds two rows is mapped once.  Then ``comm.reduce_scatter_tensor`` and
+    ``comm.all_gather_into_tensor`` over symmetric rows."""
     store = str(tmp_path / "store")
     print(f"spawning {world} ranks on cuda:0 (IpcGroup in-place all-reduce)", flush=True)
     mp.spawn(_in_place_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
@@ -201,6 +218,16 @@ def test_ipc_in_place_all_reduce(tmp_path, world):
                     got = d[f"sum_{step}_{k}"]
                     assert int(d["mapped"]) <= len(SMALL) * (world - 1)
                 assert same_bits(got, want), f"step {step} buffer {k} rank {rank}: " + first_mismatch(got, want)
+    inputs = [_rs_rows(r, world) for r in range(world)]
+    for rank in range(world):
+        with np.load(tmp_path / f"inplace_r{rank}.npz", allow_pickle=False) as d:
+            rs, ag = d["rs"], d["ag"]
+        want = inputs[0][rank * RS_S : (rank + 1) * RS_S].copy()
+        for r in range(1, world):
+            want = want + inputs[r][rank * RS_S : (rank + 1) * RS_S]  # float32, rank order
+        assert same_bits(rs, want), f"reduce_scatter rank {rank}: " + first_mismatch(rs, want)
+        want_ag = np.concatenate([x[:RS_S] for x in inputs])
+        assert same_bits(ag, want_ag), f"all_gather rank {rank}: " + first_mismatch(ag, want_ag)
 
 
 FSDP_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
