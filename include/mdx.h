@@ -63,7 +63,8 @@ enum {
   MDX_EDTYPE = -2,    /* dtype code not in {MDX_F32, MDX_BF16, MDX_F16}   */
   MDX_EWORLD = -3,    /* world outside [1, MDX_MAX_WORLD] or rank >= world */
   MDX_EALIAS = -4,    /* an output overlaps an input it must not overlap  */
-  MDX_ESIZE = -5,     /* plan buffer missing or too small                 */
+  MDX_ESIZE = -5,     /* plan buffer missing or too small; an IPC
+                         allocation of MDX_IPC_MAX_ALLOC_BYTES or more     */
   MDX_ESCRATCH = -6,  /* plan larger than MDX_NOALLOC_SCRATCH_BYTES, or the
                          stream is not on the current device (allocation-free
                          entry point only)                                  */
