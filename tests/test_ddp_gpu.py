@@ -407,8 +407,11 @@ def test_comm_stream_argument_is_checked():
         DDP(Flat([(4,)]), process_group=ResidentGroup(2, 0, DEV), comm_stream="yes")
 
 
-def test_no_sync_accumulation_then_sync():
-    """Reference tests/test_ddp.py:80-100: two half-batches under no_sync + synced == full step."""
+@pytest.mark.parametrize("explicit_finish", [False, True])
+def test_no_sync_accumulation_then_sync(explicit_finish):
+    """Reference tests/test_ddp.py:80-100: two half-batches under no_sync + synced == full step.
+    ``explicit_finish``: both halves under no_sync, then ``finish_gradient_sync()`` flushes every
+    bucket, as the reference trainer does around a pipeline schedule (examples/train_gpt.py:211-215)."""
     c = tiny_gpt.Config()
     W, rank = 2, 0
     ids, tgt = tiny_gpt.batch(c, 8)
@@ -430,8 +433,14 @@ def test_no_sync_accumulation_then_sync():
     with ddp.no_sync():
         _, l = ddp(halves[0][0].to(DEV), halves[0][1].to(DEV))
         (l / 2).backward()
-    _, l = ddp(halves[1][0].to(DEV), halves[1][1].to(DEV))
-    (l / 2).backward()
+        if explicit_finish:
+            _, l = ddp(halves[1][0].to(DEV), halves[1][1].to(DEV))
+            (l / 2).backward()
+    if explicit_finish:
+        ddp.finish_gradient_sync()
+    else:
+        _, l = ddp(halves[1][0].to(DEV), halves[1][1].to(DEV))
+        (l / 2).backward()
     for p, e in zip(model.parameters(), expected, strict=True):
         rel = (p.grad - e).abs().max().item() / max(e.abs().max().item(), 1.0)
         assert rel <= 2e-5
