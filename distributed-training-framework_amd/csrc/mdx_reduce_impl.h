@@ -35,7 +35,10 @@
 // W <= WMAX.  x_r = cvt_Acc(contribution_r[p]); x_r = rnd_Acc(x_r * pre | x_r / pre);
 // acc = rank-ordered sum in Acc; y = cvt_Out(acc); y = rnd_Out(out + y) when
 // accumulating; optional unscale + found-inf epilogue.  The pre-scale and the
-// accumulate are compile-time variants selected once per workgroup.
+// accumulate are compile-time variants selected once per workgroup.  A piece
+// may carry its own destination (PieceRun::grad), so that one dispatch writes
+// the shard gradients of several FSDP units (the multi-unit share); otherwise
+// it writes out + its position.
 //
 // Every contribution is read once per step, so every load is non-temporal;
 // each lane keeps U fragments of all W contributions in flight before the
