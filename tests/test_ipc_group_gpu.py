@@ -334,7 +334,7 @@ def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulat
 BACKWARD_CAP_MB = 0.01  # several bucket runs, launched while backward runs
 
 
-def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str, comm_stream: bool = False) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
@@ -355,7 +355,8 @@ def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str) -> Non
         for p in params:
             p.register_post_accumulate_grad_hook(capture)
         scaler = DistributedGradScaler(init_scale=SCALE, process_group=group)
-        ddp = DDP(model, process_group=group, bucket_cap_mb=BACKWARD_CAP_MB, grad_scaler=scaler)
+        ddp = DDP(model, process_group=group, bucket_cap_mb=BACKWARD_CAP_MB, grad_scaler=scaler,
+                  comm_stream=comm_stream)
         out = {"buckets": np.array(len(ddp._buckets))}
 
         class _Opt:
@@ -379,15 +380,17 @@ def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str) -> Non
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world", [2, 3])
-def test_ipc_ddp_during_backward_bitwise(tmp_path, world):
+@pytest.mark.parametrize("world,comm_stream", [(2, False), (3, False), (2, True)])
+def test_ipc_ddp_during_backward_bitwise(tmp_path, world, comm_stream):
     """DDP over an IpcGroup inside a real backward: bucket runs launch from the autograd hooks as
     they fill (pack, fences, the one-shot reduction over the mapped rows), two steps, the second
     with an overflow on one rank that every rank must skip.  Every rank's gradients against the
-    oracle's pipeline over all ranks' captured local gradients."""
+    oracle's pipeline over all ranks' captured local gradients.  ``comm_stream``: the packs, fences
+    and reductions on DDP's dedicated stream."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (DDP over an IpcGroup, real backward)", flush=True)
-    mp.spawn(_ddp_backward_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (DDP over an IpcGroup, real backward, comm_stream={comm_stream})",
+          flush=True)
+    mp.spawn(_ddp_backward_worker, args=(world, store, str(tmp_path), comm_stream), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_bwd_r{r}.npz", allow_pickle=False) as d:
