@@ -25,6 +25,7 @@ from contextlib import contextmanager
 from dataclasses import dataclass, field
 from datetime import timedelta
 
+import numpy as np
 import torch
 import torch.distributed as dist
 
@@ -236,6 +237,38 @@ class StreamWork:
 
 
 _ROW_ALIGN_BYTES = 256
+# A two-shot share starts a multiple of this many elements past the extent's start.
+_SHARE_ALIGN_ELEMS = 64
+
+
+def two_shot_shares(lo: int, hi: int, world: int, align: int = _SHARE_ALIGN_ELEMS) -> list[tuple[int, int]]:
+    """Rank j's share ``[a, b)`` of the elements ``[lo, hi)`` in a two-shot all-reduce.
+
+    The shares are contiguous and in rank order and cover ``[lo, hi)`` exactly;
+    every share but the last non-empty one is a whole number of ``align``
+    elements long (shares past the end are empty)."""
+    if world < 1 or align < 1:
+        raise ValueError("two_shot_shares: world and align must be positive")
+    step = -(-(hi - lo) // (world * align)) * align if hi > lo else 0
+    return [(min(lo + j * step, hi), min(lo + (j + 1) * step, hi)) if hi > lo else (lo, lo) for j in range(world)]
+
+
+def clip_grad_runs(runs: np.ndarray, lo: int, hi: int, grad_esize: int) -> np.ndarray:
+    """The parts of an ``mdx_grad_run`` table that fall in ``[lo, hi)``.
+
+    Each part keeps its run's order; its offset and numel are clipped to the
+    window and its gradient address (0 stays 0) is advanced to the part's
+    first element (``grad_esize`` bytes per element)."""
+    off = runs["offset"]
+    end = off + runs["numel"]
+    part = runs[(runs["numel"] > 0) & (end > lo) & (off < hi) & (lo < hi)].copy()
+    a = np.maximum(part["offset"], lo)
+    b = np.minimum(part["offset"] + part["numel"], hi)
+    moved = part["grad"] + ((a - part["offset"]) * grad_esize).astype(np.uint64)
+    part["grad"] = np.where(part["grad"] != 0, moved, np.uint64(0))
+    part["offset"] = a
+    part["numel"] = b - a
+    return part
 
 
 class _Arena:
@@ -651,27 +684,47 @@ class IpcGroup(ResidentGroup):
     The multi-GPU design of this path, runnable here with W processes sharing
     the one GPU: each rank allocates its row of every symmetric buffer
     (:meth:`zeros`, each row an allocation below 2 GiB), exports it over IPC,
-    and maps its peers' rows, so every collective is a *one-shot* reduction:
-    each rank reads all W rows with the same rank-ordered kernels a
-    :class:`ResidentGroup` uses and computes the full result itself,
-    bit-identical on every rank.  The reference hands each bucket to
-    ``dist.all_reduce`` instead (minidist/comm.py:223-234).
+    and maps its peers' rows.  The all-reduces run one of two ways
+    (``algorithm``), both with the same rank-ordered kernels a
+    :class:`ResidentGroup` uses, so every rank ends with bit-identical
+    results.  The reference hands each bucket to ``dist.all_reduce`` instead
+    (minidist/comm.py:223-234).
+
+    * ``"one_shot"``: each rank reads all W rows and computes the whole result
+      itself -- (W-1) rows pulled per rank, one exchange round.
+    * ``"two_shot"``: each rank reduces its 1/W share of the extent from all W
+      rows into its reduce target (the bucket), then copies the peers' reduced
+      shares out of their targets while unpacking -- 2(W-1)/W of a row pulled
+      per rank, two rounds.  A reduce target must then be a symmetric buffer
+      too (``symmetric_targets``); without one the sums replace the rows, which
+      is safe in place because a rank's share of its own row is read by no peer
+      in the first round.
 
     Ordering is the host's: before a reduction every rank has finished
     writing its row (stream synchronisation, then a barrier over
-    ``process_group``), and after it every rank has finished reading its
-    peers' rows (the same again) before anyone writes a row again.  No kernel
-    waits on a flag a peer sets.  The pack cannot be fused into the reduction
-    (a rank's row must be complete before its peers read it), so DDP runs the
+    ``process_group``), a two-shot reduction meets again once every share is
+    reduced, and after it every rank has finished reading its peers' memory
+    (the same again) before anyone writes a row again.  No kernel waits on a
+    flag a peer sets.  The pack cannot be fused into the reduction (a rank's
+    row must be complete before its peers read it), so DDP runs the
     two-dispatch pipeline over this group (``fuses_pack`` is False).
     ``process_group`` carries only host traffic: the handles and the barriers
     (gloo is enough).
     """
 
     fuses_pack = False
+    ALGORITHMS = ("one_shot", "two_shot")
 
-    def __init__(self, process_group=None, device: torch.device | str | None = None):
+    def __init__(self, process_group=None, device: torch.device | str | None = None, algorithm: str = "one_shot"):
+        if algorithm not in self.ALGORITHMS:
+            raise ValueError(f"IpcGroup: algorithm must be one of {self.ALGORITHMS}, got {algorithm!r}")
         self.process_group = process_group
+        self.algorithm = algorithm
+        # Two-shot: peers read each rank's reduced share out of its reduce target, so DDP
+        # allocates its buckets as symmetric buffers, and reductions run through the
+        # kernel-argument tables (a share is a different slice of the runs on every rank).
+        self.symmetric_targets = algorithm == "two_shot"
+        self.plans_reductions = algorithm == "one_shot"
         self._released = False
         # A peer's allocation mapped into this process, by (rank, handle bytes): the
         # caching allocator may carve two small rows out of one allocation, whose
@@ -680,7 +733,8 @@ class IpcGroup(ResidentGroup):
         super().__init__(dist.get_world_size(process_group), dist.get_rank(process_group), device)
 
     def __repr__(self) -> str:
-        return f"IpcGroup(world_size={self._world}, rank={self._rank}, device={self.device})"
+        return (f"IpcGroup(world_size={self._world}, rank={self._rank}, device={self.device}, "
+                f"algorithm={self.algorithm!r})")
 
     # -- symmetric memory ---------------------------------------------------
 
@@ -754,14 +808,81 @@ class IpcGroup(ResidentGroup):
         self.rows_read()
         return _CompletedWork() if async_op else None
 
+    # -- the two-shot protocol ----------------------------------------------
+
+    def set_reduce_target(self, row: torch.Tensor, target: torch.Tensor) -> None:
+        if self.symmetric_targets:
+            self._target_rows(target, row.dtype, row.numel())
+        super().set_reduce_target(row, target)
+
+    def _target_rows(self, target: torch.Tensor, dtype: torch.dtype, numel: int) -> list[int]:
+        """Every rank's address of ``target``, a two-shot reduce target (a symmetric buffer)."""
+        _native.require_device_tensor(target, "all_reduce output")
+        if target.dtype != dtype or target.numel() < numel:
+            raise ValueError("all_reduce: the reduce target must have the reduction's dtype and at least its length")
+        if not target.is_contiguous():
+            raise ValueError("all_reduce: the reduce target must be contiguous")
+        try:
+            return self._rows_of(target)
+        except RuntimeError:
+            raise ValueError(
+                "a two-shot IpcGroup reduces into symmetric buffers (IpcGroup.zeros): "
+                "the peers read each rank's reduced share from its target"
+            ) from None
+
+    @staticmethod
+    def _runs_extent(runs: np.ndarray) -> tuple[int, int]:
+        live = runs[runs["numel"] > 0]
+        if len(live) == 0:
+            return 0, 0
+        return int(live["offset"].min()), int((live["offset"] + live["numel"]).max())
+
+    def _extent_agreed(self, lo: int, hi: int) -> None:
+        """:meth:`rows_written` of a two-shot reduction.  Its barrier is a MAX over
+        (lo, hi, -lo, -hi), which also checks that every rank reduces the same
+        elements [lo, hi): each reduces its share of them for all the others."""
+        self._check_open()
+        torch.cuda.current_stream(self.device).synchronize()
+        ext = torch.tensor([lo, hi, -lo, -hi], dtype=torch.int64)
+        dist.all_reduce(ext, op=dist.ReduceOp.MAX, group=self.process_group)
+        lo_max, hi_max, lo_min, hi_min = int(ext[0]), int(ext[1]), -int(ext[2]), -int(ext[3])
+        if lo_max != lo_min or hi_max != hi_min:
+            raise RuntimeError(
+                f"IpcGroup two-shot: the ranks reduce different element ranges "
+                f"(starts {lo_min}..{lo_max}, ends {hi_min}..{hi_max})"
+            )
+
+    def _two_shot(self, lo: int, hi: int, reduce_share, copy_share, async_op: bool):
+        """The two rounds over the elements [lo, hi): ``reduce_share(a, b)`` reduces this
+        rank's share from all W rows into its target; ``copy_share(j, a, b)`` takes peer
+        j's reduced share out of peer j's target."""
+        shares = two_shot_shares(lo, hi, self._world)
+        self._extent_agreed(lo, hi)  # every row is written
+        a, b = shares[self._rank]
+        if b > a:
+            reduce_share(a, b)
+        self.rows_written()  # every share is reduced (and no peer reads a row any more)
+        for j, (a, b) in enumerate(shares):
+            if j != self._rank and b > a:
+                copy_share(j, a, b)
+        self.rows_read()  # no peer reads this rank's target any more
+        return _CompletedWork() if async_op else None
+
+    # -- collectives ----------------------------------------------------------
+
     def all_reduce_sum(self, tensors: Sequence[torch.Tensor], async_op: bool = False):
         """SUM over the W ranks' rows, rank order 0..W-1, into the buffer's reduce target.
 
         Without a target the sum replaces the rows' contents, as the reference's
-        in-place ``dist.all_reduce`` does; over IPC a rank's row is still read by
-        its peers while its own reduction runs, so the sums go to a private
-        buffer first and are copied into the rows once every rank has read them."""
+        in-place ``dist.all_reduce`` does.  One-shot: a rank's row is still read
+        by its peers while its own reduction runs, so the sums go to a private
+        buffer first and are copied into the rows once every rank has read them.
+        Two-shot: each rank reduces its share in place (no peer reads that part
+        of its row in the first round) and copies the peers' reduced shares out
+        of their rows in the second."""
         self._check_open()
+        if self.algorithm == "two_shot":
+            return self._all_reduce_sum_two_shot(tensors, async_op)
         arenas = {id(a): a for a in (self._locate(t)[0] for t in tensors)}
         staged = [a for a in arenas.values() if a.target is None]
         for arena in staged:
@@ -777,17 +898,99 @@ class IpcGroup(ResidentGroup):
                 arena.target = None
         return work
 
+    def _all_reduce_sum_two_shot(self, tensors: Sequence[torch.Tensor], async_op: bool):
+        by_arena: dict[int, tuple[_IpcArena, list[tuple[int, int, int]]]] = {}
+        for t in tensors:
+            _native.require_device_tensor(t, "all_reduce input")
+            arena, off = self._locate(t)
+            by_arena.setdefault(id(arena), (arena, []))[1].append((off, t.numel(), 0))
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        me = self._rank
+        work = None
+        for arena, parts in by_arena.values():
+            runs = _native.grad_runs_array(sorted(parts))
+            rows = arena.row_ptrs
+            outs = rows if arena.target is None else self._target_rows(arena.target, arena.dtype, arena.numel)
+            code, es = _native.dtype_code(arena.dtype), arena.esize
+
+            def reduce_share(a, b, runs=runs, rows=rows, outs=outs, code=code):
+                part = clip_grad_runs(runs, a, b, 0)
+                _native.allreduce_sum(rows, code, part["offset"].tolist(), part["numel"].tolist(), outs[me], stream)
+
+            def copy_share(j, a, b, runs=runs, outs=outs, code=code, es=es):
+                part = clip_grad_runs(runs, a, b, 0)
+                spans = [(outs[j] + o * es, outs[me] + o * es, n)
+                         for o, n in zip(part["offset"].tolist(), part["numel"].tolist())]
+                _native.pack(_native.spans_array(spans), code, code, 1.0, False, stream)
+
+            work = self._two_shot(*self._runs_extent(runs), reduce_share, copy_share, async_op)
+        return work
+
     def all_reduce_unpack(self, buffer, runs, grad_dtype, inv_scale=1.0, found_inf=None, async_op=False,
                           bucket=None):
-        return self._one_shot(lambda: ResidentGroup.all_reduce_unpack(
-            self, buffer, runs, grad_dtype, inv_scale, found_inf, bucket=bucket), async_op)
+        """:meth:`ResidentGroup.all_reduce_unpack` over the mapped rows.  Two-shot: the
+        fused reduction + unpack of this rank's share (its part of every gradient), then,
+        for each peer, the same kernel over one replica -- the peer's reduced share in its
+        bucket -- copied into this rank's bucket and unpacked into the rest of the gradients."""
+        if self.algorithm == "one_shot":
+            return self._one_shot(lambda: ResidentGroup.all_reduce_unpack(
+                self, buffer, runs, grad_dtype, inv_scale, found_inf, bucket=bucket), async_op)
+        self._check_open()
+        _native.require_device_tensor(buffer, "all_reduce input")
+        arena, off = self._locate(buffer)
+        rows = [p + off * arena.esize for p in arena.row_ptrs]
+        outs = rows if bucket is None else self._target_rows(bucket, buffer.dtype, buffer.numel())
+        code = _native.dtype_code(arena.dtype)
+        return self._two_shot_unpack(rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op,
+                                     lambda part, out, gcode, inv, flag, st: _native.allreduce_unpack(
+                                         rows, code, part, out, gcode, inv, flag, st), code)
 
     def all_reduce_unpack_wide(self, wire, bucket, runs, grad_dtype, prescale, inv_scale=1.0, found_inf=None,
                                async_op=False):
-        return self._one_shot(lambda: ResidentGroup.all_reduce_unpack_wide(
-            self, wire, bucket, runs, grad_dtype, prescale, inv_scale, found_inf), async_op)
+        """:meth:`ResidentGroup.all_reduce_unpack_wide` over the mapped rows; two-shot as in
+        :meth:`all_reduce_unpack`, the peers' reduced shares copied in the bucket dtype."""
+        if self.algorithm == "one_shot":
+            return self._one_shot(lambda: ResidentGroup.all_reduce_unpack_wide(
+                self, wire, bucket, runs, grad_dtype, prescale, inv_scale, found_inf), async_op)
+        self._check_open()
+        _native.require_device_tensor(wire, "all_reduce input")
+        arena, off = self._locate(wire)
+        rows = [p + off * arena.esize for p in arena.row_ptrs]
+        outs = self._target_rows(bucket, bucket.dtype, wire.numel())
+        wcode, bcode, pre = _native.dtype_code(arena.dtype), _native.dtype_code(bucket.dtype), _native.f32(prescale)
+        return self._two_shot_unpack(rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op,
+                                     lambda part, out, gcode, inv, flag, st: _native.allreduce_unpack_wide(
+                                         rows, wcode, part, out, bcode, gcode, pre, inv, flag, st), bcode)
+
+    def _two_shot_unpack(self, rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op, reduce_unpack,
+                         out_code):
+        gcode, gsize = _native.dtype_code(grad_dtype), torch.empty((), dtype=grad_dtype).element_size()
+        inv, flag = _native.f32(inv_scale), (found_inf.data_ptr() if found_inf is not None else None)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        me = self._rank
+        return self._two_shot(
+            *self._runs_extent(runs),
+            lambda a, b: reduce_unpack(clip_grad_runs(runs, a, b, gsize), outs[me], gcode, inv, flag, stream),
+            lambda j, a, b: _native.allreduce_unpack(
+                [outs[j]], out_code, clip_grad_runs(runs, a, b, gsize), outs[me], gcode, inv, flag, stream),
+            async_op,
+        )
+
+    def _one_shot_only(self, what: str) -> None:
+        if self.algorithm != "one_shot":
+            raise NotImplementedError(f"IpcGroup: {what} is one-shot only (a two-shot group reduces "
+                                      "through kernel-argument tables: the shares differ from rank to rank)")
+
+    def plan_all_reduce_unpack(self, *args, **kwargs):
+        self._one_shot_only("plan_all_reduce_unpack")
+        return super().plan_all_reduce_unpack(*args, **kwargs)
+
+    def plan_all_reduce_unpack_wide(self, *args, **kwargs):
+        self._one_shot_only("plan_all_reduce_unpack_wide")
+        return super().plan_all_reduce_unpack_wide(*args, **kwargs)
 
     def all_reduce_unpack_planned(self, plan, device, inv_scale=1.0, found_inf=None, async_op=False):
+        self._one_shot_only("all_reduce_unpack_planned")
         return self._one_shot(lambda: ResidentGroup.all_reduce_unpack_planned(
             self, plan, device, inv_scale, found_inf), async_op)
 

@@ -316,6 +316,80 @@ def test_bucket_spans_are_the_oracle_partition():
                 assert [[n - 1 - j for j in range(a, b)] for a, b in spans] == want, (sizes, cap_mb)
 
 
+def test_two_shot_shares_partition_the_extent():
+    """Every element of [lo, hi) belongs to exactly one rank's share, shares follow rank order,
+    and every share but the last non-empty one is a whole number of align elements; checked
+    element by element against ceil-sized blocks of the extent."""
+    rng = np.random.default_rng(3)
+    cases = [(0, 0, 4, 64), (5, 5, 3, 64), (0, 1, 8, 64), (10, 11, 1, 64), (0, 64 * 8, 8, 64),
+             (0, 64 * 8 + 1, 8, 64), (7, 1000, 3, 64), (0, 100, 16, 1)]
+    cases += [(int(lo), int(lo + n), int(w), int(a)) for lo, n, w, a in
+              zip(rng.integers(0, 10**6, 200), rng.integers(0, 5000, 200), rng.integers(1, 17, 200),
+                  rng.choice([1, 4, 64, 128], 200))]
+    for lo, hi, world, align in cases:
+        shares = comm.two_shot_shares(lo, hi, world, align)
+        assert len(shares) == world
+        block = -(-(hi - lo) // (world * align)) * align  # elements per share, rounded up to align
+        owner = np.full(hi - lo, -1)
+        for j, (a, b) in enumerate(shares):
+            assert lo <= a <= b <= hi
+            assert (owner[a - lo : b - lo] == -1).all()
+            owner[a - lo : b - lo] = j
+            if b < hi:
+                assert (b - a) % align == 0
+        want = (np.arange(hi - lo) // block) if hi > lo else np.zeros(0, int)
+        assert (owner == want).all(), (lo, hi, world, align)
+        assert [a for a, _ in shares] == sorted(a for a, _ in shares)
+
+
+def test_clip_grad_runs_against_element_map():
+    """The clipped parts of a run table address exactly the window's elements, each at its own
+    gradient byte (0 = no gradient stays 0), in run order; the parts over every share of a
+    two-shot extent put every element of every run back exactly once."""
+    rng = np.random.default_rng(11)
+    for trial in range(60):
+        n_runs = int(rng.integers(0, 12))
+        rows, pos = [], int(rng.integers(0, 50))
+        for _ in range(n_runs):
+            pos += int(rng.integers(0, 9))  # gaps between runs (bucket padding)
+            n = int(rng.integers(0, 300))
+            grad = 0 if rng.random() < 0.2 else int(rng.integers(1, 2**40)) * 256
+            rows.append((pos, n, grad))
+            pos += n
+        runs = nat.grad_runs_array(rows)
+        esize = int(rng.choice([2, 4]))
+
+        def element_map(table):
+            m = {}
+            for off, n, g in table.tolist():
+                for k in range(n):
+                    assert off + k not in m
+                    m[off + k] = 0 if g == 0 else g + k * esize
+            return m
+
+        full = element_map(runs)
+        lo = int(rng.integers(0, pos + 2))
+        hi = int(rng.integers(lo, pos + 3))
+        part = comm.clip_grad_runs(runs, lo, hi, esize)
+        assert part.dtype == nat.GRAD_RUN_DTYPE and (part["numel"] > 0).all()
+        assert list(part["offset"]) == sorted(part["offset"])
+        assert element_map(part) == {i: g for i, g in full.items() if lo <= i < hi}
+        if full:
+            xlo, xhi = min(full), max(full) + 1
+            world = int(rng.integers(1, 9))
+            merged: dict[int, int] = {}
+            for a, b in comm.two_shot_shares(xlo, xhi, world, 64):
+                got = element_map(comm.clip_grad_runs(runs, a, b, esize))
+                assert not set(got) & set(merged)
+                merged.update(got)
+            assert merged == full
+
+
+def test_ipc_group_checks_its_algorithm():
+    with pytest.raises(ValueError, match="algorithm"):
+        comm.IpcGroup(None, "cpu", algorithm="ring")
+
+
 def test_fsdp_unit_batch_is_checked():
     """unit_batch must be a positive int (rejected before any work)."""
     from minidist import FSDP

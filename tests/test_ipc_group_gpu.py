@@ -1,13 +1,15 @@
-"""The one-shot all-reduce over IPC-mapped rows: W processes on the one GPU (comm.IpcGroup).
+"""All-reduces over IPC-mapped rows: W processes on the one GPU (comm.IpcGroup).
 
 W processes (2, 3 or 4, all on ``cuda:0``) meet in a gloo group, which carries
 only host traffic: the IPC handles of each rank's contribution rows and the
-barriers of the one-shot protocol.  DDP over an ``IpcGroup`` packs each rank's
+barriers of the protocol.  DDP over an ``IpcGroup`` packs each rank's
 gradients into its own row (``mdx_pack``, x 1/W), and after every rank's pack
 is done each rank runs the fused rank-ordered reduction + unpack + unscale +
-found-inf over all W rows -- its peers' rows read through their IPC mappings
--- so every rank computes the whole average itself.  The reference hands each
-bucket to ``dist.all_reduce`` (minidist/comm.py:223-234, ddp.py:243-274).
+found-inf over the W rows -- its peers' rows read through their IPC mappings.
+One-shot: every rank reduces the whole bucket run itself.  Two-shot: every
+rank reduces its 1/W share into its (symmetric) bucket, and after a second
+barrier unpacks its peers' shares out of their buckets.  The reference hands
+each bucket to ``dist.all_reduce`` (minidist/comm.py:223-234, ddp.py:243-274).
 
 Every rank's gradients are checked bit for bit against the oracle's
 rank-ordered pipeline over all ranks' seeded gradients, for two steps: the
@@ -52,14 +54,14 @@ def _host_bits(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
 
-def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str) -> None:
+def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, algorithm: str) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
     dtype = DTYPES[dtype_name]
     try:
-        group = IpcGroup(dist.group.WORLD, dev)
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm)
         specs = wl.gpt_specs(**CFG, dtype=dtype)
         model = wl.SpecModule(specs, dev)
         params = list(model.parameters())
@@ -87,6 +89,9 @@ def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str) ->
             out[f"found_{step}"] = np.array(found)
             for i, p in enumerate(params):
                 out[f"grad_{step}_{i}"] = _host_bits(p.grad)
+        if algorithm == "two_shot":  # the peers read each rank's reduced share out of its buckets
+            for b in ddp._buckets:
+                group._rows_of(b.buffer)  # raises unless the bucket lies in a symmetric buffer
         if dtype == torch.float32:
             # the reference's own per-bucket sequence over the same group: gather_into_buffer,
             # comm.all_reduce (one-shot SUM of the rows into the bucket), scatter_from_buffer
@@ -104,13 +109,19 @@ def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str) ->
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world,dtype", [(2, "f32"), (3, "f32"), (4, "f32"), (2, "bf16"), (4, "bf16")])
-def test_ipc_one_shot_all_reduce_bitwise(tmp_path, world, dtype):
+@pytest.mark.parametrize("world,dtype,algorithm",
+                         [(2, "f32", "one_shot"), (3, "f32", "one_shot"), (4, "f32", "one_shot"),
+                          (2, "bf16", "one_shot"), (4, "bf16", "one_shot"), (2, "f32", "two_shot"),
+                          (3, "f32", "two_shot"), (4, "f32", "two_shot"), (3, "bf16", "two_shot"),
+                          (4, "bf16", "two_shot")])
+def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm):
     """fp32 gradients into fp32 buckets, or bf16 gradients into fp32 buckets with bf16 rows; in fp32
-    also the reference's per-bucket sequence through comm.all_reduce over the group."""
+    also the reference's per-bucket sequence through comm.all_reduce over the group.  Two-shot:
+    each rank reduces and unpacks its share of every bucket run, then unpacks its peers' shares
+    out of their (symmetric) buckets."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (IpcGroup one-shot all-reduce, {dtype})", flush=True)
-    mp.spawn(_worker, args=(world, store, str(tmp_path), dtype), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} all-reduce, {dtype})", flush=True)
+    mp.spawn(_worker, args=(world, store, str(tmp_path), dtype, algorithm), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_r{r}.npz", allow_pickle=False) as d:
@@ -158,13 +169,13 @@ def _rs_rows(rank: int, world: int) -> np.ndarray:
     return (np.random.default_rng(991 + rank).standard_normal(RS_S * world) * 1e2).astype(np.float32)
 
 
-def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm: str) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
     try:
-        group = IpcGroup(dist.group.WORLD, dev)
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm)
         rows = [group.zeros(n, torch.float32) for n in SMALL]
         out = {"mapped": np.array(len(group._mapped))}
         for step in range(2):
@@ -198,15 +209,15 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str) -> None:
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world", [2, 3])
-def test_ipc_in_place_all_reduce(tmp_path, world):
+@pytest.mark.parametrize("world,algorithm", [(2, "one_shot"), (3, "one_shot"), (2, "two_shot"), (3, "two_shot")])
+def test_ipc_in_place_all_reduce(tmp_path, world, algorithm):
     """``comm.all_reduce`` in place on rows of an IpcGroup buffer with no reduce target: every rank
     ends with the rank-ordered sum while its peers read its row concurrently; a peer allocation
     that holds two rows is mapped once.  Then ``comm.reduce_scatter_tensor`` and
     ``comm.all_gather_into_tensor`` over symmetric rows."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (IpcGroup in-place all-reduce)", flush=True)
-    mp.spawn(_in_place_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} in-place all-reduce)", flush=True)
+    mp.spawn(_in_place_worker, args=(world, store, str(tmp_path), algorithm), nprocs=world, join=True)
     for step in range(2):
         hosts = [_small_rows(r, step) for r in range(world)]
         for k in range(len(SMALL)):
@@ -334,13 +345,14 @@ def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulat
 BACKWARD_CAP_MB = 0.01  # several bucket runs, launched while backward runs
 
 
-def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str, comm_stream: bool = False) -> None:
+def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str, comm_stream: bool = False,
+                         algorithm: str = "one_shot") -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
     try:
-        group = IpcGroup(dist.group.WORLD, dev)
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm)
         c = tiny_gpt.Config(n_layer=2)
         model = tiny_gpt.GPT(c, seed=rank).to(dev)  # the construction broadcast makes them rank 0's
         params = list(model.parameters())
@@ -380,17 +392,20 @@ def _ddp_backward_worker(rank: int, world: int, store: str, out_dir: str, comm_s
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world,comm_stream", [(2, False), (3, False), (2, True)])
-def test_ipc_ddp_during_backward_bitwise(tmp_path, world, comm_stream):
+@pytest.mark.parametrize("world,comm_stream,algorithm",
+                         [(2, False, "one_shot"), (3, False, "one_shot"), (2, True, "one_shot"),
+                          (3, False, "two_shot"), (2, True, "two_shot")])
+def test_ipc_ddp_during_backward_bitwise(tmp_path, world, comm_stream, algorithm):
     """DDP over an IpcGroup inside a real backward: bucket runs launch from the autograd hooks as
     they fill (pack, fences, the one-shot reduction over the mapped rows), two steps, the second
     with an overflow on one rank that every rank must skip.  Every rank's gradients against the
     oracle's pipeline over all ranks' captured local gradients.  ``comm_stream``: the packs, fences
     and reductions on DDP's dedicated stream."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (DDP over an IpcGroup, real backward, comm_stream={comm_stream})",
-          flush=True)
-    mp.spawn(_ddp_backward_worker, args=(world, store, str(tmp_path), comm_stream), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (DDP over an {algorithm} IpcGroup, real backward, "
+          f"comm_stream={comm_stream})", flush=True)
+    mp.spawn(_ddp_backward_worker, args=(world, store, str(tmp_path), comm_stream, algorithm), nprocs=world,
+             join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_bwd_r{r}.npz", allow_pickle=False) as d:
