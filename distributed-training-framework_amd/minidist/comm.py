@@ -253,6 +253,25 @@ def two_shot_shares(lo: int, hi: int, world: int, align: int = _SHARE_ALIGN_ELEM
     return [(min(lo + j * step, hi), min(lo + (j + 1) * step, hi)) if hi > lo else (lo, lo) for j in range(world)]
 
 
+# A copy from several peers' memory goes out in chunks of this size, taken round-robin across
+# the peers: a dispatch's workgroups run roughly in grid order, so spans in peer order would
+# read one peer -- one xGMI link, across GPUs -- at a time.
+_GATHER_CHUNK_BYTES = 1 << 20
+
+
+def interleave_spans(spans: list[tuple[int, int, int]], src_esize: int, dst_esize: int,
+                     chunk_bytes: int = _GATHER_CHUNK_BYTES) -> list[tuple[int, int, int]]:
+    """``spans`` (src, dst, numel) cut into chunks of at most ``chunk_bytes`` of source and
+    ordered round-robin: the first chunk of every span, then the second of every span, ..."""
+    step = max(1, chunk_bytes // src_esize)
+    chunks = [[(s + k * src_esize, d + k * dst_esize, min(step, n - k)) for k in range(0, n, step)]
+              for s, d, n in spans]
+    out = []
+    for i in range(max((len(c) for c in chunks), default=0)):
+        out.extend(c[i] for c in chunks if i < len(c))
+    return out
+
+
 def clip_grad_runs(runs: np.ndarray, lo: int, hi: int, grad_esize: int) -> np.ndarray:
     """The parts of an ``mdx_grad_run`` table that fall in ``[lo, hi)``.
 
@@ -648,11 +667,16 @@ class ResidentGroup:
         if output.numel() != S * self._world or output.dtype != input_.dtype:
             raise ValueError("all_gather: output must hold world_size inputs of the same dtype")
         es, base = input_.element_size(), output.data_ptr()
-        spans = [(rows[r], base + r * S * es, S) for r in range(self._world)]
+        spans = self._gather_order([(rows[r], base + r * S * es, S) for r in range(self._world)], es)
         code = _native.dtype_code(input_.dtype)
         stream = torch.cuda.current_stream(input_.device)
         _native.pack(_native.spans_array(spans), code, code, 1.0, False, stream.cuda_stream)
         return StreamWork(stream) if async_op else None
+
+    @staticmethod
+    def _gather_order(spans: list[tuple[int, int, int]], esize: int) -> list[tuple[int, int, int]]:
+        """The order a gather copies its spans in (the rows are all local here: as given)."""
+        return spans
 
 
 class _IpcArena:
@@ -852,19 +876,29 @@ class IpcGroup(ResidentGroup):
                 f"(starts {lo_min}..{lo_max}, ends {hi_min}..{hi_max})"
             )
 
-    def _two_shot(self, lo: int, hi: int, reduce_share, copy_share, async_op: bool):
-        """The two rounds over the elements [lo, hi): ``reduce_share(a, b)`` reduces this
-        rank's share from all W rows into its target; ``copy_share(j, a, b)`` takes peer
-        j's reduced share out of peer j's target."""
+    def _two_shot(self, runs: np.ndarray, esize: int, outs: list[int], code: int, reduce_share, after_gather,
+                  async_op: bool):
+        """The two rounds over the extent of ``runs`` (an ``mdx_grad_run`` table) in targets
+        ``outs`` (every rank's address of element 0, ``esize`` bytes per element):
+        ``reduce_share(a, b)`` reduces this rank's share [a, b) from all W rows into its target;
+        then the runs' elements in every peer's share are copied out of that peer's target into
+        this rank's (one copy over all peers, in interleaved chunks), and
+        ``after_gather(peer_shares)`` runs on the peers' [a, b) ranges."""
+        lo, hi = self._runs_extent(runs)
         shares = two_shot_shares(lo, hi, self._world)
+        me = self._rank
         self._extent_agreed(lo, hi)  # every row is written
-        a, b = shares[self._rank]
+        a, b = shares[me]
         if b > a:
             reduce_share(a, b)
         self.rows_written()  # every share is reduced (and no peer reads a row any more)
-        for j, (a, b) in enumerate(shares):
-            if j != self._rank and b > a:
-                copy_share(j, a, b)
+        peer_shares = [(j, a, b) for j, (a, b) in enumerate(shares) if j != me and b > a]
+        spans = [(outs[j] + o * esize, outs[me] + o * esize, n)
+                 for j, a, b in peer_shares for o, n, _ in clip_grad_runs(runs, a, b, 0).tolist()]
+        if spans:
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            _native.pack(_native.spans_array(interleave_spans(spans, esize, esize)), code, code, 1.0, False, stream)
+            after_gather([(a, b) for _, a, b in peer_shares])
         self.rows_read()  # no peer reads this rank's target any more
         return _CompletedWork() if async_op else None
 
@@ -905,25 +939,19 @@ class IpcGroup(ResidentGroup):
             arena, off = self._locate(t)
             by_arena.setdefault(id(arena), (arena, []))[1].append((off, t.numel(), 0))
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        me = self._rank
         work = None
         for arena, parts in by_arena.values():
             runs = _native.grad_runs_array(sorted(parts))
             rows = arena.row_ptrs
             outs = rows if arena.target is None else self._target_rows(arena.target, arena.dtype, arena.numel)
-            code, es = _native.dtype_code(arena.dtype), arena.esize
+            code = _native.dtype_code(arena.dtype)
 
             def reduce_share(a, b, runs=runs, rows=rows, outs=outs, code=code):
                 part = clip_grad_runs(runs, a, b, 0)
-                _native.allreduce_sum(rows, code, part["offset"].tolist(), part["numel"].tolist(), outs[me], stream)
+                _native.allreduce_sum(rows, code, part["offset"].tolist(), part["numel"].tolist(),
+                                      outs[self._rank], stream)
 
-            def copy_share(j, a, b, runs=runs, outs=outs, code=code, es=es):
-                part = clip_grad_runs(runs, a, b, 0)
-                spans = [(outs[j] + o * es, outs[me] + o * es, n)
-                         for o, n in zip(part["offset"].tolist(), part["numel"].tolist())]
-                _native.pack(_native.spans_array(spans), code, code, 1.0, False, stream)
-
-            work = self._two_shot(*self._runs_extent(runs), reduce_share, copy_share, async_op)
+            work = self._two_shot(runs, arena.esize, outs, code, reduce_share, lambda peer_shares: None, async_op)
         return work
 
     def all_reduce_unpack(self, buffer, runs, grad_dtype, inv_scale=1.0, found_inf=None, async_op=False,
@@ -941,9 +969,9 @@ class IpcGroup(ResidentGroup):
         rows = [p + off * arena.esize for p in arena.row_ptrs]
         outs = rows if bucket is None else self._target_rows(bucket, buffer.dtype, buffer.numel())
         code = _native.dtype_code(arena.dtype)
-        return self._two_shot_unpack(rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op,
+        return self._two_shot_unpack(outs, runs, grad_dtype, inv_scale, found_inf, async_op,
                                      lambda part, out, gcode, inv, flag, st: _native.allreduce_unpack(
-                                         rows, code, part, out, gcode, inv, flag, st), code)
+                                         rows, code, part, out, gcode, inv, flag, st), arena.dtype)
 
     def all_reduce_unpack_wide(self, wire, bucket, runs, grad_dtype, prescale, inv_scale=1.0, found_inf=None,
                                async_op=False):
@@ -958,22 +986,29 @@ class IpcGroup(ResidentGroup):
         rows = [p + off * arena.esize for p in arena.row_ptrs]
         outs = self._target_rows(bucket, bucket.dtype, wire.numel())
         wcode, bcode, pre = _native.dtype_code(arena.dtype), _native.dtype_code(bucket.dtype), _native.f32(prescale)
-        return self._two_shot_unpack(rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op,
+        return self._two_shot_unpack(outs, runs, grad_dtype, inv_scale, found_inf, async_op,
                                      lambda part, out, gcode, inv, flag, st: _native.allreduce_unpack_wide(
-                                         rows, wcode, part, out, bcode, gcode, pre, inv, flag, st), bcode)
+                                         rows, wcode, part, out, bcode, gcode, pre, inv, flag, st), bucket.dtype)
 
-    def _two_shot_unpack(self, rows, outs, runs, grad_dtype, inv_scale, found_inf, async_op, reduce_unpack,
-                         out_code):
+    def _two_shot_unpack(self, outs, runs, grad_dtype, inv_scale, found_inf, async_op, reduce_unpack,
+                         out_dtype: torch.dtype):
+        out_code, osize = _native.dtype_code(out_dtype), torch.empty((), dtype=out_dtype).element_size()
         gcode, gsize = _native.dtype_code(grad_dtype), torch.empty((), dtype=grad_dtype).element_size()
         inv, flag = _native.f32(inv_scale), (found_inf.data_ptr() if found_inf is not None else None)
         stream = torch.cuda.current_stream(self.device).cuda_stream
         me = self._rank
+
+        def unpack_peer_shares(peer_shares):
+            # the copied sums -> the gradients they cover (the fused kernel's unpack epilogue)
+            spans = [(outs[me] + o * osize, g, n) for a, b in peer_shares
+                     for o, n, g in clip_grad_runs(runs, a, b, gsize).tolist()]
+            if spans:
+                _native.unpack(_native.spans_array(spans), out_code, gcode, inv, flag, stream)
+
         return self._two_shot(
-            *self._runs_extent(runs),
+            runs, osize, outs, out_code,
             lambda a, b: reduce_unpack(clip_grad_runs(runs, a, b, gsize), outs[me], gcode, inv, flag, stream),
-            lambda j, a, b: _native.allreduce_unpack(
-                [outs[j]], out_code, clip_grad_runs(runs, a, b, gsize), outs[me], gcode, inv, flag, stream),
-            async_op,
+            unpack_peer_shares, async_op,
         )
 
     def _one_shot_only(self, what: str) -> None:
@@ -1004,6 +1039,11 @@ class IpcGroup(ResidentGroup):
         of a symmetric buffer), read one-shot from the mapped rows."""
         self._check_open()
         return self._one_shot(lambda: ResidentGroup.reduce_scatter_sum(self, output, input_), async_op)
+
+    @staticmethod
+    def _gather_order(spans: list[tuple[int, int, int]], esize: int) -> list[tuple[int, int, int]]:
+        """Peers' rows are read in interleaved chunks, so that one copy draws on every peer at once."""
+        return interleave_spans(spans, esize, esize)
 
     def all_gather_into(self, output, input_, async_op: bool = False):
         """``output[r*S:(r+1)*S]`` = rank r's ``input_`` (a row of a symmetric buffer), copied

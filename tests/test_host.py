@@ -385,6 +385,29 @@ def test_clip_grad_runs_against_element_map():
             assert merged == full
 
 
+def test_interleave_spans_covers_each_span_in_round_robin_chunks():
+    """Chunks copy exactly the bytes of the spans (each source byte to its own destination byte),
+    none longer than the chunk size, ordered round-robin across the spans."""
+    rng = np.random.default_rng(5)
+    for trial in range(80):
+        ses, des = int(rng.choice([1, 2, 4])), int(rng.choice([1, 2, 4]))
+        chunk = int(rng.choice([1, 8, 64, 1000]))
+        spans = [(int(rng.integers(1, 2**30)) * 8, int(rng.integers(1, 2**30)) * 8, int(rng.integers(0, 700)))
+                 for _ in range(int(rng.integers(0, 6)))]
+        out = comm.interleave_spans(spans, ses, des, chunk)
+        step = max(1, chunk // ses)
+        assert all(0 < n <= step for _, _, n in out)
+        want = {(s + k * ses, d + k * des) for s, d, n in spans for k in range(n)}
+        got = [(s + k * ses, d + k * des) for s, d, n in out for k in range(n)]
+        assert len(got) == len(set(got)) and set(got) == want
+        # round-robin: (chunk index, span index) of the output chunks increases lexicographically
+        order = []
+        for s, d, n in out:
+            j = next(j for j, (s0, d0, n0) in enumerate(spans) if s0 <= s < s0 + n0 * ses and d - d0 == (s - s0) // ses * des)
+            order.append(((s - spans[j][0]) // ses // step, j))
+        assert order == sorted(order) and len(set(order)) == len(order)
+
+
 def test_ipc_group_checks_its_algorithm():
     with pytest.raises(ValueError, match="algorithm"):
         comm.IpcGroup(None, "cpu", algorithm="ring")
