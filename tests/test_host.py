@@ -413,6 +413,21 @@ def test_ipc_group_checks_its_algorithm():
         comm.IpcGroup(None, "cpu", algorithm="ring")
 
 
+def test_ddp_refuses_graph_capture_over_an_ipc_group(tmp_path):
+    """An IpcGroup's collectives wait on the host for the peers: no graph can hold them, so DDP
+    refuses capture_graphs over one before anything is allocated (a one-rank gloo group here)."""
+    import torch.distributed as dist
+
+    dist.init_process_group("gloo", init_method=f"file://{tmp_path / 'store'}", rank=0, world_size=1)
+    try:
+        group = comm.IpcGroup(dist.group.WORLD, "cpu")
+        assert "two_shot" not in repr(group) and group.plans_reductions and not group.symmetric_targets
+        with pytest.raises(ValueError, match="not an IpcGroup"):
+            DistributedDataParallel(nn.Linear(2, 2), process_group=group, capture_graphs=True)
+    finally:
+        dist.destroy_process_group()
+
+
 def test_fsdp_unit_batch_is_checked():
     """unit_batch must be a positive int (rejected before any work)."""
     from minidist import FSDP
