@@ -154,7 +154,10 @@ def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm):
     print("step ms per rank:", [[float(res[r][f"ms_{s}"]) for s in range(2)] for r in range(world)], flush=True)
 
 
-SMALL = (1000, 3000)  # two small symmetric buffers: the caching allocator may carve both out of one segment
+SMALL = (1000, 3000, 3000, 100)  # small symmetric buffers: the caching allocator may carve several out of
+# one segment.  Buffer 2 is reduced in two views with a gap between them, which keeps each rank's own
+# data; buffer 3 is small enough that a two-shot group of three gives one rank an empty share.
+GAP = (1000, 2000)
 
 
 def _small_rows(rank: int, step: int) -> list[np.ndarray]:
@@ -183,6 +186,8 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm:
                 row.copy_(torch.from_numpy(host).to(dev))
             comm.all_reduce(rows[0], group=group)  # in place, one buffer
             comm.all_reduce_coalesced([rows[1][:1500], rows[1][1500:]], group=group)  # two views of the other
+            comm.all_reduce_coalesced([rows[2][: GAP[0]], rows[2][GAP[1] :]], group=group)  # views with a gap
+            comm.all_reduce(rows[3], group=group)
             for k, row in enumerate(rows):
                 out[f"sum_{step}_{k}"] = row.cpu().numpy()
         # comm.reduce_scatter_tensor / all_gather_into_tensor (reference comm.py:237-265) over the rows
@@ -212,19 +217,23 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm:
 @pytest.mark.parametrize("world,algorithm", [(2, "one_shot"), (3, "one_shot"), (2, "two_shot"), (3, "two_shot")])
 def test_ipc_in_place_all_reduce(tmp_path, world, algorithm):
     """``comm.all_reduce`` in place on rows of an IpcGroup buffer with no reduce target: every rank
-    ends with the rank-ordered sum while its peers read its row concurrently; a peer allocation
-    that holds two rows is mapped once.  Then ``comm.reduce_scatter_tensor`` and
-    ``comm.all_gather_into_tensor`` over symmetric rows."""
+    ends with the rank-ordered sum while its peers read its row concurrently, elements between
+    reduced views keep each rank's own data, and a peer allocation that holds several rows is
+    mapped once.  Then ``comm.reduce_scatter_tensor`` and ``comm.all_gather_into_tensor`` over
+    symmetric rows."""
     store = str(tmp_path / "store")
     print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} in-place all-reduce)", flush=True)
     mp.spawn(_in_place_worker, args=(world, store, str(tmp_path), algorithm), nprocs=world, join=True)
     for step in range(2):
         hosts = [_small_rows(r, step) for r in range(world)]
         for k in range(len(SMALL)):
-            want = hosts[0][k].copy()
+            total = hosts[0][k].copy()
             for r in range(1, world):
-                want = want + hosts[r][k]  # float32, rank order 0..W-1
+                total = total + hosts[r][k]  # float32, rank order 0..W-1
             for rank in range(world):
+                want = total.copy()
+                if k == 2:  # outside the reduced views each rank keeps its own data
+                    want[GAP[0] : GAP[1]] = hosts[rank][k][GAP[0] : GAP[1]]
                 with np.load(tmp_path / f"inplace_r{rank}.npz", allow_pickle=False) as d:
                     got = d[f"sum_{step}_{k}"]
                     assert int(d["mapped"]) <= len(SMALL) * (world - 1)
