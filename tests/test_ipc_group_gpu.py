@@ -432,3 +432,62 @@ def test_ipc_ddp_during_backward_bitwise(tmp_path, world, comm_stream, algorithm
                 got = res[rank][f"final_{step}_{i}"]
                 assert same_bits(got, want["grads"][i]), (
                     f"step {step} rank {rank} param {i}: " + first_mismatch(got, want["grads"][i]))
+
+
+def _full_size_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=120))
+    try:
+        groups = {a: IpcGroup(dist.group.WORLD, dev, algorithm=a) for a in IpcGroup.ALGORITHMS}
+        specs = wl.gpt_specs(**wl.GPT2_SMALL)
+        model = wl.SpecModule(specs, dev)
+        params = list(model.parameters())
+        gen = torch.Generator(device=dev).manual_seed(4321 + 17 * rank)
+        inputs = [torch.randn(p.shape, device=dev, generator=gen) * (1e-3 * SCALE) for p in params]
+        if rank == world - 1:
+            inputs[7].view(-1)[inputs[7].numel() // 2] = float("inf")  # one rank overflowed: both must flag it
+        out = {}
+        results = {}
+        for name, group in groups.items():
+            scaler = DistributedGradScaler(init_scale=SCALE, process_group=group)
+            ddp = DDP(model, process_group=group, grad_scaler=scaler, broadcast_parameters=False)
+
+            class _Opt:
+                param_groups = [{"params": params}]
+
+            for p, g in zip(params, inputs, strict=True):
+                p.grad = g.clone()
+            ddp.finish_gradient_sync()
+            out[f"found_{name}"] = np.array(scaler.unscale_(_Opt()))
+            out[f"buckets_{name}"] = np.array(len(ddp._buckets))
+            results[name] = [p.grad.detach().clone() for p in params]
+            out[f"bucket_sum_{name}"] = np.array(sum(float(b.buffer.double().nan_to_num(0.0, 0.0, 0.0).sum())
+                                                     for b in ddp._buckets))
+            del ddp
+        one, two = results["one_shot"], results["two_shot"]
+        out["equal"] = np.array(all(torch.equal(a.view(torch.int32), b.view(torch.int32))
+                                    for a, b in zip(one, two, strict=True)))
+        for group in groups.values():
+            group.release()
+        np.savez(os.path.join(out_dir, f"full_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+def test_ipc_two_shot_equals_one_shot_at_cfg1_size(tmp_path):
+    """cfg1's 124M fp32 gradients (148 tensors, 18 buckets in one run of 148 kernel-argument
+    runs), two processes: the two-shot all-reduce gives every rank exactly the one-shot's
+    gradients (which the oracle pins at small sizes), bit for bit, with an inf in one rank's
+    gradient flagged on both."""
+    world = 2
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (one-shot against two-shot at cfg1 size)", flush=True)
+    mp.spawn(_full_size_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    for rank in range(world):
+        with np.load(tmp_path / f"full_r{rank}.npz", allow_pickle=False) as d:
+            assert int(d["buckets_one_shot"]) == int(d["buckets_two_shot"]) == 18
+            assert bool(d["found_one_shot"]) and bool(d["found_two_shot"])
+            assert bool(d["equal"]), f"rank {rank}: two-shot gradients differ from one-shot"
+            assert float(d["bucket_sum_one_shot"]) == float(d["bucket_sum_two_shot"])
