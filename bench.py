@@ -303,7 +303,7 @@ def bench_ddp(name: str, args) -> dict:
         """--staged: the W-way sum of the contribution rows into the buckets (one mdx_allreduce_sum)."""
         from minidist import _native
 
-        wire, flat = ddp._arenas[(ddp._buckets[0].wire_dtype, ddp._buckets[0].dtype)]
+        wire, flat = ddp._arenas[(ddp._buckets[0].wire_dtype, ddp._buckets[0].dtype, 0)]
         rows = group.replicas(wire)
         _native.allreduce_sum(
             [r.data_ptr() for r in rows], _native.dtype_code(wire.dtype), [b.arena_offset for b in ddp._buckets],

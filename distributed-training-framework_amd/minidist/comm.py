@@ -708,7 +708,9 @@ class IpcGroup(ResidentGroup):
     The multi-GPU design of this path, runnable here with W processes sharing
     the one GPU: each rank allocates its row of every symmetric buffer
     (:meth:`zeros`, each row an allocation below 2 GiB), exports it over IPC,
-    and maps its peers' rows.  The all-reduces run one of two ways
+    and maps its peers' rows.  DDP and FSDP keep every symmetric buffer within
+    ``segment_bytes`` (a model's buckets or units spread over several buffers
+    when they need more).  The all-reduces run one of two ways
     (``algorithm``), both with the same rank-ordered kernels a
     :class:`ResidentGroup` uses, so every rank ends with bit-identical
     results.  The reference hands each bucket to ``dist.all_reduce`` instead
@@ -739,11 +741,18 @@ class IpcGroup(ResidentGroup):
     fuses_pack = False
     ALGORITHMS = ("one_shot", "two_shot")
 
-    def __init__(self, process_group=None, device: torch.device | str | None = None, algorithm: str = "one_shot"):
+    def __init__(self, process_group=None, device: torch.device | str | None = None, algorithm: str = "one_shot",
+                 segment_bytes: int = 1 << 30):
         if algorithm not in self.ALGORITHMS:
             raise ValueError(f"IpcGroup: algorithm must be one of {self.ALGORITHMS}, got {algorithm!r}")
+        if not 0 < segment_bytes <= _native.IPC_MAX_ALLOC_BYTES // 2:
+            raise ValueError(f"IpcGroup: segment_bytes must be in (0, {_native.IPC_MAX_ALLOC_BYTES // 2}], "
+                             f"got {segment_bytes}")
         self.process_group = process_group
         self.algorithm = algorithm
+        # A row is one allocation, exported whole; DDP and FSDP split their symmetric buffers
+        # into segments of at most this many bytes (the runtime maps allocations below 2 GiB).
+        self.segment_bytes = segment_bytes
         # Two-shot: peers read each rank's reduced share out of its reduce target, so DDP
         # allocates its buckets as symmetric buffers, and reductions run through the
         # kernel-argument tables (a share is a different slice of the runs on every rank).

@@ -408,9 +408,42 @@ def test_interleave_spans_covers_each_span_in_round_robin_chunks():
         assert order == sorted(order) and len(set(order)) == len(order)
 
 
+def test_ddp_segments_bound_each_allocation():
+    """Buckets grouped into allocations of at most ``limit`` bytes: in order, every bucket once at an
+    aligned offset, no segment over the limit, a new segment only when the next bucket would not
+    fit; one allocation without a limit; a bucket larger than the limit refused."""
+    from minidist.ddp import _Bucket, _segments
+
+    rng = np.random.default_rng(9)
+    for trial in range(200):
+        n = int(rng.integers(1, 30))
+        numels = [int(x) for x in rng.integers(1, 5000, n)]
+        buckets = [_Bucket(k, [nn.Parameter(torch.empty(m, device="meta"))]) for k, m in enumerate(numels)]
+        align, esize = int(rng.choice([64, 128])), int(rng.choice([2, 4]))
+        limit = int(rng.integers(max(numels) * esize, 4 * 5000 * esize + 1))
+        segs = _segments(buckets, align, esize, limit)
+        assert [b for seg in segs for b, _ in seg] == buckets
+        for k, seg in enumerate(segs):
+            assert seg and seg[0][1] == 0
+            assert all(off % align == 0 for _, off in seg)
+            assert all(o2 >= o1 + b1.numel for (b1, o1), (_, o2) in zip(seg, seg[1:]))
+            last, off = seg[-1]
+            assert (off + last.numel) * esize <= limit
+            if k + 1 < len(segs):  # the next segment's first bucket did not fit here
+                nxt = segs[k + 1][0][0]
+                padded_end = off + -(-last.numel // align) * align
+                assert (padded_end + nxt.numel) * esize > limit
+        assert len(_segments(buckets, align, esize, None)) == 1
+        with pytest.raises(ValueError, match="bucket_cap_mb"):
+            _segments(buckets, align, esize, max(numels) * esize - 1)
+
+
 def test_ipc_group_checks_its_algorithm():
     with pytest.raises(ValueError, match="algorithm"):
         comm.IpcGroup(None, "cpu", algorithm="ring")
+    for bad in (0, -1, 1 << 31):
+        with pytest.raises(ValueError, match="segment_bytes"):
+            comm.IpcGroup(None, "cpu", segment_bytes=bad)
 
 
 def test_ddp_refuses_graph_capture_over_an_ipc_group(tmp_path):

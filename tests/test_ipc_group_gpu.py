@@ -54,14 +54,15 @@ def _host_bits(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
 
 
-def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, algorithm: str) -> None:
+def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, algorithm: str,
+            segment_bytes: int) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
     dtype = DTYPES[dtype_name]
     try:
-        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm)
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm, segment_bytes=segment_bytes)
         specs = wl.gpt_specs(**CFG, dtype=dtype)
         model = wl.SpecModule(specs, dev)
         params = list(model.parameters())
@@ -76,6 +77,8 @@ def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, al
         host = _grads(rank, specs, dtype)
         out = {"buckets": np.array(len(ddp._buckets))}
         for step in range(2):
+            if step == 1:
+                out["segments"] = np.array(len({b.segment for b in ddp._buckets}))
             for i, (p, g) in enumerate(zip(params, host, strict=True)):
                 t = g.clone()
                 if step == 1 and (rank, i) == INF_AT[:2]:
@@ -109,19 +112,27 @@ def _worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, al
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world,dtype,algorithm",
-                         [(2, "f32", "one_shot"), (3, "f32", "one_shot"), (4, "f32", "one_shot"),
-                          (2, "bf16", "one_shot"), (4, "bf16", "one_shot"), (2, "f32", "two_shot"),
-                          (3, "f32", "two_shot"), (4, "f32", "two_shot"), (3, "bf16", "two_shot"),
-                          (4, "bf16", "two_shot")])
-def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm):
+SEGMENT = 1 << 30  # the default: the model's buckets fit one symmetric buffer per dtype
+SMALL_SEGMENT = 4 << 20  # the tiny GPT's 13.8 MB of buckets spread over several buffers
+
+
+@pytest.mark.parametrize("world,dtype,algorithm,segment_bytes",
+                         [(2, "f32", "one_shot", SEGMENT), (3, "f32", "one_shot", SEGMENT),
+                          (4, "f32", "one_shot", SEGMENT), (2, "bf16", "one_shot", SEGMENT),
+                          (4, "bf16", "one_shot", SEGMENT), (2, "f32", "two_shot", SEGMENT),
+                          (3, "f32", "two_shot", SEGMENT), (4, "f32", "two_shot", SEGMENT),
+                          (3, "bf16", "two_shot", SEGMENT), (4, "bf16", "two_shot", SEGMENT),
+                          (2, "bf16", "one_shot", SMALL_SEGMENT), (3, "f32", "two_shot", SMALL_SEGMENT)])
+def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm, segment_bytes):
     """fp32 gradients into fp32 buckets, or bf16 gradients into fp32 buckets with bf16 rows; in fp32
     also the reference's per-bucket sequence through comm.all_reduce over the group.  Two-shot:
     each rank reduces and unpacks its share of every bucket run, then unpacks its peers' shares
-    out of their (symmetric) buckets."""
+    out of their (symmetric) buckets.  A small ``segment_bytes`` spreads the buckets over several
+    symmetric buffers, each launch run then one collective per buffer."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} all-reduce, {dtype})", flush=True)
-    mp.spawn(_worker, args=(world, store, str(tmp_path), dtype, algorithm), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} all-reduce, {dtype}, "
+          f"segments of {segment_bytes} bytes)", flush=True)
+    mp.spawn(_worker, args=(world, store, str(tmp_path), dtype, algorithm, segment_bytes), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_r{r}.npz", allow_pickle=False) as d:
@@ -132,6 +143,7 @@ def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm):
     numels = [s.numel for s in specs]
     n = len(specs)
     assert int(res[0]["buckets"]) > 2
+    assert (int(res[0]["segments"]) > 2) == (segment_bytes == SMALL_SEGMENT)
     for step in range(2):
         replica = [[_host_bits(g) for g in _grads(r, specs, tdt)] for r in range(world)]
         if step == 1:
@@ -254,13 +266,13 @@ FSDP_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float1
 
 
 def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, unit_batch: int,
-                 accumulate: bool = False) -> None:
+                 accumulate: bool = False, segment_bytes: int = SEGMENT) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
                             timeout=timedelta(seconds=60))
     try:
-        group = IpcGroup(dist.group.WORLD, dev)
+        group = IpcGroup(dist.group.WORLD, dev, segment_bytes=segment_bytes)
         c = tiny_gpt.Config(n_layer=2)
         model = tiny_gpt.GPT(c, seed=rank).to(dev)  # the construction broadcast makes them rank 0's
         params = list(model.parameters())
@@ -276,7 +288,7 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
         fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=group, mixed_precision=policy,
                     unit_batch=unit_batch)
         scaler = DistributedGradScaler(init_scale=16.0, process_group=group)
-        out = {"units": np.array(len(fsdp._units))}
+        out = {"units": np.array(len(fsdp._units)), "segments": np.array(len({u.segment for u in fsdp._units}))}
         for u, unit in enumerate(fsdp._units):
             out[f"unit_{u}_params"] = np.array([index[id(p)] for p in unit.params])
         with fsdp.summon_full_params():
@@ -313,19 +325,26 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
         dist.destroy_process_group()
 
 
-@pytest.mark.parametrize("world,dtype,unit_batch,accumulate",
-                         [(2, "f32", 1, False), (3, "bf16", 1, False), (4, "bf16", 2, False), (2, "f16", 3, False),
-                          (3, "f32", 1, True), (2, "bf16", 2, True)])
-def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulate):
+# A tiny-GPT block unit is 12,704 elements (the root 4,672): 64 KB of fp32 rows put every unit in a
+# buffer of its own; 40 KB of 16-bit rows put the two blocks apart and the root with the second.
+@pytest.mark.parametrize("world,dtype,unit_batch,accumulate,segment_bytes",
+                         [(2, "f32", 1, False, SEGMENT), (3, "bf16", 1, False, SEGMENT),
+                          (4, "bf16", 2, False, SEGMENT), (2, "f16", 3, False, SEGMENT),
+                          (3, "f32", 1, True, SEGMENT), (2, "bf16", 2, True, SEGMENT),
+                          (3, "bf16", 2, False, 40_000), (2, "f32", 1, True, 64_000)])
+def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulate, segment_bytes):
     """FSDP over an IpcGroup: each unit's all-gather is its ranks' published shards copied from the
     mapped rows, its reduce-scatter the share kernel over every rank's published full-size gradient
     (the reference's fsdp.py:172-241 with comm.all_gather_into_tensor / reduce_scatter_tensor).
     Gathered parameters, every rank's shard gradient (against the oracle on the ranks' captured
     local gradients) and the found-inf flag exchanged over the host group.  ``accumulate``: two
-    half-batch backwards under ``no_sync`` and the flush of every unit at once."""
+    half-batch backwards under ``no_sync`` and the flush of every unit at once.  A small
+    ``segment_bytes`` spreads the units over several pairs of symmetric buffers."""
     store = str(tmp_path / "store")
-    print(f"spawning {world} ranks on cuda:0 (FSDP over an IpcGroup, {dtype}, unit_batch={unit_batch})", flush=True)
-    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch, accumulate), nprocs=world, join=True)
+    print(f"spawning {world} ranks on cuda:0 (FSDP over an IpcGroup, {dtype}, unit_batch={unit_batch}, "
+          f"segments of {segment_bytes} bytes)", flush=True)
+    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch, accumulate, segment_bytes),
+             nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_fsdp_r{r}.npz", allow_pickle=False) as d:
@@ -335,6 +354,7 @@ def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulat
     pdt = {"f32": o.F32, "bf16": o.BF16, "f16": o.F16}[dtype]
     n_units = int(res[0]["units"])
     assert n_units == c.n_layer + 1
+    assert int(res[0]["segments"]) == {SEGMENT: 1, 40_000: 2, 64_000: 3}[segment_bytes]
     for u in range(n_units):
         idx = [int(i) for i in res[0][f"unit_{u}_params"]]
         numels = [init0[i].size for i in idx]
