@@ -211,6 +211,14 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm:
         comm.reduce_scatter_tensor(rs_out, rs_in, group=group)
         comm.all_gather_into_tensor(ag_out, ag_in, group=group)
         out["rs"], out["ag"] = rs_out.cpu().numpy(), ag_out.cpu().numpy()
+        # ranks asking for different symmetric buffers are told so, every one of them, before any
+        # peer row is mapped
+        try:
+            group.zeros(64 + rank, torch.float32)
+        except RuntimeError as e:
+            assert "different buffers" in str(e)
+        else:
+            raise AssertionError("IpcGroup.zeros accepted rows of different sizes")
         group.release()
         # a released group maps nothing: every further use is refused, nothing is launched
         for use in (lambda: comm.all_reduce(rows[0], group=group), lambda: group.zeros(16, torch.float32),
