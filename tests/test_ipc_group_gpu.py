@@ -41,7 +41,7 @@ CFG = dict(n_layer=4, n_embd=256, vocab=1024, ctx=128)  # 52 gradients: one devi
 INF_AT = (1, 3, 17)  # (rank, parameter, element) that overflows in step 1
 
 
-DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16}
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
 
 
 def _grads(rank: int, specs, dtype: torch.dtype = torch.float32) -> list[torch.Tensor]:
@@ -122,9 +122,10 @@ SMALL_SEGMENT = 4 << 20  # the tiny GPT's 13.8 MB of buckets spread over several
                           (4, "bf16", "one_shot", SEGMENT), (2, "f32", "two_shot", SEGMENT),
                           (3, "f32", "two_shot", SEGMENT), (4, "f32", "two_shot", SEGMENT),
                           (3, "bf16", "two_shot", SEGMENT), (4, "bf16", "two_shot", SEGMENT),
-                          (2, "bf16", "one_shot", SMALL_SEGMENT), (3, "f32", "two_shot", SMALL_SEGMENT)])
+                          (2, "bf16", "one_shot", SMALL_SEGMENT), (3, "f32", "two_shot", SMALL_SEGMENT),
+                          (3, "f16", "one_shot", SEGMENT), (4, "f16", "two_shot", SMALL_SEGMENT)])
 def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm, segment_bytes):
-    """fp32 gradients into fp32 buckets, or bf16 gradients into fp32 buckets with bf16 rows; in fp32
+    """fp32 gradients into fp32 buckets, or bf16 / fp16 gradients into fp32 buckets with 16-bit rows; in fp32
     also the reference's per-bucket sequence through comm.all_reduce over the group.  Two-shot:
     each rank reduces and unpacks its share of every bucket run, then unpacks its peers' shares
     out of their (symmetric) buckets.  A small ``segment_bytes`` spreads the buckets over several
@@ -138,7 +139,7 @@ def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm, segment_bytes
         with np.load(tmp_path / f"ipc_r{r}.npz", allow_pickle=False) as d:
             res.append({k: d[k] for k in d.files})
     tdt = DTYPES[dtype]
-    odt = o.F32 if dtype == "f32" else o.BF16
+    odt = {"f32": o.F32, "bf16": o.BF16, "f16": o.F16}[dtype]
     specs = wl.gpt_specs(**CFG, dtype=tdt)
     numels = [s.numel for s in specs]
     n = len(specs)
@@ -149,7 +150,7 @@ def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm, segment_bytes
         if step == 1:
             rr, i, k = INF_AT
             replica[rr][i] = replica[rr][i].copy()
-            replica[rr][i][k] = np.inf if odt == o.F32 else np.uint16(0x7F80)
+            replica[rr][i][k] = np.uint16(0x7F80) if odt == o.BF16 else np.inf
         for rank in range(world):
             want = o.ddp_pipeline(replica, [odt] * n, numels, CAP_MB, rank, 1.0 / SCALE,
                                   bucket_dtype=o.F32)
