@@ -45,11 +45,13 @@ whose replicas fit in host memory):
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import subprocess
 import sys
 import time
+from contextlib import contextmanager
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -88,6 +90,21 @@ def cpu_baseline(workload: str, steps: int, threads: int) -> dict | None:
         return None
     line = [ln for ln in res.stdout.splitlines() if ln.startswith("{")][-1]
     return json.loads(line)
+
+
+@contextmanager
+def gc_paused():
+    """Python's cyclic garbage collector paused over a timed region, as ``timeit`` does: a full
+    collection in a process that holds torch takes 10-50 ms and would otherwise land inside one
+    step -- or between a HIP event and the dispatch it brackets, inflating that launch's time."""
+    was_enabled = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was_enabled:
+            gc.enable()
 
 
 def affinity_cpus() -> int:
@@ -355,23 +372,24 @@ def bench_ddp(name: str, args) -> dict:
     # own stream (two event records per step cost ~0.8% of a cfg1 step).  Every
     # step ends in the scaler's flag read (a host synchronisation), so the host
     # clock between step ends is each step's own time.
-    timing["on"] = not args.graphs
-    t0 = time.perf_counter()
-    found_any = False
-    ends = []
-    for _ in range(steps):
-        found_any |= step()
-        ends.append(time.perf_counter())
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    step_ms = sorted((b - a) * 1e3 for a, b in zip([t0] + ends[:-1], ends))
-    if args.graphs:
-        ddp._capture_graphs = False
-        timing["on"] = True
-        for _ in range(min(steps, 50)):
-            step()
+    with gc_paused():
+        timing["on"] = not args.graphs
+        t0 = time.perf_counter()
+        found_any = False
+        ends = []
+        for _ in range(steps):
+            found_any |= step()
+            ends.append(time.perf_counter())
         torch.cuda.synchronize()
-    timing["on"] = False
+        elapsed = time.perf_counter() - t0
+        step_ms = sorted((b - a) * 1e3 for a, b in zip([t0] + ends[:-1], ends))
+        if args.graphs:
+            ddp._capture_graphs = False
+            timing["on"] = True
+            for _ in range(min(steps, 50)):
+                step()
+            torch.cuda.synchronize()
+        timing["on"] = False
     setattr(ResidentGroup, hook_name, orig)
 
     b0 = ddp._buckets[0]
@@ -445,7 +463,7 @@ def bench_ddp(name: str, args) -> dict:
             "alg_bytes_formula": alg_note,
             "alg_gbs": round(alg_gbs, 2),
             "alg_frac_of_peak": round(alg_gbs / HBM_PEAK_GBS, 4),
-            "ms_per_step_stat": f"median of {steps} timed steps",
+            "ms_per_step_stat": f"median of {steps} timed steps (Python's garbage collector paused)",
             "ms_per_step_mean": round(mean_ms, 4),
             "ms_per_step_min": round(step_ms[0], 4),
             # a full 25 MiB bucket's share of the measured step (one bucket alone would sit in the
@@ -622,25 +640,26 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
     # Step pass: one event before the first dispatch and one after the last
     # (an event between two dispatches costs a few microseconds of its own).
     per_step = []
-    for _ in range(steps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(hold_cycles)  # hold the stream while the host enqueues the whole step
-        e0.record()
-        step()
-        e1.record()
-        torch.cuda.synchronize()
-        per_step.append(e0.elapsed_time(e1))
-    # Kernel pass: the same steps on one stream with events around every dispatch.
     cast_ms, share_ms = [], []
-    one_stream(True)
-    for _ in range(min(steps, 5)):
-        ev = {"cast": [], "share": []}
-        torch.cuda._sleep(hold_cycles)
-        step(ev)
-        torch.cuda.synchronize()
-        cast_ms += [e0.elapsed_time(e1) for e0, e1 in ev["cast"]]
-        share_ms += [e0.elapsed_time(e1) for e0, e1 in ev["share"]]
-    one_stream(False)
+    with gc_paused():
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(hold_cycles)  # hold the stream while the host enqueues the whole step
+            e0.record()
+            step()
+            e1.record()
+            torch.cuda.synchronize()
+            per_step.append(e0.elapsed_time(e1))
+        # Kernel pass: the same steps on one stream with events around every dispatch.
+        one_stream(True)
+        for _ in range(min(steps, 5)):
+            ev = {"cast": [], "share": []}
+            torch.cuda._sleep(hold_cycles)
+            step(ev)
+            torch.cuda.synchronize()
+            cast_ms += [e0.elapsed_time(e1) for e0, e1 in ev["cast"]]
+            share_ms += [e0.elapsed_time(e1) for e0, e1 in ev["share"]]
+        one_stream(False)
     # units one timed launch covers (unit-batch: the mean over its groups)
     per_launch = {"batched": n_units, "unit-batch": n_units / -(-n_units // K)}.get(mode, 1)
     ms_per_step = sorted(per_step)[len(per_step) // 2]
@@ -681,7 +700,7 @@ def bench_fsdp(args, param_dtype_name: str = "bf16") -> dict:
                                           "(comm_streams=True)",
                       "unit-batch": f"unit_batch={K}: a cast dispatch per {K} units in forward order, a multi-unit "
                                     f"share per {K} units in backward order"}[mode],
-            "ms_per_step_stat": f"median of {steps} steps",
+            "ms_per_step_stat": f"median of {steps} steps (Python's garbage collector paused)",
             "world": W,
             "units": n_units,
             "shard_numel": S,
@@ -801,11 +820,12 @@ def bench_overlap(args) -> dict:
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / steps * 1e3
+        with gc_paused():
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / steps * 1e3
 
     steps = min(args.steps, 30)
     results = {}
