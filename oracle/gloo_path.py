@@ -35,7 +35,7 @@ normal-range values (not on gradients halved and unscaled step after step
 into subnormals and zeros).
 
 Timing: ``perf_counter`` around the step bracketed by barriers, max over
-ranks.  Prints one JSON line.
+ranks, with Python's garbage collector paused over the timed steps.  Prints one JSON line.
 
     python -m oracle.gloo_path --config gpt2-small --world 8 --steps 3 --warmup 1 --threads 2
     python -m oracle.gloo_path --config llama-7b --layers 1 --world 8 --steps 3 --threads 2
@@ -45,6 +45,7 @@ ranks.  Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -126,6 +127,8 @@ def _worker(rank, world, store, cfg, steps, warmup, threads, cap_mb, scale, out_
         restore()
         step()
     times = []
+    gc.collect()
+    gc.disable()  # as in the GPU measurement: no collector pause inside a timed step
     for _ in range(steps):
         restore()
         dist.barrier()
@@ -133,6 +136,7 @@ def _worker(rank, world, store, cfg, steps, warmup, threads, cap_mb, scale, out_
         step()
         dist.barrier()
         times.append(time.perf_counter() - t0)
+    gc.enable()
     t = torch.tensor(times, dtype=torch.float64)
     dist.all_reduce(t, op=dist.ReduceOp.MAX)
     if rank == 0:
@@ -203,12 +207,15 @@ def _fsdp_worker(rank, world, store, h, units, steps, warmup, threads, out_path,
     for _ in range(warmup):
         step()
     times = []
+    gc.collect()
+    gc.disable()
     for _ in range(steps):
         dist.barrier()
         t0 = time.perf_counter()
         step()
         dist.barrier()
         times.append(time.perf_counter() - t0)
+    gc.enable()
     t = torch.tensor(times, dtype=torch.float64)
     dist.all_reduce(t, op=dist.ReduceOp.MAX)
     if rank == 0:
