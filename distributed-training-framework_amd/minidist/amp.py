@@ -201,9 +201,9 @@ class DistributedGradScaler:
         (None: the default group).
 
         Not under a ResidentGroup (this process saw every value there is).  An
-        IpcGroup's ranks are processes: DDP's one-shot reduction gives each the
-        same flag, but FSDP's ranks check different shards, so the flag is
-        exchanged over the group's host process group (4 bytes)."""
+        IpcGroup's ranks are processes: DDP's reductions (one- or two-shot) give
+        each the same flag, but FSDP's ranks check different shards, so the flag
+        is exchanged over the group's host process group (4 bytes)."""
         group = self.process_group
         if isinstance(group, comm.IpcGroup):
             return group.size() > 1, group.process_group

@@ -371,15 +371,17 @@ MDX_API int mdx_pack_allreduce_unpack_planned_noalloc(const void* plan, float in
                                                       int32_t* clear_flag, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Peer rows over IPC: the transport of the one-shot all-reduce.
+ * Peer rows over IPC: the transport of the one-shot and two-shot all-reduces.
  *
  * No counterpart in the reference, which hands every bucket to
  * dist.all_reduce (minidist/comm.py:223-234, called from ddp.py:243-247):
- * these calls let W processes map each other's contribution rows, so that each
- * rank runs the same rank-ordered fused reduction (mdx_allreduce_unpack[_planned])
- * over the peers' rows -- the one-shot all-reduce.  The caller orders the ranks
- * (every rank's pack complete before any rank reads it, every read complete
- * before a rank overwrites its row).
+ * these calls let W processes map each other's contribution rows (and
+ * buckets), so that each rank runs the same rank-ordered fused reduction
+ * (mdx_allreduce_unpack[_planned]) over the peers' rows -- the one-shot
+ * all-reduce -- or over its share of them, then copies the peers' reduced
+ * shares out of their buckets -- the two-shot all-reduce.  The caller orders
+ * the ranks (every rank's pack complete before any rank reads it, every read
+ * complete before a rank overwrites its row).
  * ------------------------------------------------------------------------- */
 
 #define MDX_IPC_HANDLE_BYTES 64
