@@ -870,20 +870,23 @@ class IpcGroup(ResidentGroup):
             return 0, 0
         return int(live["offset"].min()), int((live["offset"] + live["numel"]).max())
 
-    def _extent_agreed(self, lo: int, hi: int) -> None:
-        """:meth:`rows_written` of a two-shot reduction.  Its barrier is a MAX over
-        (lo, hi, -lo, -hi), which also checks that every rank reduces the same
-        elements [lo, hi): each reduces its share of them for all the others."""
+    def _runs_agreed(self, runs: np.ndarray) -> None:
+        """:meth:`rows_written` of a two-shot reduction.  Its barrier is a MAX over the runs'
+        signature (first element, end, a hash of every run's offset and length) and its
+        negation, which also checks that every rank reduces the same runs: each reduces its
+        share of them for all the others."""
         self._check_open()
         torch.cuda.current_stream(self.device).synchronize()
-        ext = torch.tensor([lo, hi, -lo, -hi], dtype=torch.int64)
-        dist.all_reduce(ext, op=dist.ReduceOp.MAX, group=self.process_group)
-        lo_max, hi_max, lo_min, hi_min = int(ext[0]), int(ext[1]), -int(ext[2]), -int(ext[3])
-        if lo_max != lo_min or hi_max != hi_min:
-            raise RuntimeError(
-                f"IpcGroup two-shot: the ranks reduce different element ranges "
-                f"(starts {lo_min}..{lo_max}, ends {hi_min}..{hi_max})"
-            )
+        live = runs[runs["numel"] > 0]
+        lo, hi = self._runs_extent(runs)
+        # tuples of ints hash the same in every process (no per-process salt)
+        sig = hash(tuple(zip(live["offset"].tolist(), live["numel"].tolist()))) & ((1 << 62) - 1)
+        mine = [lo, hi, sig]
+        both = torch.tensor(mine + [-x for x in mine], dtype=torch.int64)
+        dist.all_reduce(both, op=dist.ReduceOp.MAX, group=self.process_group)
+        if [int(x) for x in both[:3]] != [-int(x) for x in both[3:]]:
+            raise RuntimeError(f"IpcGroup two-shot: the ranks reduce different runs (this rank: elements "
+                               f"[{lo}, {hi}) in {len(live)} runs)")
 
     def _two_shot(self, runs: np.ndarray, esize: int, outs: list[int], code: int, reduce_share, after_gather,
                   async_op: bool):
@@ -896,7 +899,7 @@ class IpcGroup(ResidentGroup):
         lo, hi = self._runs_extent(runs)
         shares = two_shot_shares(lo, hi, self._world)
         me = self._rank
-        self._extent_agreed(lo, hi)  # every row is written
+        self._runs_agreed(runs)  # every row is written, and every rank reduces these runs
         a, b = shares[me]
         if b > a:
             reduce_share(a, b)

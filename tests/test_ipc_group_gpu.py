@@ -212,6 +212,15 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm:
         comm.reduce_scatter_tensor(rs_out, rs_in, group=group)
         comm.all_gather_into_tensor(ag_out, ag_in, group=group)
         out["rs"], out["ag"] = rs_out.cpu().numpy(), ag_out.cpu().numpy()
+        if algorithm == "two_shot":
+            # each rank reduces its share of the runs for all the others: ranks handing in
+            # different runs are told so, every one of them, before anything is launched
+            try:
+                comm.all_reduce(rows[0][: 100 + 10 * rank], group=group)
+            except RuntimeError as e:
+                assert "different runs" in str(e)
+            else:
+                raise AssertionError("a two-shot all-reduce accepted different runs on different ranks")
         # ranks asking for different symmetric buffers are told so, every one of them, before any
         # peer row is mapped
         try:
