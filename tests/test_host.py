@@ -329,7 +329,10 @@ def test_two_shot_shares_partition_the_extent():
     for lo, hi, world, align in cases:
         shares = comm.two_shot_shares(lo, hi, world, align)
         assert len(shares) == world
-        block = -(-(hi - lo) // (world * align)) * align  # elements per share, rounded up to align
+        # elements per share: the smallest multiple of align whose W copies cover the extent (searched)
+        block = align
+        while world * block < hi - lo:
+            block += align
         owner = np.full(hi - lo, -1)
         for j, (a, b) in enumerate(shares):
             assert lo <= a <= b <= hi
