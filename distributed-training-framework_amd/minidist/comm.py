@@ -15,6 +15,11 @@ unchanged.  What changes is what sits under the collective hook:
   as a gfx950 kernel over them, in the fixed rank order 0..W-1.  The call
   returns a Work whose ``wait()`` orders the caller's stream after the kernel;
   nothing synchronises the host.
+* With an :class:`IpcGroup` -- W processes of a real group -- the rows are
+  each process's own allocations, mapped into its peers over IPC, and the
+  same kernels run one-shot (each rank reads all W rows) or two-shot (each
+  rank reduces its share, then copies its peers' reduced shares), ordered by
+  host barriers over the wrapped group.
 """
 
 from __future__ import annotations
