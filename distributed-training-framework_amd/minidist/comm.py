@@ -254,8 +254,10 @@ def two_shot_shares(lo: int, hi: int, world: int, align: int = _SHARE_ALIGN_ELEM
     elements long (shares past the end are empty)."""
     if world < 1 or align < 1:
         raise ValueError("two_shot_shares: world and align must be positive")
-    step = -(-(hi - lo) // (world * align)) * align if hi > lo else 0
-    return [(min(lo + j * step, hi), min(lo + (j + 1) * step, hi)) if hi > lo else (lo, lo) for j in range(world)]
+    if hi <= lo:
+        return [(lo, lo)] * world
+    step = -(-(hi - lo) // (world * align)) * align  # ceil((hi - lo) / world), rounded up to align
+    return [(min(lo + j * step, hi), min(lo + (j + 1) * step, hi)) for j in range(world)]
 
 
 # A copy from several peers' memory goes out in chunks of this size, taken round-robin across
