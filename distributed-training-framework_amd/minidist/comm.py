@@ -242,6 +242,14 @@ class StreamWork:
 
 
 _ROW_ALIGN_BYTES = 256
+
+
+def _address(t: torch.Tensor) -> int:
+    """The address of ``t``'s first element -- also for a tensor with no elements, whose
+    ``data_ptr()`` torch reports as 0 (an empty bucket is still a place in its buffer)."""
+    if t.numel():
+        return t.data_ptr()
+    return t.untyped_storage().data_ptr() + t.storage_offset() * t.element_size()
 # A two-shot share starts a multiple of this many elements past the extent's start.
 _SHARE_ALIGN_ELEMS = 64
 
@@ -318,7 +326,7 @@ class _Arena:
         return self.data[r, : self.numel]
 
     def offset_of(self, t: torch.Tensor) -> int | None:
-        p = t.data_ptr()
+        p = _address(t)
         off, rem = divmod(p - self.own_base, self.esize)
         if rem or off < 0 or off + t.numel() > self.numel or t.dtype != self.dtype:
             return None
@@ -702,7 +710,7 @@ class _IpcArena:
         self.target: torch.Tensor | None = None
 
     def offset_of(self, t: torch.Tensor) -> int | None:
-        p = t.data_ptr()
+        p = _address(t)
         off, rem = divmod(p - self.own_base, self.esize)
         if rem or off < 0 or off + t.numel() > self.numel or t.dtype != self.dtype:
             return None

@@ -101,6 +101,42 @@ def test_finish_gradient_sync_bitwise(rng, dtype, W, rank, cap):
         assert same_bits(host_bits(bucket.buffer), want["reduced"][b])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("cap", [1e-6, 25.0])
+def test_zero_element_parameters(rng, dtype, cap):
+    """Parameters with no elements (a shape with a 0) anywhere in the order, as the reference's
+    ``copy_`` of an empty gradient allows: with one bucket per parameter some buckets are empty.
+    Every gradient and bucket bit for bit against the oracle, two steps."""
+    shapes = [(0,), (33,), (0, 4), (5, 7), (0,), (1,), (64,), (0, 0)]
+    W, rank = 4, 1
+    model = Flat(shapes, dtype)
+    grp = ResidentGroup(W, rank, DEV)
+    scaler = DistributedGradScaler(init_scale=2.0**8)
+    ddp = DDP(model, process_group=grp, bucket_cap_mb=cap, grad_scaler=scaler)
+    assert any(b.numel == 0 for b in ddp._buckets) == (cap < 1)
+    dts = [odt(dtype)] * len(shapes)
+    numels = [int(np.prod(s)) for s in shapes]
+
+    class _Opt:
+        param_groups = [{"params": list(model.parameters())}]
+
+    for step in range(2):
+        grads = synthetic_grads(rng, shapes, W, dtype, 2.0**8)
+        stage_peers(ddp, grads, dts, rank, W)
+        for p, g in zip(model.parameters(), grads[rank], strict=True):
+            p.grad = dev_from(g, p.shape)
+        ddp.finish_gradient_sync()
+        assert not scaler.unscale_(_Opt())
+        scaler.update()
+        want = o.ddp_pipeline(grads, dts, numels, cap, rank, 1.0 / 2.0**8)
+        for i, p in enumerate(model.parameters()):
+            got = host_bits(p.grad)
+            assert got.size == numels[i]
+            assert same_bits(got, want["grads"][i]), f"step {step} param {i}: " + first_mismatch(got, want["grads"][i])
+        for b, bucket in enumerate(ddp._buckets):
+            assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"step {step} bucket {b}"
+
+
 def test_bucket_caps_give_identical_grads(rng):
     """cfg2's property at small scale: 1 B, 25 MB and one giant bucket agree exactly."""
     shapes = [(300, 7), (11,), (1024,), (5, 5), (2048, 3), (9,)]

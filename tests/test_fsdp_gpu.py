@@ -184,6 +184,61 @@ def test_unit_and_memory_summaries(param_dtype):
     }
 
 
+class _HollowBlock(torch.nn.Module):
+    """A unit whose parameters include empty ones: a Linear with no input features (weight
+    [8, 0]) and a parameter with no elements (its gradient is empty too)."""
+
+    def __init__(self, seed: int):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.a = torch.nn.Linear(8, 8)
+        self.hollow = torch.nn.Linear(0, 8)
+        self.nothing = torch.nn.Parameter(torch.zeros(0))
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=g))
+
+    def forward(self, x):
+        return torch.tanh(self.a(x) + self.hollow(x[..., :0]) + self.nothing.sum())
+
+
+class _HollowNet(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.blocks = torch.nn.ModuleList([_HollowBlock(s) for s in range(3)])
+        self.empty_root = torch.nn.Parameter(torch.zeros(0, 3))
+
+    def forward(self, x):
+        for b in self.blocks:
+            x = b(x)
+        return x.square().mean()
+
+
+@pytest.mark.parametrize("W,rank,unit_batch", [(2, 0, 1), (3, 2, 2)])
+def test_zero_element_parameters(W, rank, unit_batch):
+    """Units holding parameters with no elements, and a root unit whose only parameter is empty and
+    unused (it never completes, as in the reference, and ``finish_gradient_sync`` finds no gradient
+    to flush): every shard gradient bit for bit against the oracle on the gradients this rank
+    produced (peers contribute zeros)."""
+    model = _HollowNet().to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture(captured))
+    fsdp = FSDP(model, unit_types=(_HollowBlock,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
+    assert len(fsdp._units) == 4 and any(0 in u.numels for u in fsdp._units)
+    x = torch.randn(5, 8, generator=torch.Generator().manual_seed(3)).to(DEV)
+    fsdp(x).backward()
+    fsdp.finish_gradient_sync()
+    for unit in fsdp._units:
+        assert all(p.grad is None for p in unit.params)
+        own = [host_bits(captured[id(p)]) if id(p) in captured else np.zeros(n, np.float32)
+               for p, n in zip(unit.params, unit.numels, strict=True)]
+        grads = [own if r == rank else [np.zeros(n, np.float32) for n in unit.numels] for r in range(W)]
+        want = o.fsdp_reduce_scatter_share(grads, o.F32, unit.numels, rank, o.F32, o.F32)
+        got = host_bits(unit.flat_shard.grad) if unit.flat_shard.grad is not None else np.zeros(0, np.float32)
+        assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):

@@ -186,6 +186,14 @@ def test_resident_group_symmetric_rows_cpu_layout():
     assert len({r.data_ptr() for r in reps}) == 3
     with pytest.raises(RuntimeError):
         grp.replicas(torch.zeros(4))
+    # views with no elements (an empty bucket) are still places in the buffer, whose data_ptr()
+    # torch reports as 0: each is found at its offset, and its replicas are empty too
+    for lo in (0, 4, 10):
+        empty = own[lo:lo]
+        assert empty.data_ptr() == 0 and grp._locate(empty)[1] == lo
+        assert [r.numel() for r in grp.replicas(empty)] == [0, 0, 0]
+    nothing = grp.zeros(0, torch.float32)
+    assert grp._locate(nothing)[1] == 0 and grp.row_addresses(nothing)[2] != 0
 
 
 # ---------------------------------------------------------------------------
