@@ -137,6 +137,37 @@ def test_zero_element_parameters(rng, dtype, cap):
             assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"step {step} bucket {b}"
 
 
+@pytest.mark.parametrize("cap", [1e-6, 0.001, 25.0])
+def test_frozen_parameters_stay_out_of_the_buckets(rng, cap):
+    """Parameters that do not require gradients are not bucketed (ddp.py:146): the buckets hold the
+    trainable ones only, in their reverse order, and a frozen parameter's gradient is left as the
+    caller set it.  Trainable gradients bit for bit against the oracle over the trainable list."""
+    shapes = [(33,), (64, 8), (5,), (130,), (1,), (7, 9)]
+    frozen = {1, 4}
+    W, rank = 4, 3
+    model = Flat(shapes)
+    for i, p in enumerate(model.parameters()):
+        p.requires_grad_(i not in frozen)
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap)
+    trainable = [i for i in range(len(shapes)) if i not in frozen]
+    bucketed = [id(p) for b in ddp._buckets for p in b.params]
+    params = list(model.parameters())
+    assert sorted(bucketed) == sorted(id(params[i]) for i in trainable)
+    grads = synthetic_grads(rng, [shapes[i] for i in trainable], W, torch.float32, 2.0**10)
+    dts = [o.F32] * len(trainable)
+    stage_peers(ddp, grads, dts, rank, W)
+    marker = torch.full((64, 8), 7.0, device=DEV)
+    params[1].grad = marker  # a frozen parameter's gradient, set by the caller: untouched
+    for k, i in enumerate(trainable):
+        params[i].grad = dev_from(grads[rank][k], shapes[i])
+    ddp.finish_gradient_sync()
+    want = o.ddp_pipeline(grads, dts, [int(np.prod(shapes[i])) for i in trainable], cap, rank, None)
+    for k, i in enumerate(trainable):
+        got = host_bits(params[i].grad)
+        assert same_bits(got, want["grads"][k]), f"param {i}: " + first_mismatch(got, want["grads"][k])
+    assert params[1].grad is marker and bool((marker == 7.0).all()) and params[4].grad is None
+
+
 def test_bucket_caps_give_identical_grads(rng):
     """cfg2's property at small scale: 1 B, 25 MB and one giant bucket agree exactly."""
     shapes = [(300, 7), (11,), (1024,), (5, 5), (2048, 3), (9,)]

@@ -239,6 +239,36 @@ def test_zero_element_parameters(W, rank, unit_batch):
         assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("W,rank,unit_batch", [(2, 1, 1), (4, 0, 3)])
+def test_frozen_parameters(W, rank, unit_batch):
+    """Parameters that do not require gradients stay in their unit's flat shard (the reference
+    flattens every parameter) but get no hook: a unit completes when its trainable gradients
+    have arrived, and the frozen ones contribute zeros.  Shard gradients bit for bit against the
+    oracle on the gradients this rank produced (peers contribute zeros)."""
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c).to(DEV)
+    frozen = [p for n, p in model.named_parameters() if n.endswith(("ln1.weight", "proj.bias"))]
+    assert frozen
+    for p in frozen:
+        p.requires_grad_(False)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        if p.requires_grad:
+            p.register_post_accumulate_grad_hook(_capture(captured))
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
+    ids, tgt = tiny_gpt.batch(c, 8, seed=11)
+    _, loss = fsdp(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    for unit in fsdp._units:
+        assert not unit.is_unsharded and all(p.grad is None for p in unit.params)
+        own = [host_bits(captured[id(p)]) if p.requires_grad else np.zeros(n, np.float32)
+               for p, n in zip(unit.params, unit.numels, strict=True)]
+        grads = [own if r == rank else [np.zeros(n, np.float32) for n in unit.numels] for r in range(W)]
+        want = o.fsdp_reduce_scatter_share(grads, o.F32, unit.numels, rank, o.F32, o.F32)
+        got = host_bits(unit.flat_shard.grad)
+        assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):
