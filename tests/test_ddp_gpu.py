@@ -168,6 +168,46 @@ def test_frozen_parameters_stay_out_of_the_buckets(rng, cap):
     assert params[1].grad is marker and bool((marker == 7.0).all()) and params[4].grad is None
 
 
+class _TiedLM(nn.Module):
+    """An embedding whose weight is also the output projection's (a tied LM head): one parameter,
+    two uses in forward, one accumulated gradient."""
+
+    def __init__(self, vocab: int = 50, h: int = 16):
+        super().__init__()
+        g = torch.Generator().manual_seed(5)
+        self.emb = nn.Embedding(vocab, h)
+        self.mid = nn.Linear(h, h)
+        self.head = nn.Linear(h, vocab, bias=False)
+        self.head.weight = self.emb.weight
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=g) * 0.1)
+
+    def forward(self, ids):
+        return self.head(torch.tanh(self.mid(self.emb(ids)))).logsumexp(-1).mean()
+
+
+@pytest.mark.parametrize("cap,overlap", [(1e-6, True), (25.0, True), (25.0, False)])
+def test_tied_parameter_is_reduced_once(cap, overlap):
+    """A parameter used twice in forward is bucketed once (``parameters()`` yields it once), its hook
+    fires once per backward, and it is averaged once: with the peers' contributions zero, every
+    gradient is this rank's own backward gradient times 1/W, bit for bit (W a power of two)."""
+    W, rank = 4, 0
+    model = _TiedLM().to(DEV)
+    params = list(model.parameters())
+    assert len(params) == 3
+    captured: dict[int, torch.Tensor] = {}
+    for p in params:
+        p.register_post_accumulate_grad_hook(lambda q: captured.__setitem__(id(q), q.grad.detach().clone()))
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap)
+    assert sum(len(b.params) for b in ddp._buckets) == 3
+    ids = torch.randint(0, 50, (4, 9), generator=torch.Generator().manual_seed(2)).to(DEV)
+    ddp(ids).backward()
+    for p in params:
+        want = captured[id(p)] * (1.0 / W)
+        assert torch.equal(p.grad, want)
+
+
 def test_bucket_caps_give_identical_grads(rng):
     """cfg2's property at small scale: 1 B, 25 MB and one giant bucket agree exactly."""
     shapes = [(300, 7), (11,), (1024,), (5, 5), (2048, 3), (9,)]
