@@ -269,6 +269,41 @@ def test_frozen_parameters(W, rank, unit_batch):
         assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
 
 
+class _MixedBlock(torch.nn.Module):
+    """A unit whose parameters come in two dtypes: a bf16 scale -- the module's own parameter, so
+    ``parameters()`` yields it before its child's -- and the child's fp32 weights."""
+
+    def __init__(self, seed: int):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.lin = torch.nn.Linear(6, 6)
+        self.scale = torch.nn.Parameter(torch.randn(6, generator=g).to(torch.bfloat16))
+        with torch.no_grad():
+            self.lin.weight.copy_(torch.randn(6, 6, generator=g))
+            self.lin.bias.copy_(torch.randn(6, generator=g))
+
+    def forward(self, x):
+        return self.lin(x) * self.scale.float()
+
+
+@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
+def test_units_of_mixed_dtypes_flatten_as_copy_converts(param_dtype):
+    """The flat parameter takes the unit's first parameter's dtype and every parameter is converted
+    into it as the reference's ``copy_`` converts it (fsdp.py:144-148) -- here the fp32 weights
+    are rounded to bf16, the first parameter's dtype: gathered, each parameter holds its value
+    taken through that dtype and then ``param_dtype``, bit for bit."""
+    net = torch.nn.Sequential(_MixedBlock(1), _MixedBlock(2)).to(DEV)
+    originals = [p.detach().clone() for p in net.parameters()]
+    assert [p.dtype for p in net[0].parameters()] == [torch.bfloat16, torch.float32, torch.float32]
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    fsdp = FSDP(net, unit_types=(_MixedBlock,), process_group=ResidentGroup(2, 1, DEV), mixed_precision=policy)
+    assert all(u.flat_shard.dtype == torch.bfloat16 for u in fsdp._units)
+    with fsdp.summon_full_params():
+        for p, want in zip(net.parameters(), originals, strict=True):
+            expect = want.to(torch.bfloat16).to(param_dtype)
+            assert p.dtype == param_dtype and torch.equal(p.detach(), expect)
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):
