@@ -304,6 +304,32 @@ def test_units_of_mixed_dtypes_flatten_as_copy_converts(param_dtype):
             assert p.dtype == param_dtype and torch.equal(p.detach(), expect)
 
 
+@pytest.mark.parametrize("param_dtype", [torch.float32, torch.bfloat16])
+def test_single_process_without_a_group(param_dtype):
+    """FSDP with no process group (world 1, the reference trainer run as one process): every unit
+    holds the whole flat parameter as its shard, and its reduce-scatter is the world-1 path of
+    fsdp.py:230-231 -- the flattened gradients, unscaled by nothing, set as the shard gradient --
+    bit for bit against the oracle on the gradients backward produced."""
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture(captured))
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), mixed_precision=policy, device=DEV)
+    assert fsdp.world_size == 1 and all(u.shard_numel == u.total_numel for u in fsdp._units)
+    ids, tgt = tiny_gpt.batch(c, 4, seed=21)
+    _, loss = fsdp(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    gdt = {torch.bfloat16: o.BF16}.get(param_dtype, o.F32)
+    for unit in fsdp._units:
+        assert all(p.grad is None for p in unit.params)
+        want = o.fsdp_reduce_scatter_share([[host_bits(captured[id(p)]) for p in unit.params]], gdt, unit.numels,
+                                           0, o.F32, o.F32)
+        got = host_bits(unit.flat_shard.grad)
+        assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):
