@@ -629,6 +629,36 @@ def test_unscale_is_idempotent():
         assert torch.equal(p.grad, torch.full_like(p.grad, 3.0))
 
 
+@pytest.mark.parametrize("inject", [None, "f32", "bf16", "f16"])
+def test_scaler_unscale_over_mixed_dtypes_matches_oracle(rng, inject):
+    """``scaler.unscale_`` on its own (no DDP), over an optimizer whose gradients come in fp32,
+    bf16 and fp16 across two param groups (one launch per dtype): every gradient and the
+    found-inf decision bit for bit against the oracle (amp.py:201-219), with an inf in one
+    dtype's gradient or none."""
+    S = 2.0**12
+    dts = [torch.float32, torch.bfloat16, torch.float16, torch.float32, torch.bfloat16]
+    sizes = [300, 77, 4100, 1, 65]
+    params = [nn.Parameter(torch.zeros(n, dtype=dt, device=DEV)) for n, dt in zip(sizes, dts, strict=True)]
+    hosts = [o.from_f32((rng.standard_normal(n) * 1e-2 * S).astype(np.float32), odt(dt))
+             for n, dt in zip(sizes, dts, strict=True)]
+    if inject is not None:
+        k = {"f32": 0, "bf16": 1, "f16": 2}[inject]
+        hosts[k] = hosts[k].copy()
+        hosts[k][5] = np.uint16(0x7F80) if inject == "bf16" else np.inf
+    for p, h in zip(params, hosts, strict=True):
+        p.grad = dev_from(h, p.shape)
+
+    class _Opt:
+        param_groups = [{"params": params[:2]}, {"params": params[2:]}]
+
+    scaler = DistributedGradScaler(init_scale=S)
+    found = scaler.unscale_(_Opt())
+    want, want_found = o.unscale_found_inf(hosts, [odt(dt) for dt in dts], 1.0 / S)
+    assert found == want_found == (inject is not None)
+    for p, w in zip(params, want, strict=True):
+        assert same_bits(host_bits(p.grad), w), first_mismatch(host_bits(p.grad), w)
+
+
 def test_mixed_overflow_history_final_scale():
     m, opt = _linear()
     scaler = DistributedGradScaler(init_scale=4096.0, growth_interval=2)
