@@ -330,6 +330,31 @@ def test_single_process_without_a_group(param_dtype):
         assert same_bits(got, want), f"unit {unit.name}: " + first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("unit_batch", [1, 4])
+def test_root_unit_only(unit_batch):
+    """No unit types: the whole model is the root unit (fsdp.py:343-354), gathered before forward,
+    reduced when its last gradient arrives.  Its shard gradient bit for bit against the oracle on
+    this rank's gradients (peers contribute zeros)."""
+    c = tiny_gpt.Config(n_layer=2)
+    model = tiny_gpt.GPT(c).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        p.register_post_accumulate_grad_hook(_capture(captured))
+    W, rank = 4, 2
+    fsdp = FSDP(model, process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
+    assert [u.name for u in fsdp._units] == ["<root>"]
+    ids, tgt = tiny_gpt.batch(c, 4, seed=8)
+    _, loss = fsdp(ids.to(DEV), tgt.to(DEV))
+    loss.backward()
+    unit = fsdp._units[0]
+    assert not unit.is_unsharded and all(p.grad is None for p in unit.params)
+    own = [host_bits(captured[id(p)]) for p in unit.params]
+    grads = [own if r == rank else [np.zeros(n, np.float32) for n in unit.numels] for r in range(W)]
+    want = o.fsdp_reduce_scatter_share(grads, o.F32, unit.numels, rank, o.F32, o.F32)
+    got = host_bits(unit.flat_shard.grad)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
 def test_sharding_is_real_and_unit_count():
     c = tiny_gpt.Config(n_layer=3)
     for W in (2, 4):
