@@ -208,6 +208,50 @@ def test_tied_parameter_is_reduced_once(cap, overlap):
         assert torch.equal(p.grad, want)
 
 
+class _WithUnused(nn.Module):
+    def __init__(self):
+        super().__init__()
+        g = torch.Generator().manual_seed(9)
+        self.a = nn.Linear(8, 8)
+        self.unused = nn.Linear(8, 8)  # never called: its hooks never fire
+        self.b = nn.Linear(8, 1)
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=g))
+
+    def forward(self, x):
+        return self.b(torch.tanh(self.a(x))).square().mean()
+
+
+@pytest.mark.parametrize("cap,overlap", [(1e-6, True), (25.0, True), (1e-6, False)])
+def test_unused_parameter_gets_the_average_of_the_peers(rng, cap, overlap):
+    """A parameter that takes no part in forward: its bucket is flushed at the end of backward
+    with zeros for this rank (ddp.py:87-88) and it receives a fresh gradient holding the average
+    (ddp.py:98-99) -- here of the peers' staged contributions; every other gradient is this
+    rank's averaged with the peers'.  Bit for bit against the oracle with this rank's captured
+    gradients and None for the unused ones."""
+    W, rank = 4, 1
+    model = _WithUnused().to(DEV)
+    params = list(model.parameters())
+    unused = {id(p) for p in model.unused.parameters()}
+    captured: dict[int, torch.Tensor] = {}
+    for p in params:
+        p.register_post_accumulate_grad_hook(lambda q: captured.__setitem__(id(q), q.grad.detach().clone()))
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap)
+    shapes = [tuple(p.shape) for p in params]
+    peers = synthetic_grads(rng, shapes, W, torch.float32, 1.0)
+    stage_peers(ddp, peers, [o.F32] * len(params), rank, W)
+    x = torch.randn(6, 8, generator=torch.Generator().manual_seed(4)).to(DEV)
+    ddp(x).backward()
+    own = [None if id(p) in unused else host_bits(captured[id(p)]) for p in params]
+    grads = [own if r == rank else peers[r] for r in range(W)]
+    want = o.ddp_pipeline(grads, [o.F32] * len(params), [p.numel() for p in params], cap, rank, None)
+    for i, p in enumerate(params):
+        assert p.grad is not None
+        got = host_bits(p.grad)
+        assert same_bits(got, want["grads"][i]), f"param {i}: " + first_mismatch(got, want["grads"][i])
+
+
 def test_bucket_caps_give_identical_grads(rng):
     """cfg2's property at small scale: 1 B, 25 MB and one giant bucket agree exactly."""
     shapes = [(300, 7), (11,), (1024,), (5, 5), (2048, 3), (9,)]
