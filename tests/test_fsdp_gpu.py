@@ -366,6 +366,12 @@ def test_sharding_is_real_and_unit_count():
         s = fsdp.memory_summary()
         assert s["num_units"] == c.n_layer + 1
         assert s["fsdp_state_MB"] < s["ddp_state_MB"]
+        # what an optimizer sees: the flat shards only, named as the reference names them
+        n = c.n_layer + 1
+        assert [name for name, _ in fsdp.named_parameters()] == [f"_flat_shard_{i}" for i in range(n)]
+        assert [name for name, _ in fsdp.named_parameters(prefix="m")] == [f"m._flat_shard_{i}" for i in range(n)]
+        assert [p is u.flat_shard for p, u in zip(fsdp.parameters(), fsdp._units, strict=True)] == [True] * n
+        assert [k for k in fsdp.state_dict() if k.startswith("_shards.")] == [f"_shards.{i}" for i in range(n)]
 
 
 @pytest.mark.parametrize("comm_streams,unit_batch", [(False, 1), (True, 1), (False, 3), (True, 3)])
