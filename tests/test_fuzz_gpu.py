@@ -61,7 +61,17 @@ class Flat(nn.Module):
 
 @pytest.mark.parametrize("seed", range(24))
 def test_random_pipeline_matches_oracle(seed):
-    rng = np.random.default_rng(9000 + seed)
+    _pipeline_case(seed, np.random.default_rng(9000 + seed))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_pipeline_with_empty_parameters(seed):
+    """The same draws with about a fifth of the parameters replaced by empty ones (so some
+    buckets hold no elements at one bucket per parameter)."""
+    _pipeline_case(seed, np.random.default_rng(19000 + seed), empty_rate=0.2)
+
+
+def _pipeline_case(seed: int, rng, empty_rate: float = 0.0) -> None:
     dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
     widening = dtype != torch.float32 and rng.random() < 0.5
     gdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(dtype, o.F32)
@@ -70,6 +80,8 @@ def test_random_pipeline_matches_oracle(seed):
     n_params = int(rng.integers(20, 41))
     shapes = [(int(rng.integers(1, 3000)),) if rng.random() < 0.7 else (int(rng.integers(1, 60)), int(rng.integers(1, 40)))
               for _ in range(n_params)]
+    if empty_rate:
+        shapes = [(0,) if rng.random() < empty_rate else s for s in shapes]
     numels = [int(np.prod(s)) for s in shapes]
     total_mb = sum(numels) * (4 if dtype == torch.float32 else 2) / 2**20
     cap = float(rng.choice([1e-6, total_mb / 7, total_mb / 3, 1e6]))
@@ -81,7 +93,7 @@ def test_random_pipeline_matches_oracle(seed):
         row = []
         for n in numels:
             g = (rng.standard_normal(n) * 1e-3 * scale).astype(np.float32)
-            if rng.random() < 0.05:  # a rare special value in this gradient
+            if n and rng.random() < 0.05:  # a rare special value in this gradient
                 g[int(rng.integers(0, n))] = SPECIALS[int(rng.integers(0, len(SPECIALS)))]
             row.append(o.from_f32(g, gdt))
         grads.append(row)
