@@ -137,3 +137,95 @@ def _pipeline_case(seed: int, rng, empty_rate: float = 0.0) -> None:
         assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"{case} bucket {b}"
     if scaler is not None:
         assert found == want["found_inf"], case
+
+
+class _FuzzBlock(nn.Module):
+    """A random FSDP unit: a square Linear (its bias frozen in some), and an extra parameter that
+    is empty in some."""
+
+    def __init__(self, h: int, seed: int, frozen_bias: bool, empty_extra: bool):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.lin = nn.Linear(h, h)
+        self.extra = nn.Parameter(torch.zeros(0 if empty_extra else 3))
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=g) * 0.5)
+        self.lin.bias.requires_grad_(not frozen_bias)
+
+    def forward(self, x):
+        x = x.to(self.lin.weight.dtype)
+        return torch.tanh(self.lin(x)) + self.extra.sum()
+
+
+class _FuzzNet(nn.Module):
+    def __init__(self, blocks: list[_FuzzBlock], h: int):
+        super().__init__()
+        self.blocks = nn.ModuleList(blocks)
+        self.head = nn.Linear(h, 1)
+
+    def forward(self, x):
+        for b in self.blocks:
+            x = b(x)
+        return self.head(x.to(self.head.weight.dtype)).float().square().mean()
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_fsdp_matches_oracle(seed):
+    """Seeded random FSDP configurations through the Python API: W, rank, 1-5 units of random
+    width (frozen biases, empty parameters), the gather dtype, ``unit_batch``,
+    ``reshard_after_forward`` and accumulation under ``no_sync`` with the final flush.  The peers'
+    full-size gradients are staged at random; every unit's shard gradient bit for bit against
+    oracle.fsdp_reduce_scatter_share on them and the gradients this rank's backward produced."""
+    from minidist import FSDP, MixedPrecisionPolicy
+
+    rng = np.random.default_rng(29000 + seed)
+    W = int(rng.integers(2, 9))
+    rank = int(rng.integers(0, W))
+    h = int(rng.integers(3, 41))
+    n_blocks = int(rng.integers(1, 6))
+    param_dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    unit_batch = int(rng.integers(1, 4))
+    reshard = bool(rng.random() < 0.7)
+    accumulate = bool(rng.random() < 0.4)
+    blocks = [_FuzzBlock(h, 1000 * seed + k, bool(rng.random() < 0.3), bool(rng.random() < 0.3))
+              for k in range(n_blocks)]
+    model = _FuzzNet(blocks, h).to(DEV)
+    captured: dict[int, torch.Tensor] = {}
+    for p in model.parameters():
+        if p.requires_grad:
+            p.register_post_accumulate_grad_hook(lambda q: captured.__setitem__(id(q), q.grad.detach().clone()))
+    policy = MixedPrecisionPolicy(param_dtype=param_dtype, reduce_dtype=torch.float32)
+    fsdp = FSDP(model, unit_types=(_FuzzBlock,), process_group=ResidentGroup(W, rank, DEV), mixed_precision=policy,
+                unit_batch=unit_batch, reshard_after_forward=reshard)
+    gdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(param_dtype, o.F32)
+    peer = {}  # (unit index, rank) -> per-parameter gradients in the gather dtype
+    for u, unit in enumerate(fsdp._units):
+        rows = unit.peer_grad_contributions()
+        for r in range(W):
+            if r == rank:
+                continue
+            per = [o.from_f32((rng.standard_normal(n) * 0.1).astype(np.float32), gdt) for n in unit.numels]
+            peer[u, r] = per
+            flat = np.concatenate([x.reshape(-1) for x in per]) if per else np.zeros(0, np.float32)
+            if flat.size:
+                rows[r, : flat.size].copy_(dev_from(flat))
+    x = torch.randn(6, h, generator=torch.Generator().manual_seed(seed)).to(DEV)
+    if accumulate:
+        with fsdp.no_sync():
+            for half in x.chunk(2):
+                (fsdp(half) / 2).backward()
+        fsdp.finish_gradient_sync()
+    else:
+        fsdp(x).backward()
+        fsdp.finish_gradient_sync()
+    case = f"seed {seed}: W={W} rank={rank} h={h} units={len(fsdp._units)} {param_dtype} ub={unit_batch} " \
+           f"reshard={reshard} accumulate={accumulate}"
+    for u, unit in enumerate(fsdp._units):
+        assert all(p.grad is None for p in unit.params), case
+        own = [host_bits(captured[id(p)]) if id(p) in captured else o.zeros(n, gdt)
+               for p, n in zip(unit.params, unit.numels, strict=True)]
+        grads = [own if r == rank else peer[u, r] for r in range(W)]
+        want = o.fsdp_reduce_scatter_share(grads, gdt, unit.numels, rank, o.F32, o.F32)
+        got = host_bits(unit.flat_shard.grad)
+        assert same_bits(got, want), f"{case} unit {unit.name}: " + first_mismatch(got, want)
