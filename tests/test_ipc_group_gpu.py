@@ -284,7 +284,7 @@ FSDP_DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float1
 
 
 def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: str, unit_batch: int,
-                 accumulate: bool = False, segment_bytes: int = SEGMENT) -> None:
+                 accumulate: bool = False, segment_bytes: int = SEGMENT, keep_low: bool = False) -> None:
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
@@ -302,7 +302,8 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
 
         for p in params:
             p.register_post_accumulate_grad_hook(capture)
-        policy = MixedPrecisionPolicy(param_dtype=FSDP_DTYPES[dtype_name], reduce_dtype=torch.float32)
+        policy = MixedPrecisionPolicy(param_dtype=FSDP_DTYPES[dtype_name], reduce_dtype=torch.float32,
+                                      keep_low_precision_shard=keep_low)
         fsdp = FSDP(model, unit_types=(tiny_gpt.Block,), process_group=group, mixed_precision=policy,
                     unit_batch=unit_batch)
         scaler = DistributedGradScaler(init_scale=16.0, process_group=group)
@@ -345,24 +346,26 @@ def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, dtype_name: st
 
 # A tiny-GPT block unit is 12,704 elements (the root 4,672): 64 KB of fp32 rows put every unit in a
 # buffer of its own; 40 KB of 16-bit rows put the two blocks apart and the root with the second.
-@pytest.mark.parametrize("world,dtype,unit_batch,accumulate,segment_bytes",
-                         [(2, "f32", 1, False, SEGMENT), (3, "bf16", 1, False, SEGMENT),
-                          (4, "bf16", 2, False, SEGMENT), (2, "f16", 3, False, SEGMENT),
-                          (3, "f32", 1, True, SEGMENT), (2, "bf16", 2, True, SEGMENT),
-                          (3, "bf16", 2, False, 40_000), (2, "f32", 1, True, 64_000)])
-def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulate, segment_bytes):
+@pytest.mark.parametrize("world,dtype,unit_batch,accumulate,segment_bytes,keep_low",
+                         [(2, "f32", 1, False, SEGMENT, False), (3, "bf16", 1, False, SEGMENT, False),
+                          (4, "bf16", 2, False, SEGMENT, False), (2, "f16", 3, False, SEGMENT, False),
+                          (3, "f32", 1, True, SEGMENT, False), (2, "bf16", 2, True, SEGMENT, False),
+                          (3, "bf16", 2, False, 40_000, False), (2, "f32", 1, True, 64_000, False),
+                          (3, "bf16", 2, False, SEGMENT, True), (2, "f16", 1, True, SEGMENT, True)])
+def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulate, segment_bytes, keep_low):
     """FSDP over an IpcGroup: each unit's all-gather is its ranks' published shards copied from the
     mapped rows, its reduce-scatter the share kernel over every rank's published full-size gradient
     (the reference's fsdp.py:172-241 with comm.all_gather_into_tensor / reduce_scatter_tensor).
     Gathered parameters, every rank's shard gradient (against the oracle on the ranks' captured
     local gradients) and the found-inf flag exchanged over the host group.  ``accumulate``: two
     half-batch backwards under ``no_sync`` and the flush of every unit at once.  A small
-    ``segment_bytes`` spreads the units over several pairs of symmetric buffers."""
+    ``segment_bytes`` spreads the units over several pairs of symmetric buffers.  ``keep_low``: the
+    master shards (and their gradients) in the gather dtype."""
     store = str(tmp_path / "store")
     print(f"spawning {world} ranks on cuda:0 (FSDP over an IpcGroup, {dtype}, unit_batch={unit_batch}, "
           f"segments of {segment_bytes} bytes)", flush=True)
-    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch, accumulate, segment_bytes),
-             nprocs=world, join=True)
+    mp.spawn(_fsdp_worker, args=(world, store, str(tmp_path), dtype, unit_batch, accumulate, segment_bytes,
+                                 keep_low), nprocs=world, join=True)
     res = []
     for r in range(world):
         with np.load(tmp_path / f"ipc_fsdp_r{r}.npz", allow_pickle=False) as d:
@@ -383,7 +386,7 @@ def test_ipc_fsdp_one_shot_bitwise(tmp_path, world, dtype, unit_batch, accumulat
         grads = [[res[r][f"local_{i}"] for i in idx] for r in range(world)]
         for rank in range(world):
             assert same_bits(res[rank][f"full_{u}"], gathered), f"unit {u} rank {rank}: all-gather"
-            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, o.F32)
+            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, pdt if keep_low else o.F32)
             got = res[rank][f"shard_grad_{u}"]
             assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)
     assert all(bool(res[r]["found"]) for r in range(world))
