@@ -260,6 +260,9 @@ class _FSDPUnit:
         self.reshard()
 
         self._grads_pending = 0
+        # set when this step's backward has completed the unit's gradients, cleared by the
+        # next forward: a batched backward gather must not bring such a unit back
+        self._backward_done = False
         self._hook_handles: list[torch.utils.hooks.RemovableHandle] = []
 
     # -- hooks ----------------------------------------------------------------
@@ -395,11 +398,13 @@ class _FSDPUnit:
 
     def arm_gradient_reduction(self) -> None:
         self._grads_pending = sum(1 for p in self.params if p.requires_grad)
+        self._backward_done = False
 
     def on_param_grad_ready(self, sync: bool) -> None:
         self._grads_pending -= 1
         if self._grads_pending > 0:
             return
+        self._backward_done = True
         if sync:
             self.reduce_scatter_grads()
         self.reshard()
@@ -802,6 +807,7 @@ class FullyShardedDataParallel(nn.Module):
         self._chain = [u for u, spec in zip(self._units, specs, strict=True) if not spec.is_root]
         self._chain_index = {id(u): i for i, u in enumerate(self._chain)}
         self._held_reductions: list[_FSDPUnit] = []
+        self._prefetched_for_backward: list[_FSDPUnit] = []
         self._end_queued = False
         for unit in self._units:
             unit.streams = self._streams
@@ -970,25 +976,41 @@ class FullyShardedDataParallel(nn.Module):
         """Gather ``unit`` before its forward (or backward) and make the caller's stream wait for it.
 
         With ``unit_batch`` > 1 a unit that is not gathered yet is gathered together with
-        the units that run next -- the following ones in forward, the preceding ones in
-        backward, up to ``unit_batch`` in all -- in one batched unshard."""
+        the units that are expected next -- the following ones in forward, the preceding
+        ones in backward, up to ``unit_batch`` in all -- in one batched unshard.  The
+        expectation is registration order; where the model runs its units in another
+        order, a backward batch leaves out every unit whose backward this step has
+        already completed (gathering it again would keep pre-update weights past the
+        optimizer step), and a unit it brought along whose backward then never comes is
+        freed when the engine finishes the backward, so every unit is sharded after
+        backward, as in the reference."""
         if not unit.is_unsharded:
             k = self.unit_batch
             i = self._chain_index.get(id(unit))
             if k == 1 or i is None:
                 unit.unshard()
+            elif forward:
+                self._unshard_many([u for u in self._chain[i : i + k] if not u.is_unsharded])
             else:
-                chain = self._chain[i : i + k] if forward else self._chain[max(0, i - k + 1) : i + 1][::-1]
-                self._unshard_many([u for u in chain if not u.is_unsharded])
+                ahead = [u for u in self._chain[max(0, i - k + 1) : i][::-1]
+                         if not u.is_unsharded and not u._backward_done]
+                self._unshard_many([unit, *ahead])
+                if ahead:
+                    self._prefetched_for_backward.extend(ahead)
+                    self._queue_end_of_backward()
         unit.wait_gathered()
 
+    def _queue_end_of_backward(self) -> None:
+        if not self._end_queued:
+            self._end_queued = True
+            torch.autograd.Variable._execution_engine.queue_callback(self._end_of_backward)
+
     def _on_grad_ready(self, unit: _FSDPUnit) -> None:
-        if not self._end_queued and (self._streams is not None or self.unit_batch > 1):
+        if self._streams is not None or self.unit_batch > 1:
             # Held reduce-scatters are flushed, and shard gradients written on the reduce
             # stream ordered before whatever follows on the caller's stream (the optimizer),
             # when the engine finishes this backward.
-            self._end_queued = True
-            torch.autograd.Variable._execution_engine.queue_callback(self._end_of_backward)
+            self._queue_end_of_backward()
         sync = self.require_backward_grad_sync
         if self.unit_batch == 1:
             unit.on_param_grad_ready(sync=sync)
@@ -996,6 +1018,7 @@ class FullyShardedDataParallel(nn.Module):
         unit._grads_pending -= 1
         if unit._grads_pending > 0:
             return
+        unit._backward_done = True
         # The unit's gradients are complete: its reduce-scatter waits for the next ones'
         # (it reads the gradients, not the gathered parameters, so the unit reshards now).
         if sync:
@@ -1016,6 +1039,9 @@ class FullyShardedDataParallel(nn.Module):
     def _end_of_backward(self) -> None:
         self._end_queued = False
         self._reduce_held()
+        prefetched, self._prefetched_for_backward = self._prefetched_for_backward, []
+        for unit in prefetched:
+            unit.reshard()
         if self._streams is not None:
             self._streams.join()
 

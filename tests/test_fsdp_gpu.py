@@ -506,6 +506,88 @@ def test_sgd_steps_track_full_batch(W, rank, comm_streams, unit_batch):
         assert rel <= 1e-5, f"unit {unit.name}: {rel:.3e}"
 
 
+class _OrderBlock(torch.nn.Module):
+    def __init__(self, gen: torch.Generator):
+        super().__init__()
+        self.lin = torch.nn.Linear(8, 8)
+        with torch.no_grad():
+            self.lin.weight.copy_(torch.randn(8, 8, generator=gen) * 0.5)
+            self.lin.bias.copy_(torch.randn(8, generator=gen) * 0.1)
+
+    def forward(self, x):
+        return torch.tanh(self.lin(x))
+
+
+class _OutOfOrderNet(torch.nn.Module):
+    """Blocks registered 0..n-1 but run in ``order``: the unit chain a batched gather walks
+    (registration order) is not the order the units run in."""
+
+    def __init__(self, order: list[int], seed: int = 17):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.order = list(order)
+        self.inp = torch.nn.Linear(4, 8)
+        self.blocks = torch.nn.ModuleList([_OrderBlock(g) for _ in range(len(order))])
+        self.head = torch.nn.Linear(8, 1)
+        with torch.no_grad():
+            for p in (*self.inp.parameters(), *self.head.parameters()):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.5)
+
+    def forward(self, x):
+        x = torch.tanh(self.inp(x))
+        for i in self.order:
+            x = self.blocks[i](x)
+        return self.head(x).square().mean()
+
+
+@pytest.mark.parametrize("order", [[3, 2, 1, 0], [0, 2, 1, 3], [1, 3, 0, 2]])
+@pytest.mark.parametrize("unit_batch", [2, 3])
+def test_units_run_out_of_registration_order(order, unit_batch):
+    """A batched backward gather walks the units in registration order; when the model runs
+    them in another order it must not bring back a unit whose backward has already finished
+    (it would stay gathered past the optimizer step and the next forward would use pre-update
+    weights).  Every unit is sharded after each backward (the reference's invariant,
+    fsdp.py:199-213), and after 3 SGD steps this rank's shards equal its slice of the
+    full-batch model's weights."""
+    W, rank, steps, lr = 2, 1, 3, 0.2
+    x = torch.randn(8, 4, generator=torch.Generator().manual_seed(23)).to(DEV)
+    ref = _OutOfOrderNet(order).to(DEV)
+    model = _OutOfOrderNet(order).to(DEV)
+    names_by_id = {id(p): n for n, p in model.named_parameters()}
+    fsdp = FSDP(model, unit_types=(_OrderBlock,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
+    opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
+    opt_ref = torch.optim.SGD(ref.parameters(), lr=lr)
+    for _ in range(steps):
+        cur = {n: p.detach().clone() for n, p in ref.named_parameters()}
+        for unit in fsdp._units:
+            flat = torch.cat([cur[names_by_id[id(p)]].reshape(-1) for p in unit.params])
+            flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
+            S, shards = unit.shard_numel, unit.peer_param_shards()
+            shards[1 - rank].copy_(flat[(1 - rank) * S : (2 - rank) * S])
+        peer = _OutOfOrderNet(order).to(DEV)
+        with torch.no_grad():
+            for n, p in peer.named_parameters():
+                p.copy_(cur[n])
+        peer(x.chunk(W)[1 - rank]).backward()
+        replica = [{n: p.grad.detach().clone() for n, p in peer.named_parameters()}, {}]
+        _stage(fsdp, names_by_id, replica if rank == 1 else replica[::-1], rank, W)
+        fsdp(x.chunk(W)[rank]).backward()
+        assert not any(u.is_unsharded for u in fsdp._units), "a unit is still gathered after backward"
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        ref(x).backward()
+        opt_ref.step()
+        opt_ref.zero_grad(set_to_none=True)
+    final = {n: p.detach() for n, p in ref.named_parameters()}
+    for unit in fsdp._units:
+        flat = torch.cat([final[names_by_id[id(p)]].reshape(-1) for p in unit.params])
+        flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
+        S = unit.shard_numel
+        want = flat[rank * S : (rank + 1) * S]
+        rel = (unit.flat_shard.detach() - want).abs().max().item() / max(want.abs().max().item(), 1.0)
+        assert rel <= 1e-5, f"unit {unit.name}: {rel:.3e}"
+
+
 @pytest.mark.parametrize("param_dtype", [torch.bfloat16, torch.float16])
 def test_low_precision_params_track_fp32_training(param_dtype):
     """Reference tests/test_fsdp.py:189-211: bf16 gathered parameters with fp32 reduction keep the
