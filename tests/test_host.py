@@ -810,6 +810,43 @@ def test_new_entry_points_check_arguments_before_any_launch():
     assert "256 KiB" in nat.strerror(nat.MDX_ESCRATCH)
 
 
+def test_noalloc_rejects_oversize_plan_and_aliased_flags():
+    """A plan beyond MDX_NOALLOC_SCRATCH_BYTES is refused with MDX_ESCRATCH, and found_inf ==
+    clear_flag with MDX_EALIAS, both before any HIP call: the addresses here are made up and
+    never touched (no GPU in this process).  The Python copy of the limit is the header's."""
+    limit = re.search(r"#define MDX_NOALLOC_SCRATCH_BYTES \((\d+) \* (\d+)\)", HEADER.read_text())
+    assert limit is not None and int(limit[1]) * int(limit[2]) == nat.NOALLOC_SCRATCH_BYTES
+    base = 1 << 40
+    reps = [base + r * (1 << 30) for r in range(2)]
+
+    def plan(n_runs):
+        runs = nat.pack_runs_array([(4 * k, 1, base + (1 << 36) + 64 * k, base + (1 << 37) + 64 * k)
+                                    for k in range(n_runs)])
+        size = ctypes.c_int64(0)
+        rc = nat.lib().mdx_plan_pack_allreduce_unpack(nat._ptrs(reps), 2, 0, nat.MDX_F32, nat._ptr(runs), n_runs,
+                                                      base + (1 << 38), nat.MDX_F32, 0.5, None, ctypes.byref(size))
+        assert rc == nat.MDX_ESIZE
+        host = np.zeros((size.value + 7) // 8, dtype=np.uint64)
+        cap = ctypes.c_int64(host.nbytes)
+        nat.check(nat.lib().mdx_plan_pack_allreduce_unpack(nat._ptrs(reps), 2, 0, nat.MDX_F32, nat._ptr(runs),
+                                                           n_runs, base + (1 << 38), nat.MDX_F32, 0.5,
+                                                           host.ctypes.data, ctypes.byref(cap)), "plan")
+        return host, size.value
+
+    host, nbytes = plan(9000)  # about 32 bytes per run: well past 256 KiB
+    assert nbytes > nat.NOALLOC_SCRATCH_BYTES
+    flag, other = ctypes.c_void_p(base + (1 << 39)), ctypes.c_void_p(base + (1 << 39) + 256)
+    L = nat.lib()
+    rc = L.mdx_pack_allreduce_unpack_planned_noalloc(host.ctypes.data, 1.0, flag, other, None)
+    assert rc == nat.MDX_ESCRATCH, nat.strerror(rc)
+    assert "256 KiB" in nat.strerror(rc)
+    small, nbytes = plan(16)
+    assert nbytes <= nat.NOALLOC_SCRATCH_BYTES
+    for h in (host, small):
+        rc = L.mdx_pack_allreduce_unpack_planned_noalloc(h.ctypes.data, 1.0, flag, flag, None)
+        assert rc == nat.MDX_EALIAS, nat.strerror(rc)
+
+
 def test_cfg1_plan_fits_the_allocation_free_buffer():
     """The fused plan of GPT-2-124M's 148 gradients in 18 buckets (the headline step) is well under
     MDX_NOALLOC_SCRATCH_BYTES; the plan is built on the host from addresses alone."""

@@ -13,8 +13,6 @@ leak into the second.
 
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 import pytest
 import torch
@@ -71,31 +69,3 @@ def test_noalloc_matches_planned_twice(first, second):
         assert got_new[4] == 0
         _check(new, numels, W, rank, wdt, bdt, inv, flags[1])
 
-
-def test_noalloc_rejects_oversize_plan_and_aliased_flags():
-    """A plan beyond MDX_NOALLOC_SCRATCH_BYTES is refused before anything is launched (the
-    addresses in it are never touched), and found_inf == clear_flag is refused as by the
-    planned entry point."""
-    n_runs = 9000  # about 32 bytes per run: well past 256 KiB
-    base = 1 << 40
-    reps = [base + r * (1 << 30) for r in range(2)]
-    runs = nat.pack_runs_array([(4 * k, 1, base + (1 << 36) + 64 * k, base + (1 << 37) + 64 * k)
-                                for k in range(n_runs)])
-    size = ctypes.c_int64(0)
-    rc = nat.lib().mdx_plan_pack_allreduce_unpack(nat._ptrs(reps), 2, 0, nat.MDX_F32, nat._ptr(runs), n_runs,
-                                                  base + (1 << 38), nat.MDX_F32, 0.5, None, ctypes.byref(size))
-    assert rc == nat.MDX_ESIZE and size.value > nat.NOALLOC_SCRATCH_BYTES
-    host = np.zeros((size.value + 7) // 8, dtype=np.uint64)
-    cap = ctypes.c_int64(host.nbytes)
-    nat.check(nat.lib().mdx_plan_pack_allreduce_unpack(nat._ptrs(reps), 2, 0, nat.MDX_F32, nat._ptr(runs), n_runs,
-                                                       base + (1 << 38), nat.MDX_F32, 0.5, host.ctypes.data,
-                                                       ctypes.byref(cap)), "plan")
-    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
-    rc = nat.lib().mdx_pack_allreduce_unpack_planned_noalloc(host.ctypes.data, 1.0, flag.data_ptr(), None, stream())
-    assert rc == nat.MDX_ESCRATCH, nat.strerror(rc)
-    assert "256 KiB" in nat.strerror(rc)
-    rc = nat.lib().mdx_pack_allreduce_unpack_planned_noalloc(host.ctypes.data, 1.0, flag.data_ptr(),
-                                                             flag.data_ptr(), stream())
-    assert rc == nat.MDX_EALIAS, nat.strerror(rc)
-    torch.cuda.synchronize()
-    assert flag.item() == 0
