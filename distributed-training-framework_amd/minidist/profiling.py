@@ -10,6 +10,13 @@ the gfx950 kernels that carry the data-parallel exchange are classified too:
     mdx allreduce_unpack / allreduce / allreduce_wide kernels  -> all_reduce
     mdx share_kernel (the reduce-scatter share)                -> reduce_scatter
     mdx copy_kernel (bucket pack / unpack, unscale, gather cast) -> bucket_copy
+    mdx clear_flag_kernel (the scaler's found-inf flag)        -> flag_clear
+    mdx upload_kernel (a plan copied in by the allocation-free
+    launch)                                                    -> plan_upload
+
+A kernel is recognised by its demangled name (``mdx::`` namespace) or its
+mangled one (``_ZN3mdx``): which of the two a trace holds depends on the
+tracer, not on the kernel.
 
 so "how much of the gradient exchange did backward hide" is answered for a
 ResidentGroup run exactly as for an RCCL one.  Besides the profiler's Chrome
@@ -49,7 +56,7 @@ __all__ = [
 
 # Substrings that mark an event as part of a collective: RCCL/NCCL device
 # kernels and host ops, torch.distributed's dispatcher ops and annotations,
-# and the gradient path's own kernels (namespace mdx::).
+# and the gradient path's own kernels (namespace mdx::, demangled or mangled).
 COLLECTIVE_PATTERNS: tuple[str, ...] = (
     "nccl",
     "rccl",
@@ -58,6 +65,7 @@ COLLECTIVE_PATTERNS: tuple[str, ...] = (
     "ProcessGroupNCCL",
     "ProcessGroupGloo",
     "mdx::",
+    "_ZN3mdx",
 )
 
 # (kind, lower-case substrings), first match wins: the mdx kernel names come
@@ -70,6 +78,8 @@ _KINDS: tuple[tuple[str, tuple[str, ...]], ...] = (
     ("send_recv", ("sendrecv", "send", "recv", "p2p")),
     ("barrier", ("barrier",)),
     ("bucket_copy", ("copy_kernel",)),
+    ("flag_clear", ("clear_flag_kernel",)),
+    ("plan_upload", ("upload_kernel",)),
 )
 
 
