@@ -591,6 +591,7 @@ class ResidentGroup:
         found_inf: torch.Tensor | None = None,
         clear_flag: torch.Tensor | None = None,
         async_op: bool = False,
+        reduce_dtype: torch.dtype | None = None,
     ):
         """Pack this rank's gradients into its row of ``wire``, then SUM over the W rows into gradients.
 
@@ -604,11 +605,13 @@ class ResidentGroup:
         times ``inv_scale`` and checked into ``found_inf``, in every gradient.
         ``clear_flag`` is set to 0 by the same dispatch (the scaler's flag for
         the next step).  One dispatch; this rank's contribution is summed from
-        registers, not re-read from its row."""
+        registers, not re-read from its row.  Without a ``bucket`` nothing is
+        written besides the row and the gradients; ``reduce_dtype`` (default:
+        the bucket's, else the wire's) is then the dtype the sum is taken in."""
         _native.require_device_tensor(wire, "all_reduce input")
         arena, off = self._locate(wire)
         bases = [b + off * arena.esize for b in arena.row_ptrs]
-        reduce_dtype = wire.dtype if bucket is None else bucket.dtype
+        reduce_dtype = _fused_reduce_dtype(wire, bucket, reduce_dtype)
         if bucket is not None:
             _native.require_device_tensor(bucket, "all_reduce output")
             if bucket.numel() < wire.numel():
@@ -623,13 +626,14 @@ class ResidentGroup:
         return StreamWork(stream) if async_op else None
 
     def plan_pack_all_reduce_unpack(
-        self, wire: torch.Tensor, bucket: torch.Tensor | None, runs, scale: float
+        self, wire: torch.Tensor, bucket: torch.Tensor | None, runs, scale: float,
+        reduce_dtype: torch.dtype | None = None,
     ) -> "_native.Plan":
         """Device plan of :meth:`pack_all_reduce_unpack` for fixed ``runs`` (one dispatch per launch)."""
         _native.require_device_tensor(wire, "all_reduce input")
         arena, off = self._locate(wire)
         bases = [b + off * arena.esize for b in arena.row_ptrs]
-        reduce_dtype = wire.dtype if bucket is None else bucket.dtype
+        reduce_dtype = _fused_reduce_dtype(wire, bucket, reduce_dtype)
         if bucket is not None:
             _native.require_device_tensor(bucket, "all_reduce output")
             if bucket.numel() < wire.numel():
@@ -692,6 +696,15 @@ class ResidentGroup:
     def _gather_order(spans: list[tuple[int, int, int]], esize: int) -> list[tuple[int, int, int]]:
         """The order a gather copies its spans in (the rows are all local here: as given)."""
         return spans
+
+
+def _fused_reduce_dtype(wire: torch.Tensor, bucket: torch.Tensor | None, reduce_dtype: torch.dtype | None):
+    """The dtype a fused pack + all-reduce sums in: the given one, else the bucket's, else the wire's."""
+    if reduce_dtype is None:
+        return wire.dtype if bucket is None else bucket.dtype
+    if bucket is not None and bucket.dtype != reduce_dtype:
+        raise TypeError(f"all_reduce: a {bucket.dtype} bucket cannot hold a {reduce_dtype} sum")
+    return reduce_dtype
 
 
 class _IpcArena:

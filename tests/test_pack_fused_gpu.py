@@ -314,6 +314,61 @@ def test_ddp_step_leaves_packed_row_and_averaged_bucket(rng, dtype, reduce_dtype
         assert same_bits(host_bits(p.grad), want["grads"][i]), f"param {i}"
 
 
+@pytest.mark.parametrize("dtype,reduce_dtype", [(torch.float32, None), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("n_params,cap", [(5, 0.001), (70, 25.0)])
+@pytest.mark.parametrize("inf", [False, True])
+def test_ddp_without_bucket_average(rng, dtype, reduce_dtype, n_params, cap, inf):
+    """``keep_bucket_average=False``: the same step as the default -- gradients, found-inf and this
+    rank's packed rows bit for bit, and against the oracle -- while every bucket keeps the sentinel
+    it held before the step.  Small runs go through kernel-argument tables (one bucket per launch),
+    70 gradients in one bucket through a device plan; fp32 and widening bf16 -> fp32 buckets."""
+    from minidist import DDP, DistributedGradScaler, ResidentGroup
+    from test_ddp_gpu import Flat, odt, stage_peers, synthetic_grads, dev_from, host_bits
+
+    W, rank, S = 4, 3, 2.0**10
+    shapes = [(int(rng.integers(1, 300)),) if k % 3 else (int(rng.integers(1, 40)), 7) for k in range(n_params)]
+    grads = synthetic_grads(rng, shapes, W, dtype, S)
+    if inf:
+        grads[1][n_params // 2] = grads[1][n_params // 2].copy()
+        grads[1][n_params // 2][0] = o.from_f32(np.array([np.inf], np.float32), odt(dtype))[0]
+    dts = [odt(dtype)] * len(shapes)
+    states = []
+    for keep in (True, False):
+        model = Flat(shapes, dtype)
+        scaler = DistributedGradScaler(init_scale=S)
+        ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, reduce_dtype=reduce_dtype,
+                  grad_scaler=scaler, keep_bucket_average=keep)
+        stage_peers(ddp, grads, dts, rank, W)
+        for b in ddp._buckets:
+            b.buffer.fill_(-3.25)
+        for p, g in zip(model.parameters(), grads[rank], strict=True):
+            p.grad = dev_from(g, p.shape)
+        ddp.finish_gradient_sync()
+        planned = any(st.plan is not None for plan in ddp._plans.values() for st in plan.packed_calls)
+        assert planned == (n_params > 48)
+
+        class _Opt:
+            param_groups = [{"params": list(model.parameters())}]
+
+        found = scaler.unscale_(_Opt())
+        states.append((
+            [host_bits(p.grad) for p in model.parameters()],
+            [host_bits(ddp.bucket_replicas(i)[rank]) for i in range(len(ddp._buckets))],
+            [b.buffer.detach().clone() for b in ddp._buckets],
+            found,
+        ))
+    (g_keep, r_keep, b_keep, f_keep), (g_skip, r_skip, b_skip, f_skip) = states
+    want = o.ddp_pipeline(grads, dts, [int(np.prod(s)) for s in shapes], cap, rank, 1.0 / S,
+                          **({"bucket_dtype": odt(reduce_dtype)} if reduce_dtype else {}))
+    assert f_keep == f_skip == want["found_inf"] == inf
+    for i in range(len(shapes)):
+        assert same_bits(g_skip[i], g_keep[i]) and same_bits(g_skip[i], want["grads"][i]), f"param {i}"
+    for k in range(len(r_keep)):
+        assert same_bits(r_skip[k], r_keep[k]), f"bucket {k} packed row"
+        assert same_bits(host_bits(b_keep[k]), want["reduced"][k]), f"bucket {k} average (default)"
+        assert bool((b_skip[k] == -3.25).all()), f"bucket {k} was written"
+
+
 @pytest.mark.parametrize("graphs", [False, True])
 def test_found_inf_flags_alternate_across_steps(rng, graphs):
     """Each step reports its own overflow: the fused pack of step s clears the flag of step s+1,
