@@ -21,8 +21,12 @@ traffic the rocprofv3 FETCH_SIZE / WRITE_SIZE counters measure.  The
 configuration's staged accounting, 52*N (pack 8N, W-way 36N, unpack 8N: the
 pipeline as three passes, which the fused kernel does not need), is reported
 beside it as config.alg_gbs.  The roofline object is for the dominant (and
-only) kernel: the same 44*N bytes per dispatch over its average HIP-event
-time, recorded on its own stream around every dispatch of the timed region.
+only) kernel, timed by HIP events recorded on its own stream around every
+dispatch of the timed region: ``achieved`` is the configuration's algorithmic
+bytes of the step that one dispatch performs (52*N) over its average time,
+``hbm_achieved`` the 44*N it actually moves, and ``traffic`` what the PMC
+counters read.  ``--no-bucket-average`` measures keep_bucket_average=False
+(40*N moved: the average is not copied into the buckets).
 The CPU baseline (reference op chain on torch CPU + gloo, W processes) runs
 first, before anything touches the GPU.
 
@@ -182,12 +186,122 @@ def calibrate_copy() -> int:
     return 0
 
 
+def dispatch_floor() -> int:
+    """cfg3 issued per unit (the reference's order): how fast can two stream-ordered dispatches
+    per unit -- the unshard cast and the reduce-scatter share -- possibly be?
+
+    Measured with the library entry points FSDP calls per unit (mdx_cast_f32_bf16 and
+    mdx_reduce_scatter_share, W = 8, one piece), each sequence enqueued behind a spin kernel and
+    timed on the GPU from first to last dispatch:
+
+    * the stream's cost of one dispatch that moves nothing: a one-workgroup cast, 400 back to back;
+    * per-dispatch times of the cast and the share at shard sizes from 2^20 to 2^25 elements,
+      rotating over up to 48 units (every sequence's data exceeds the 256 MB Infinity Cache), and
+      their sustained rates: the slope between the two largest sizes.
+
+    The floor of a unit is then two empty dispatches plus its 26*S bytes at the sustained rates;
+    it is compared with the time per unit that 70% of 8 TB/s allows."""
+    import torch
+
+    from minidist import _native
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    s_ptr = stream.cuda_stream
+    W, n_units, S_cfg3 = 8, 48, 3_842_600
+
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    torch.cuda._sleep(1_000_000)
+    c1.record()
+    torch.cuda.synchronize()
+    hold = int(1_000_000 * 20.0 / max(c0.elapsed_time(c1), 1e-3))  # ~20 ms
+
+    def gpu_ms(enqueue, reps: int = 5) -> float:
+        """Median GPU time of the enqueued sequence (the host enqueues it while a spin holds the stream)."""
+        out = []
+        for _ in range(reps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(hold)
+            e0.record()
+            enqueue()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1))
+        return sorted(out[1:])[reps // 2]
+
+    tiny_src = torch.ones(8, device=dev)
+    tiny_dst = torch.empty(8, dtype=torch.bfloat16, device=dev)
+    n_tiny = 400
+
+    def tiny():
+        for _ in range(n_tiny):
+            _native.cast_f32_bf16(tiny_src.data_ptr(), tiny_dst.data_ptr(), 8, s_ptr)
+
+    empty_us = gpu_ms(tiny) * 1e3 / n_tiny
+    sweep = []
+    for S in (1 << 20, 1 << 21, 1 << 22, S_cfg3, 1 << 23, 1 << 24, 1 << 25):
+        n = max(4, min(n_units, (4 << 30) // (26 * S)))
+        src = torch.randn(n, S, device=dev) * 0.02
+        dst = torch.empty(n, S, dtype=torch.bfloat16, device=dev)
+        rows = (torch.randn(W, n, S, device=dev) * 1e-3).to(torch.bfloat16)
+        out = torch.empty(n, S, device=dev)
+        pieces = [_native.pieces_array([(rows[0, k].data_ptr(), 0, S)]) for k in range(n)]
+        peers = [[rows[r, k].data_ptr() for r in range(W)] for k in range(n)]
+
+        def casts():
+            for k in range(n):
+                _native.cast_f32_bf16(src[k].data_ptr(), dst[k].data_ptr(), S, s_ptr)
+
+        def shares():
+            for k in range(n):
+                _native.reduce_scatter_share(pieces[k], peers[k], 0, _native.MDX_BF16, _native.MDX_F32, True,
+                                             out[k].data_ptr(), _native.MDX_F32, False, 1.0, None, s_ptr)
+
+        def units():
+            for k in range(n):
+                _native.cast_f32_bf16(src[k].data_ptr(), dst[k].data_ptr(), S, s_ptr)
+                _native.reduce_scatter_share(pieces[k], peers[k], 0, _native.MDX_BF16, _native.MDX_F32, True,
+                                             out[k].data_ptr(), _native.MDX_F32, False, 1.0, None, s_ptr)
+
+        cast_us, share_us, unit_us = (gpu_ms(f) * 1e3 / n for f in (casts, shares, units))
+        sweep.append({"S": S, "units": n, "cast_us": round(cast_us, 3), "share_us": round(share_us, 3),
+                      "unit_us": round(unit_us, 3), "cast_gbs": round(6 * S / (cast_us * 1e-6) / 1e9, 1),
+                      "share_gbs": round(20 * S / (share_us * 1e-6) / 1e9, 1)})
+        print(f"[bench] dispatch floor: {sweep[-1]}", file=sys.stderr, flush=True)
+        del src, dst, rows, out
+        torch.cuda.empty_cache()
+    big = sorted(sweep, key=lambda r: r["S"])[-2:]
+    dS = big[1]["S"] - big[0]["S"]
+    cast_rate = 6 * dS / ((big[1]["cast_us"] - big[0]["cast_us"]) * 1e-6) / 1e9
+    share_rate = 20 * dS / ((big[1]["share_us"] - big[0]["share_us"]) * 1e-6) / 1e9
+    floor_unit_us = 2 * empty_us + (6 * S_cfg3 / (cast_rate * 1e9) + 20 * S_cfg3 / (share_rate * 1e9)) * 1e6
+    bar_unit_us = 26 * S_cfg3 / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6
+    measured = next(r for r in sweep if r["S"] == S_cfg3)
+    print(json.dumps({
+        "probe": "cfg3 per-unit dispatch floor (mdx_cast_f32_bf16 + mdx_reduce_scatter_share, W=8)",
+        "empty_dispatch_us": round(empty_us, 3),
+        "sustained_cast_gbs": round(cast_rate, 1),
+        "sustained_share_gbs": round(share_rate, 1),
+        "cfg3_unit_measured_us": measured["unit_us"],
+        "cfg3_unit_floor_us": round(floor_unit_us, 3),
+        "cfg3_unit_bar_us": round(bar_unit_us, 3),
+        "cfg3_step_floor_ms": round(n_units * floor_unit_us * 1e-3, 4),
+        "cfg3_step_measured_ms": round(n_units * measured["unit_us"] * 1e-3, 4),
+        "cfg3_step_bar_ms": round(n_units * bar_unit_us * 1e-3, 4),
+        "sweep": sweep,
+    }), flush=True)
+    return 0
+
+
 # Committed rocprofv3 FETCH_SIZE + WRITE_SIZE summaries of each workload's dominant kernel: the
 # pack fused into the all-reduce + unpack (default), or the two-dispatch pipeline's fused
 # all-reduce + unpack (--two-dispatch).
 TRAFFIC_FILES = {
     ("cfg0", True): "pack_allreduce_tiny_gpt_w4_traffic.json",
     ("cfg1", True): "pack_allreduce_gpt2_124m_w8_traffic.json",
+    ("cfg1", True, "no-bucket-average"): "pack_allreduce_gpt2_124m_w8_no_bucket_average_traffic.json",
     ("cfg2", True): "pack_allreduce_gpt2_medium_w4_traffic.json",
     ("cfg4", True): "pack_allreduce_llama7b_w8_traffic.json",
     ("cfg0", False): "allreduce_unpack_tiny_gpt_w4_traffic.json",
@@ -199,9 +313,10 @@ TRAFFIC_FILES = {
 }
 
 
-def measured_traffic(workload: str, fused_pack: bool = False) -> int | None:
+def measured_traffic(workload: str, fused_pack: bool = False, keep_bucket: bool = True) -> int | None:
     """HBM bytes per dispatch of the dominant kernel, from the committed PMC summary."""
-    path = ROOT / "profiles" / TRAFFIC_FILES.get((workload, fused_pack), "")
+    key = (workload, fused_pack) if keep_bucket else (workload, fused_pack, "no-bucket-average")
+    path = ROOT / "profiles" / TRAFFIC_FILES.get(key, "")
     if not path.is_file():
         return None
     return json.loads(path.read_text()).get("bytes_per_launch")
@@ -260,8 +375,10 @@ def bench_ddp(name: str, args) -> dict:
     fused_unscale = not args.dropin
     if args.dropin and reduce_dtype is not None:
         raise SystemExit("--dropin covers the same-dtype workloads (cfg0, cfg1, cfg2)")
+    # --no-bucket-average: the fused launch leaves the bucket out (keep_bucket_average=False)
+    keep_bucket = not args.no_bucket_average
     ddp = DDP(model, process_group=group, bucket_cap_mb=CAP_MB, grad_scaler=scaler if fused_unscale else None,
-              reduce_dtype=reduce_dtype, capture_graphs=args.graphs)
+              reduce_dtype=reduce_dtype, capture_graphs=args.graphs, keep_bucket_average=keep_bucket)
     # --two-dispatch: pack, then the fused all-reduce + unpack (the pipeline before the pack was fused in)
     ddp._fuse_pack = not (args.two_dispatch or args.staged)
     fused_pack = ddp._fuse_pack
@@ -401,7 +518,7 @@ def bench_ddp(name: str, args) -> dict:
     # Fused pack: the gradient read, W-1 peer rows read, this rank's packed row, the bucket and
     # the gradient written -- one dispatch.  Two-dispatch pipeline: the pack (gradient read, row
     # written), then W rows read, bucket and gradient written.
-    red_bytes = (N * (2 * s_g + W * s_w + s_b) if fused_pack
+    red_bytes = (N * (2 * s_g + W * s_w + (s_b if keep_bucket else 0)) if fused_pack
                  else N * (W * s_w + s_b + s_g))
     if b0.widening:
         alg_bytes = N * (W * s_w + s_b + s_b + s_g)  # the configuration's accounting (26*N)
@@ -431,14 +548,20 @@ def bench_ddp(name: str, args) -> dict:
         hbm_bytes = N * (s_g + s_b) + red_bytes + N * (s_b + s_g)
         kname = f"allreduce_kernel<float, float, {W}, false> (mdx_allreduce_sum)"
     red_gbs = red_bytes / (red_avg_ms * 1e-3) / 1e9
+    # The roofline's algorithmic bytes per launch: when the one dispatch is the whole step (the
+    # pack fused in), the configuration's accounting of the step (52*N for fp32 at W = 8, 26*N
+    # for cfg4); otherwise what the timed kernel itself must move.
+    roof_bytes = alg_bytes if fused_pack and not args.staged else red_bytes
+    roof_gbs = roof_bytes / (red_avg_ms * 1e-3) / 1e9
 
-    traffic = None if args.staged else measured_traffic(name, fused_pack)
+    traffic = None if args.staged else measured_traffic(name, fused_pack, keep_bucket)
 
     return {
         "metric": (METRIC if name == "cfg1" else f"grad-bucket pipeline HBM GB/s (% of 8 TB/s) {name}; ms/step")
                   + "".join(f" [{tag}]" for tag, on in (("staged", args.staged), ("two-dispatch", args.two_dispatch),
                                                         ("graphs", args.graphs), ("dropin", args.dropin),
-                                                        ("misaligned", args.misaligned)) if on),
+                                                        ("misaligned", args.misaligned),
+                                                        ("no-bucket-average", not keep_bucket)) if on),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -479,18 +602,24 @@ def bench_ddp(name: str, args) -> dict:
             "pipeline": "staged: pack, W-way sum, unpack (three dispatches)" if args.staged
                         else "pack + fused W-way sum / unpack / unscale (two dispatches)" if not fused_pack
                         else "pack fused into the W-way sum / unpack / unscale (one dispatch)",
+            "bucket_average": "written into every bucket (the reference's bucket state)" if keep_bucket
+                              else "not written (keep_bucket_average=False)",
         },
         "roofline": {
             "bound": "hbm",
             "kernel": kname if args.staged else
                       f"{kname} ({'mdx_pack_allreduce_unpack_planned' if fused_pack else 'mdx_allreduce_unpack_planned'}"
                       f", all {len(ddp._buckets)} buckets in one dispatch)",
-            "achieved": round(red_gbs, 2),
+            "achieved": round(roof_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(red_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(roof_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "bytes_per_launch": red_bytes,
+            "bytes_per_launch": roof_bytes,
+            "bytes_formula": alg_note if roof_bytes == alg_bytes else "the timed kernel's own reads and writes",
+            "hbm_bytes_per_launch": red_bytes,
+            "hbm_achieved": round(red_gbs, 2),
+            "hbm_frac": round(red_gbs / HBM_PEAK_GBS, 4),
             "avg_launch_ms": round(red_avg_ms, 4),
         },
         "cpu_baseline": None,
@@ -905,6 +1034,9 @@ def main() -> int:
     ap.add_argument("--dropin", action="store_true",
                     help="DDP workloads: the reference's call sequence unchanged (no grad_scaler=): the scaler's "
                          "unscale_ runs its own pass over the gradients")
+    ap.add_argument("--no-bucket-average", action="store_true",
+                    help="DDP workloads: keep_bucket_average=False (the fused launch does not copy the average "
+                         "into the buckets)")
     ap.add_argument("--misaligned", action="store_true",
                     help="DDP workloads: every gradient a view one element into its allocation")
     ap.add_argument("--unit-batch", type=int, default=8,
@@ -918,9 +1050,16 @@ def main() -> int:
         help="only run a plain 1 GiB fp32 copy (mdx_pack, scale 1) 10 times: the known-size "
              "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings",
     )
+    ap.add_argument(
+        "--dispatch-floor", action="store_true",
+        help="only measure the per-unit floor of cfg3 issued in the reference's order (two stream-ordered "
+             "dispatches per unit; see dispatch_floor)",
+    )
     args = ap.parse_args()
     if args.calibrate_copy:
         return calibrate_copy()
+    if args.dispatch_floor:
+        return dispatch_floor()
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU: this build emulates the W={W_CFG1} data-parallel replicas on a single "
