@@ -463,6 +463,31 @@ class ResidentGroup:
             )
         return StreamWork(stream) if async_op else None
 
+    def all_reduce_op(self, tensors: Sequence[torch.Tensor], op: int, async_op: bool = False):
+        """:meth:`all_reduce_sum` with the reduction ``op`` (``_native.MDX_OP_*``): every element
+        folded over the W replicas in rank order with torch's maximum / minimum / mul, in place or
+        into the buffer's reduce target (``mdx_allreduce_op``, one dispatch per symmetric buffer)."""
+        if op == _native.MDX_OP_SUM:
+            return self.all_reduce_sum(tensors, async_op)
+        if not tensors:
+            return None
+        stream = torch.cuda.current_stream(tensors[0].device)
+        groups: dict[int, tuple[_Arena, list[int], list[int]]] = {}
+        for t in tensors:
+            _native.require_device_tensor(t, "all_reduce input")
+            arena, off = self._locate(t)
+            entry = groups.setdefault(id(arena), (arena, [], []))
+            entry[1].append(off)
+            entry[2].append(t.numel())
+        for arena, offs, nums in groups.values():
+            order = sorted(range(len(offs)), key=offs.__getitem__)
+            _native.allreduce_op(
+                arena.row_ptrs, _native.dtype_code(arena.dtype), op, [offs[i] for i in order],
+                [nums[i] for i in order], arena.own_base if arena.target is None else arena.target.data_ptr(),
+                stream.cuda_stream,
+            )
+        return StreamWork(stream) if async_op else None
+
     def all_reduce_unpack(
         self,
         buffer: torch.Tensor,
@@ -656,6 +681,25 @@ class ResidentGroup:
         # the Work's stream object is built after the launch, off the path to the GPU
         return StreamWork(torch.cuda.current_stream(device)) if async_op else None
 
+    def reduce_scatter_op(self, output: torch.Tensor, input_: torch.Tensor, op: int, async_op: bool = False):
+        """:meth:`reduce_scatter_sum` with the reduction ``op`` (``_native.MDX_OP_*``): this rank's
+        slice of the W replicas folded in rank order (``mdx_allreduce_op`` over the slices)."""
+        if op == _native.MDX_OP_SUM:
+            return self.reduce_scatter_sum(output, input_, async_op)
+        _native.require_device_tensor(input_, "reduce_scatter input")
+        rows = self._rows_of(input_)
+        S = output.numel()
+        if input_.numel() != S * self._world:
+            raise ValueError(f"reduce_scatter: input has {input_.numel()} elements, expected {S * self._world}")
+        if output.dtype != input_.dtype:
+            raise TypeError("reduce_scatter: output and input dtypes differ")
+        _native.require_dense(output, "reduce_scatter output")
+        lo = self._rank * S * input_.element_size()
+        stream = torch.cuda.current_stream(input_.device)
+        _native.allreduce_op([r + lo for r in rows], _native.dtype_code(input_.dtype), op, [0], [S],
+                             output.data_ptr(), stream.cuda_stream)
+        return StreamWork(stream) if async_op else None
+
     def reduce_scatter_sum(self, output: torch.Tensor, input_: torch.Tensor, async_op: bool = False):
         """``output = sum_r replicas(input_)[r][rank*S:(rank+1)*S]``, rank order."""
         _native.require_device_tensor(input_, "reduce_scatter input")
@@ -711,10 +755,11 @@ class _IpcArena:
     """One symmetric buffer of an :class:`IpcGroup`: this rank's row is a tensor of its own;
     the peers' rows are inside their allocations, mapped into this process over IPC."""
 
-    __slots__ = ("own", "numel", "dtype", "esize", "own_base", "row_ptrs", "target")
+    __slots__ = ("own", "pool", "numel", "dtype", "esize", "own_base", "row_ptrs", "target")
 
-    def __init__(self, own: torch.Tensor, numel: int, row_ptrs: list[int]):
+    def __init__(self, own: torch.Tensor, numel: int, row_ptrs: list[int], pool=None):
         self.own = own
+        self.pool = pool  # the row's own memory pool: it lives as long as the row
         self.numel = numel
         self.dtype = own.dtype
         self.esize = own.element_size()
@@ -806,9 +851,21 @@ class IpcGroup(ResidentGroup):
         esize = torch.empty((), dtype=dtype).element_size()
         align = _ROW_ALIGN_BYTES // esize
         row_elems = max(align, (numel + align - 1) // align * align)
-        own = torch.zeros(row_elems, dtype=dtype, device=self.device)
+        # The row is an allocation of its own (a pool of its own whose blocks are never split):
+        # what a peer maps is this row and nothing else, and its size never includes a cached
+        # segment that the caching allocator would otherwise have carved the row from.
+        pool = torch.cuda.MemPool(no_split=True)
+        with torch.cuda.use_mem_pool(pool, device=self.device):
+            own = torch.zeros(row_elems, dtype=dtype, device=self.device)
         torch.cuda.current_stream(self.device).synchronize()  # the zeros are in place before a peer maps the row
-        handle = _native.ipc_export(own.data_ptr())
+        try:
+            handle = _native.ipc_export(own.data_ptr())
+        except RuntimeError as exc:
+            raise RuntimeError(
+                f"IpcGroup.zeros: the {row_elems * esize}-byte row could not be exported (the runtime maps "
+                f"allocations below {_native.IPC_MAX_ALLOC_BYTES} bytes: keep symmetric buffers within the "
+                f"group's segment_bytes): {exc}"
+            ) from exc
         raw: list = [None] * self._world
         dist.all_gather_object(raw, (handle.to_bytes(), row_elems, str(dtype)), group=self.process_group)
         # every kernel reads all W rows over this rank's extent: the rows must agree
@@ -828,7 +885,7 @@ class IpcGroup(ResidentGroup):
                 base = _native.ipc_open(h) - int(h.offset)
                 self._mapped[key] = base
             row_ptrs.append(base + int(h.offset))
-        arena = _IpcArena(own, numel, row_ptrs)
+        arena = _IpcArena(own, numel, row_ptrs, pool)
         self._arenas.append(arena)
         return own[:numel]
 
@@ -957,12 +1014,25 @@ class IpcGroup(ResidentGroup):
         self._check_open()
         if self.algorithm == "two_shot":
             return self._all_reduce_sum_two_shot(tensors, async_op)
+        return self._one_shot_all_reduce(tensors, lambda: ResidentGroup.all_reduce_sum(self, tensors), async_op)
+
+    def all_reduce_op(self, tensors: Sequence[torch.Tensor], op: int, async_op: bool = False):
+        """:meth:`ResidentGroup.all_reduce_op` over the mapped rows, one-shot whatever the group's
+        algorithm (PRODUCT, MIN and MAX carry flags and small tensors)."""
+        if op == _native.MDX_OP_SUM:
+            return self.all_reduce_sum(tensors, async_op)
+        self._check_open()
+        return self._one_shot_all_reduce(tensors, lambda: ResidentGroup.all_reduce_op(self, tensors, op), async_op)
+
+    def _one_shot_all_reduce(self, tensors: Sequence[torch.Tensor], reduce, async_op: bool):
+        """``reduce()`` over the mapped rows between the fences; a buffer without a reduce target
+        is reduced into a private copy first, copied into the rows once every rank has read them."""
         arenas = {id(a): a for a in (self._locate(t)[0] for t in tensors)}
         staged = [a for a in arenas.values() if a.target is None]
         for arena in staged:
             arena.target = torch.empty_like(arena.own)
         try:
-            work = self._one_shot(lambda: ResidentGroup.all_reduce_sum(self, tensors), async_op)
+            work = self._one_shot(reduce, async_op)
             for t in tensors:
                 arena, off = self._locate(t)
                 if arena in staged:
@@ -1079,6 +1149,11 @@ class IpcGroup(ResidentGroup):
         of a symmetric buffer), read one-shot from the mapped rows."""
         self._check_open()
         return self._one_shot(lambda: ResidentGroup.reduce_scatter_sum(self, output, input_), async_op)
+
+    def reduce_scatter_op(self, output, input_, op: int, async_op: bool = False):
+        """:meth:`ResidentGroup.reduce_scatter_op` read one-shot from the mapped rows."""
+        self._check_open()
+        return self._one_shot(lambda: ResidentGroup.reduce_scatter_op(self, output, input_, op), async_op)
 
     @staticmethod
     def _gather_order(spans: list[tuple[int, int, int]], esize: int) -> list[tuple[int, int, int]]:
@@ -1197,10 +1272,17 @@ def all_reduce(tensor: torch.Tensor, op=dist.ReduceOp.SUM, group=None, async_op:
         return None
     record_all_reduce(_nbytes(tensor), world)
     if isinstance(group, ResidentGroup):
-        if op != dist.ReduceOp.SUM:
-            raise NotImplementedError("ResidentGroup all_reduce implements SUM")
-        return group.all_reduce_sum([tensor], async_op=async_op)
+        return group.all_reduce_op([tensor], _resident_op(op, "all_reduce"), async_op=async_op)
     return dist_all_reduce(tensor, op=op, group=group, async_op=async_op)
+
+
+def _resident_op(op, what: str) -> int:
+    """The ``mdx_allreduce_op`` code of a ``dist.ReduceOp`` a ResidentGroup reduces with."""
+    for red, code in ((dist.ReduceOp.SUM, _native.MDX_OP_SUM), (dist.ReduceOp.PRODUCT, _native.MDX_OP_PRODUCT),
+                      (dist.ReduceOp.MIN, _native.MDX_OP_MIN), (dist.ReduceOp.MAX, _native.MDX_OP_MAX)):
+        if op == red:
+            return code
+    raise NotImplementedError(f"ResidentGroup {what} implements SUM, PRODUCT, MIN and MAX, not {op}")
 
 
 def all_reduce_coalesced(tensors: Sequence[torch.Tensor], group=None, async_op: bool = False):
@@ -1245,9 +1327,7 @@ def reduce_scatter_tensor(
     payload = _nbytes(input_)
     comm_stats.add("reduce_scatter", payload, int((world - 1) / world * payload))
     if isinstance(group, ResidentGroup):
-        if op != dist.ReduceOp.SUM:
-            raise NotImplementedError("ResidentGroup reduce_scatter implements SUM")
-        return group.reduce_scatter_sum(output, input_, async_op=async_op)
+        return group.reduce_scatter_op(output, input_, _resident_op(op, "reduce_scatter"), async_op=async_op)
     return dist_reduce_scatter_tensor(output, input_, op=op, group=group, async_op=async_op)
 
 

@@ -167,9 +167,9 @@ def test_ipc_all_reduce_bitwise(tmp_path, world, dtype, algorithm, segment_bytes
     print("step ms per rank:", [[float(res[r][f"ms_{s}"]) for s in range(2)] for r in range(world)], flush=True)
 
 
-SMALL = (1000, 3000, 3000, 100)  # small symmetric buffers: the caching allocator may carve several out of
-# one segment.  Buffer 2 is reduced in two views with a gap between them, which keeps each rank's own
-# data; buffer 3 is small enough that a two-shot group of three gives one rank an empty share.
+SMALL = (1000, 3000, 3000, 100)  # small symmetric buffers, each an allocation of its own.  Buffer 2 is
+# reduced in two views with a gap between them, which keeps each rank's own data; buffer 3 is small
+# enough that a two-shot group of three gives one rank an empty share.
 GAP = (1000, 2000)
 
 
@@ -248,8 +248,8 @@ def _in_place_worker(rank: int, world: int, store: str, out_dir: str, algorithm:
 def test_ipc_in_place_all_reduce(tmp_path, world, algorithm):
     """``comm.all_reduce`` in place on rows of an IpcGroup buffer with no reduce target: every rank
     ends with the rank-ordered sum while its peers read its row concurrently, elements between
-    reduced views keep each rank's own data, and a peer allocation that holds several rows is
-    mapped once.  Then ``comm.reduce_scatter_tensor`` and ``comm.all_gather_into_tensor`` over
+    reduced views keep each rank's own data, and every row is an allocation of its own, mapped
+    once by each peer.  Then ``comm.reduce_scatter_tensor`` and ``comm.all_gather_into_tensor`` over
     symmetric rows."""
     store = str(tmp_path / "store")
     print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm} in-place all-reduce)", flush=True)
@@ -266,7 +266,7 @@ def test_ipc_in_place_all_reduce(tmp_path, world, algorithm):
                     want[GAP[0] : GAP[1]] = hosts[rank][k][GAP[0] : GAP[1]]
                 with np.load(tmp_path / f"inplace_r{rank}.npz", allow_pickle=False) as d:
                     got = d[f"sum_{step}_{k}"]
-                    assert int(d["mapped"]) <= len(SMALL) * (world - 1)
+                    assert int(d["mapped"]) == len(SMALL) * (world - 1)
                 assert same_bits(got, want), f"step {step} buffer {k} rank {rank}: " + first_mismatch(got, want)
     inputs = [_rs_rows(r, world) for r in range(world)]
     for rank in range(world):
@@ -532,3 +532,56 @@ def test_ipc_two_shot_equals_one_shot_at_cfg1_size(tmp_path):
             assert bool(d["found_one_shot"]) and bool(d["found_two_shot"])
             assert bool(d["equal"]), f"rank {rank}: two-shot gradients differ from one-shot"
             assert float(d["bucket_sum_one_shot"]) == float(d["bucket_sum_two_shot"])
+
+
+ROW = 1 << 20  # fp32 elements of the row allocated after a large block was cached
+
+
+def _cached_segment_worker(rank: int, world: int, store: str, out_dir: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        big = torch.empty(3 << 30, dtype=torch.uint8, device=dev)
+        del big  # the caching allocator keeps the 3 GiB segment: a small request could be carved from it
+        from minidist import _native
+
+        group = IpcGroup(dist.group.WORLD, dev)
+        row = group.zeros(ROW, torch.float32)
+        h = _native.ipc_export(row.data_ptr())
+        row.fill_(float(rank + 1))
+        torch.cuda.synchronize()
+        dist.barrier()
+        seen = []
+        for r, addr in enumerate(group.row_addresses(row)):  # every rank's row, through its mapping
+            copy = torch.empty(ROW, device=dev)
+            _native.pack(_native.spans_array([(addr, copy.data_ptr(), ROW)]), _native.MDX_F32, _native.MDX_F32,
+                         1.0, False, torch.cuda.current_stream(dev).cuda_stream)
+            torch.cuda.synchronize()
+            seen.append(copy.cpu().numpy())
+        dist.barrier()
+        group.release()
+        np.savez(os.path.join(out_dir, f"seg_r{rank}.npz"), offset=np.array(h.offset),
+                 alloc=np.array(h.alloc_bytes), seen=np.stack(seen))
+    finally:
+        dist.destroy_process_group()
+
+
+def test_ipc_row_is_its_own_allocation(tmp_path):
+    """A symmetric row allocated while the caching allocator holds a 3 GiB free segment is still an
+    allocation of its own: its IPC export starts at the row (offset 0) and covers the segment the
+    allocator sizes for the request alone (20 MiB under 10 MiB, else the request rounded up to
+    2 MiB), never split for another tensor -- not the cached segment, which the runtime could not
+    map (2 GiB and more) and which would hand every peer unrelated tensors -- and each rank reads
+    every peer's row through its mapping."""
+    world = 2
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup rows after a cached 3 GiB segment)", flush=True)
+    mp.spawn(_cached_segment_worker, args=(world, store, str(tmp_path)), nprocs=world, join=True)
+    for rank in range(world):
+        with np.load(tmp_path / f"seg_r{rank}.npz", allow_pickle=False) as d:
+            assert int(d["offset"]) == 0
+            assert ROW * 4 <= int(d["alloc"]) <= max(20 << 20, -(-ROW * 4 // (2 << 20)) * (2 << 20))
+            for r in range(world):
+                assert np.all(d["seen"][r] == float(r + 1)), f"rank {rank} read rank {r}'s row"
