@@ -684,6 +684,7 @@ const char* mdx_strerror(int code) {
     case MDX_ESIZE: return "mdx: plan buffer missing or too small (required size returned)";
     case MDX_ESCRATCH:
       return "mdx: plan larger than MDX_NOALLOC_SCRATCH_BYTES (256 KiB), or stream not on the current device";
+    case MDX_EOP: return "mdx: unsupported reduction op (MDX_OP_SUM, MDX_OP_PRODUCT, MDX_OP_MIN, MDX_OP_MAX)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -727,6 +728,65 @@ int mdx_cast_f32_bf16(const float* src, uint16_t* dst, int64_t numel, void* stre
   mdx_span sp{src, dst, numel};
   CopyParams p{1.0f, 0, nullptr, nullptr};
   return run_copy(&sp, 1, MDX_F32, MDX_BF16, p, false, static_cast<hipStream_t>(stream));
+}
+
+int mdx_allreduce_op(const void* const* replicas, int world, int dtype, int op, const int64_t* offsets,
+                     const int64_t* numels, int n_runs, void* out, void* stream) {
+  if (op == MDX_OP_SUM) return mdx_allreduce_sum(replicas, world, dtype, offsets, numels, n_runs, out, stream);
+  if (op != MDX_OP_PRODUCT && op != MDX_OP_MIN && op != MDX_OP_MAX) return MDX_EOP;
+  if (!valid_dtype(dtype)) return MDX_EDTYPE;
+  if (world < 1 || world > MDX_MAX_WORLD) return MDX_EWORLD;
+  if (n_runs < 0 || replicas == nullptr) return MDX_EINVAL;
+  if (n_runs > 0 && (offsets == nullptr || numels == nullptr)) return MDX_EINVAL;
+  int64_t end = 0;
+  bool any = false;
+  for (int k = 0; k < n_runs; ++k) {
+    if (offsets[k] < 0 || numels[k] < 0 || offsets[k] < end) return MDX_EINVAL;
+    end = offsets[k] + numels[k];
+    any = any || numels[k] > 0;
+  }
+  if (!any) return MDX_OK;
+  if (out == nullptr) return MDX_EINVAL;
+  const int es = dtype_size(dtype);
+  OpParams p;
+  memset(&p, 0, sizeof(p));
+  for (int r = 0; r < world; ++r) {
+    if (replicas[r] == nullptr) return MDX_EINVAL;
+    // Same base = the in-place case; any other overlap of the reduced extent is rejected.
+    if (replicas[r] != out && any_overlap(replicas[r], end * es, out, end * es)) return MDX_EALIAS;
+    p.rep[r] = replicas[r];
+  }
+  p.out = out;
+  p.world = world;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  constexpr int64_t kElemsPerBlock = int64_t(kOpLanes) * kOpPerLane;
+  OpRuns t;
+  memset(&t, 0, sizeof(t));
+  int blocks = 0;
+  auto flush = [&]() -> int {
+    if (t.count == 0) return MDX_OK;
+    t.first_block[t.count] = blocks;
+    const int r = status(launch_allreduce_op(dtype, op, t, blocks, p, st));
+    memset(&t, 0, sizeof(t));
+    blocks = 0;
+    return r;
+  };
+  for (int k = 0; k < n_runs; ++k) {
+    // runs of at most kMaxRunElems elements keep every dispatch far below 2^31 workgroups
+    for (int64_t a = 0; a < numels[k]; a += kMaxRunElems) {
+      if (t.count == kRunsPerLaunch) {
+        const int rc = flush();
+        if (rc != MDX_OK) return rc;
+      }
+      const int64_t n = min_i64(kMaxRunElems, numels[k] - a);
+      t.offset[t.count] = offsets[k] + a;
+      t.numel[t.count] = n;
+      t.first_block[t.count] = blocks;
+      blocks += int((n + kElemsPerBlock - 1) / kElemsPerBlock);
+      ++t.count;
+    }
+  }
+  return flush();
 }
 
 int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,

@@ -354,6 +354,27 @@ constexpr int share_unroll(int wmax, int frag_in_bytes) {
   return clamp_unroll(kReduceLoadBytesPerLane / (wmax * frag_in_bytes));
 }
 
+// Non-SUM all-reduce (mdx_allreduce_op): runs of the replica layout in the
+// kernel arguments, kOpLanes x kOpPerLane elements per workgroup.
+constexpr int kOpLanes = 256;
+constexpr int kOpPerLane = 8;
+
+struct OpRuns {
+  int64_t offset[kRunsPerLaunch];
+  int64_t numel[kRunsPerLaunch];
+  int32_t first_block[kRunsPerLaunch + 1];
+  int32_t count;
+};
+
+struct OpParams {
+  const void* rep[MDX_MAX_WORLD];
+  void* out;
+  int32_t world;
+};
+
+hipError_t launch_allreduce_op(int dtype, int op, const OpRuns& t, int blocks, const OpParams& p,
+                               hipStream_t stream);
+
 // Host-side dispatch into the instantiating translation units.
 hipError_t launch_allreduce(int dtype, int grad_dtype, bool unpack, int world, const PieceBatch& b,
                             const ReduceParams& p, hipStream_t stream);

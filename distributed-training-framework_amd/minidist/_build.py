@@ -33,6 +33,7 @@ SOURCES = [
     "mdx_allreduce_wide_f16.hip",
     "mdx_allreduce_pack.hip",
     "mdx_allreduce_pack_wide.hip",
+    "mdx_allreduce_op.hip",
     "mdx_share_fast.hip",
     "mdx_share_generic.hip",
     "mdx_share_generic_bf16.hip",

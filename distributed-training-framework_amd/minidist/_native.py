@@ -25,7 +25,9 @@ MDX_F32 = 0
 MDX_BF16 = 1
 MDX_F16 = 2
 MDX_MAX_WORLD = 16
-ABI_VERSION = 9
+ABI_VERSION = 10
+# Reduction operations of mdx_allreduce_op (torch.distributed.ReduceOp's SUM, PRODUCT, MIN, MAX).
+MDX_OP_SUM, MDX_OP_PRODUCT, MDX_OP_MIN, MDX_OP_MAX = 0, 1, 2, 3
 
 # Every function declared in include/mdx.h, with (restype, argtypes).
 _vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -34,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
     "mdx_unpack": (_i32, [_vp, _i32, _i32, _i32, _f32, _vp, _vp]),
     "mdx_unscale_found_inf": (_i32, [_vp, _i32, _i32, _f32, _vp, _vp]),
     "mdx_allreduce_sum": (_i32, [_vp, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
+    "mdx_allreduce_op": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _vp]),
     "mdx_allreduce_unpack": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp]),
     "mdx_allreduce_unpack_wide": (_i32, [_vp, _i32, _i32, _vp, _i32, _vp, _i32, _i32, _f32, _f32, _vp, _vp]),
     "mdx_reduce_scatter_share": (
@@ -210,6 +213,16 @@ def allreduce_sum(
     check(rc, "mdx_allreduce_sum")
 
 
+def allreduce_op(
+    replicas: list[int], dtype: int, op: int, offsets: list[int], numels: list[int], out: int, stream: int
+) -> None:
+    n = len(offsets)
+    offs = (ctypes.c_int64 * n)(*offsets)
+    nums = (ctypes.c_int64 * n)(*numels)
+    rc = lib().mdx_allreduce_op(_ptrs(replicas), len(replicas), dtype, op, offs, nums, n, out, stream)
+    check(rc, "mdx_allreduce_op")
+
+
 def grad_runs_array(rows: list[tuple[int, int, int]]) -> np.ndarray:
     return np.array(rows, dtype=GRAD_RUN_DTYPE)
 
@@ -276,6 +289,7 @@ MDX_EDTYPE = -2
 MDX_EALIAS = -4
 MDX_ESIZE = -5
 MDX_ESCRATCH = -6
+MDX_EOP = -7
 NOALLOC_SCRATCH_BYTES = 256 * 1024
 
 

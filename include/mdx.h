@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MDX_ABI_VERSION 9
+#define MDX_ABI_VERSION 10
 
 /* Only the entry points below are exported (the library builds with hidden
  * visibility by default). */
@@ -68,6 +68,7 @@ enum {
   MDX_ESCRATCH = -6,  /* plan larger than MDX_NOALLOC_SCRATCH_BYTES, or the
                          stream is not on the current device (allocation-free
                          entry point only)                                  */
+  MDX_EOP = -7,       /* reduction operation not one of MDX_OP_*           */
 };
 
 #define MDX_MAX_WORLD 16
@@ -137,6 +138,27 @@ MDX_API int mdx_unscale_found_inf(const mdx_span* spans, int n_spans, int dtype,
  * (minidist/comm.py:223-234) on DDP buckets (minidist/ddp.py:243-247). */
 MDX_API int mdx_allreduce_sum(const void* const* replicas, int world, int dtype, const int64_t* offsets,
                       const int64_t* numels, int n_runs, void* out, void* stream);
+
+/* Reduction operations of mdx_allreduce_op: torch.distributed.ReduceOp's
+ * SUM, PRODUCT, MIN and MAX. */
+enum { MDX_OP_SUM = 0, MDX_OP_PRODUCT = 1, MDX_OP_MIN = 2, MDX_OP_MAX = 3 };
+
+/* mdx_allreduce_sum with the reduction `op`: per element, in the fixed rank
+ * order, acc = in[0], then acc = f(acc, in[r]) for r = 1 .. W-1, with f the
+ * IEEE 754-2019 operation that torch's CPU elementwise op computes in `dtype`:
+ *   MDX_OP_MAX      maximum: NaN if either is NaN, else the larger (-0 < +0)
+ *   MDX_OP_MIN      minimum: NaN if either is NaN, else the smaller (-0 < +0)
+ *   MDX_OP_PRODUCT  mul: one rounding per step
+ * A NaN result of MAX or MIN is the dtype's quiet NaN (0x7FC00000, 0x7FC0,
+ * 0x7E00); a tie of -0 and +0 gives +0 (MAX) or -0 (MIN) in either order;
+ * MDX_OP_SUM is mdx_allreduce_sum.  Layout, runs and aliasing rules
+ * are mdx_allreduce_sum's (`out` may be a replica base: in place).
+ * Replaces the reduction of comm.all_reduce(tensor, op) (minidist/comm.py:
+ * 223-234) and of comm.reduce_scatter_tensor(output, input_, op) (comm.py:
+ * 252-265) for op in PRODUCT / MIN / MAX -- the reference forwards any op to
+ * dist.*, e.g. the scaler's found-inf MAX (minidist/amp.py:216-217). */
+MDX_API int mdx_allreduce_op(const void* const* replicas, int world, int dtype, int op, const int64_t* offsets,
+                             const int64_t* numels, int n_runs, void* out, void* stream);
 
 /* One parameter's slice of a bucket for the fused all-reduce + unpack:
  * elements [offset, offset + numel) of the replica layout are delivered to

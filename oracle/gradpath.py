@@ -43,6 +43,9 @@ pack / unpack              torch CPU ``copy_`` + ``mul_`` on the same inputs;
                            identity round trip
 allreduce_sum              torch CPU sequential ``add_`` (fp32) and bf16 ``+``;
                            exact closed form W*x for power-of-two W
+allreduce_op               torch CPU ``maximum`` / ``minimum`` / ``mul`` chains
+                           over special values; numpy's max / min reductions
+                           and exact power-of-two products
 unscale_found_inf          torch CPU ``mul_`` + ``isfinite``; special values
 ScalerState                known answers of tests/test_amp.py:19-104
 fsdp_layout                closed form ceil(total/W); tests/test_fsdp.py
@@ -251,6 +254,60 @@ def allreduce_sum(contribs: list[np.ndarray], dtype: str) -> np.ndarray:
     acc = np.array(contribs[0], copy=True)
     for c in contribs[1:]:
         acc = add(acc, c, dtype)
+    return acc
+
+
+QUIET_NAN_BITS = {F32: 0x7FC00000, BF16: 0x7FC0, F16: 0x7E00}
+
+
+def _bits(a: np.ndarray, dtype: str) -> np.ndarray:
+    """The stored bit patterns of an oracle array (uint32 for fp32, uint16 otherwise)."""
+    a = np.asarray(a)
+    return a.view(np.uint32) if dtype == F32 else a.view(np.uint16)
+
+
+def _from_bits_of(u: np.ndarray, dtype: str) -> np.ndarray:
+    return u.view(np.float32) if dtype == F32 else (u if dtype == BF16 else u.view(np.float16))
+
+
+def allreduce_op(contribs: list[np.ndarray], dtype: str, op: str) -> np.ndarray:
+    """all_reduce with ``op`` in {"product", "min", "max"}, fixed rank order 0..W-1.
+
+    minidist/comm.py:223-234 forwards ``op`` to the backend; the oracle folds
+    ``acc = f(acc, c_r)`` in ``dtype`` with ``f`` the IEEE 754-2019 operations
+    that torch's ``maximum`` / ``minimum`` and ``mul`` compute on the CPU:
+    ``maximum`` / ``minimum`` -- NaN when either is NaN, else the larger /
+    smaller value, where -0 < +0 (torch itself returns its first operand on a
+    tie of -0 and +0 in its scalar loop and its second in its vectorised one;
+    the IEEE rule makes the fold independent of rank order); ``mul`` -- the
+    fp32 product rounded once to ``dtype``.  A NaN from maximum / minimum is
+    the dtype's quiet NaN.
+    """
+    if op not in ("product", "min", "max"):
+        raise ValueError(f"allreduce_op: unknown op {op!r}")
+    acc = np.array(contribs[0], copy=True)
+    for c in contribs[1:]:
+        c = np.asarray(c)
+        a, b = to_f32(acc, dtype), to_f32(c, dtype)
+        if op == "product":
+            with np.errstate(over="ignore", invalid="ignore", under="ignore"):
+                acc = from_f32(a * b, dtype)
+            continue
+        # equal values have equal bits except the zeros: -0 & +0 = +0 (max), -0 | +0 = -0 (min)
+        ua, ub = _bits(acc, dtype), _bits(c, dtype)
+        tie = (ua & ub) if op == "max" else (ua | ub)
+        res = _from_bits_of(np.where(a < b, ub, np.where(b < a, ua, tie)) if op == "max"
+                            else np.where(b < a, ub, np.where(a < b, ua, tie)), dtype)
+        nan = np.isnan(a) | np.isnan(b)
+        if nan.any():
+            bits = QUIET_NAN_BITS[dtype]
+            if dtype == F32:
+                res[nan] = np.array([bits], dtype=np.uint32).view(np.float32)[0]
+            elif dtype == BF16:
+                res[nan] = np.uint16(bits)
+            else:
+                res[nan] = np.array([bits], dtype=np.uint16).view(np.float16)[0]
+        acc = res
     return acc
 
 

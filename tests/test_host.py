@@ -54,7 +54,8 @@ def test_exported_symbols_are_only_the_abi():
 
 
 def test_strerror_names_every_mdx_code():
-    for code_, frag in [(0, "success"), (-1, "invalid"), (-2, "dtype"), (-3, "world"), (-4, "overlap")]:
+    for code_, frag in [(0, "success"), (-1, "invalid"), (-2, "dtype"), (-3, "world"), (-4, "overlap"),
+                        (-7, "reduction op")]:
         assert frag in nat.strerror(code_)
     assert "unknown" in nat.strerror(-99)
 
@@ -118,6 +119,16 @@ def test_argument_checks_happen_before_any_launch():
     # dtypes 2 pass the dtype check; the out-of-range rank is what is rejected (nothing launches)
     assert L.mdx_reduce_scatter_share(pc.ctypes.data, 1, peers, 2, 2, 2, 2, 1, P(1 << 20), 2, 0, 1.0, None,
                                       None) == -3
+    # the non-SUM all-reduce: op, then mdx_allreduce_sum's checks
+    assert L.mdx_allreduce_op(reps, 2, 0, 4, offs, nums, 1, P(4096), None) == nat.MDX_EOP
+    assert L.mdx_allreduce_op(reps, 2, 0, -1, offs, nums, 1, P(4096), None) == nat.MDX_EOP
+    for op in (nat.MDX_OP_PRODUCT, nat.MDX_OP_MIN, nat.MDX_OP_MAX, nat.MDX_OP_SUM):
+        assert L.mdx_allreduce_op(reps, 2, 9, op, offs, nums, 1, P(4096), None) == -2
+        assert L.mdx_allreduce_op(reps, 17, 0, op, offs, nums, 1, P(4096), None) == -3
+        assert L.mdx_allreduce_op(reps, 2, 0, op, bad_offs, bad_nums, 2, P(4096), None) == -1
+        assert L.mdx_allreduce_op(reps, 2, 0, op, offs, nums, 1, P(4096 + 4), None) == -4  # partial overlap
+        assert L.mdx_allreduce_op(reps, 2, 0, op, offs, nums, 1, None, None) == -1
+        assert L.mdx_allreduce_op(reps, 2, 2, op, offs, nums, 0, None, None) == 0  # nothing to reduce
 
 
 # ---------------------------------------------------------------------------

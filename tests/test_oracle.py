@@ -222,6 +222,61 @@ def test_allreduce_sum_matches_torch_sequential_add(rng, dtype, W):
     assert same_bits(got, _torch_bits(acc)), first_mismatch(got, _torch_bits(acc))
 
 
+TORCH_FOLD = {"max": torch.maximum, "min": torch.minimum, "product": torch.mul}
+
+
+@pytest.mark.parametrize("dtype", [o.F32, o.BF16, o.F16])
+@pytest.mark.parametrize("W", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("op", ["max", "min", "product"])
+def test_allreduce_op_matches_torch_chain(rng, dtype, W, op):
+    """The rank-ordered fold against torch CPU's own maximum / minimum / mul on the same tensors:
+    special values (NaN, +-inf, +-0, subnormals, overflow) and repeated values among the ranks.
+    For MAX and MIN the sign of a zero is compared separately (closed form below): torch answers
+    a tie of -0 and +0 differently in its scalar and vectorised loops."""
+    contribs = [o.from_f32(_random_with_specials(rng, 6000), dtype) for _ in range(W)]
+    if W > 1:
+        contribs[1][:500] = contribs[0][:500]  # ties between ranks
+    got = o.allreduce_op(contribs, dtype, op)
+    acc = _from_bits(contribs[0], dtype).clone()
+    for c in contribs[1:]:
+        acc = TORCH_FOLD[op](acc, _from_bits(c, dtype))
+    want = _torch_bits(acc)
+    if op != "product":
+        got, want = _unsigned_zeros(got, dtype), _unsigned_zeros(want, dtype)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+def _unsigned_zeros(a: np.ndarray, dtype: str) -> np.ndarray:
+    a = np.array(a, copy=True)
+    a[o.to_f32(a, dtype) == 0] = o.zeros(1, dtype)[0]
+    return a
+
+
+def test_allreduce_op_closed_forms(rng):
+    """Without NaNs MAX and MIN are numpy's max and min reductions (by value); products of signed
+    powers of two are exact; a tie of -0 and +0 is +0 under MAX and -0 under MIN in either rank
+    order (IEEE 754-2019 maximum / minimum), and -0 with -0 stays -0."""
+    x = rng.standard_normal((5, 4000)).astype(np.float32) * 1e3
+    contribs = list(x)
+    assert np.array_equal(o.allreduce_op(contribs, o.F32, "max"), x.max(axis=0))
+    assert np.array_equal(o.allreduce_op(contribs, o.F32, "min"), x.min(axis=0))
+    k = rng.integers(-20, 20, (6, 4000))
+    sign = rng.choice([-1.0, 1.0], (6, 4000))
+    p = (sign * 2.0 ** k).astype(np.float32)
+    want = (sign.prod(axis=0) * 2.0 ** k.sum(axis=0)).astype(np.float32)
+    assert np.array_equal(o.allreduce_op(list(p), o.F32, "product"), want)
+    for dtype in (o.F32, o.BF16, o.F16):
+        z, nz = o.from_f32(np.array([0.0], np.float32), dtype), o.from_f32(np.array([-0.0], np.float32), dtype)
+        for op, want_neg in (("max", False), ("min", True)):
+            for pair in ([nz, z], [z, nz], [nz, z, nz]):
+                got = o.to_f32(o.allreduce_op(pair, dtype, op), dtype)
+                assert got[0] == 0 and bool(np.signbit(got[0])) == want_neg, (dtype, op, pair)
+            both = o.to_f32(o.allreduce_op([nz, nz], dtype, op), dtype)
+            assert np.signbit(both[0])
+    nan = o.allreduce_op([np.array([1.0, np.nan], np.float32), np.array([np.nan, 2.0], np.float32)], o.F32, "max")
+    assert np.isnan(nan).all()
+
+
 @pytest.mark.parametrize("W", [2, 3, 7, 8, 16])
 def test_allreduce_sum_of_short_mantissa_copies_is_exact(rng, W):
     """Inputs k * 2^-10 with |k| < 2^16 keep every partial sum exact in fp32, so the
