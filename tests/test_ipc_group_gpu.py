@@ -585,3 +585,60 @@ def test_ipc_row_is_its_own_allocation(tmp_path):
             assert ROW * 4 <= int(d["alloc"]) <= max(20 << 20, -(-ROW * 4 // (2 << 20)) * (2 << 20))
             for r in range(world):
                 assert np.all(d["seen"][r] == float(r + 1)), f"rank {rank} read rank {r}'s row"
+
+
+OP_N, OP_S = 5000, 611  # all-reduce length; reduce-scatter share per rank
+
+
+def _op_rows(rank: int, n: int, seed: int) -> np.ndarray:
+    g = np.random.default_rng(seed + 131 * rank)
+    x = (g.standard_normal(n) * 4).astype(np.float32)
+    x[: n // 10] = np.random.default_rng(seed).standard_normal(n // 10).astype(np.float32)  # equal on every rank
+    x[g.integers(0, n, n // 50)] = np.float32(-0.0 if rank % 2 else 0.0)
+    x[g.integers(0, n, n // 200)] = np.float32(np.nan)
+    x[g.integers(0, n, n // 200)] = np.float32(np.inf if rank % 2 else -np.inf)
+    return x
+
+
+def _op_worker(rank: int, world: int, store: str, out_dir: str, algorithm: str) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=algorithm)
+        out = {}
+        for k, (name, op) in enumerate((("max", dist.ReduceOp.MAX), ("min", dist.ReduceOp.MIN),
+                                        ("product", dist.ReduceOp.PRODUCT))):
+            row = group.zeros(OP_N, torch.float32)
+            row.copy_(torch.from_numpy(_op_rows(rank, OP_N, 10 + k)).to(dev))
+            comm.all_reduce(row, op=op, group=group)  # in place: peers read this row meanwhile
+            out[f"ar_{name}"] = row.cpu().numpy()
+            inp = group.zeros(OP_S * world, torch.float32)
+            inp.copy_(torch.from_numpy(_op_rows(rank, OP_S * world, 20 + k)).to(dev))
+            rs = torch.empty(OP_S, device=dev)
+            comm.reduce_scatter_tensor(rs, inp, op=op, group=group)
+            out[f"rs_{name}"] = rs.cpu().numpy()
+        group.release()
+        np.savez(os.path.join(out_dir, f"op_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("world,algorithm", [(2, "one_shot"), (3, "two_shot"), (4, "one_shot")])
+def test_ipc_non_sum_ops(tmp_path, world, algorithm):
+    """``comm.all_reduce`` (in place) and ``comm.reduce_scatter_tensor`` with MAX, MIN and PRODUCT over
+    an IpcGroup: one-shot over the mapped rows whatever the group's algorithm, every rank's result
+    bit for bit the oracle's rank-ordered fold (NaN, +-inf, +-0 and values equal on every rank)."""
+    store = str(tmp_path / "store")
+    print(f"spawning {world} ranks on cuda:0 (IpcGroup {algorithm}: MAX / MIN / PRODUCT)", flush=True)
+    mp.spawn(_op_worker, args=(world, store, str(tmp_path), algorithm), nprocs=world, join=True)
+    for k, name in enumerate(("max", "min", "product")):
+        want_ar = o.allreduce_op([_op_rows(r, OP_N, 10 + k) for r in range(world)], o.F32, name)
+        rs_in = [_op_rows(r, OP_S * world, 20 + k) for r in range(world)]
+        for rank in range(world):
+            with np.load(tmp_path / f"op_r{rank}.npz", allow_pickle=False) as d:
+                got_ar, got_rs = d[f"ar_{name}"], d[f"rs_{name}"]
+            assert same_bits(got_ar, want_ar), f"all_reduce {name} rank {rank}: " + first_mismatch(got_ar, want_ar)
+            want_rs = o.allreduce_op([x[rank * OP_S : (rank + 1) * OP_S] for x in rs_in], o.F32, name)
+            assert same_bits(got_rs, want_rs), f"reduce_scatter {name} rank {rank}: " + first_mismatch(got_rs, want_rs)
