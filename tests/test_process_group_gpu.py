@@ -23,6 +23,7 @@ the wrapper's own, which therefore run first.
 from __future__ import annotations
 
 import os
+from contextlib import nullcontext
 from datetime import timedelta
 
 import numpy as np
@@ -33,7 +34,7 @@ import torch.multiprocessing as mp
 
 import tiny_gpt
 from conftest import first_mismatch, same_bits
-from minidist import DDP, FSDP, DistributedGradScaler, MixedPrecisionPolicy
+from minidist import DDP, FSDP, DistributedGradScaler, MixedPrecisionPolicy, comm
 from oracle import gradpath as o
 
 pytestmark = pytest.mark.gpu
@@ -93,9 +94,12 @@ def _ddp_rank(rank: int, out_dir: str, comm_stream: bool) -> None:
         state["inject"] = step == 1
         for p in params:
             p.grad = None
-        _, loss = ddp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
-        scaler.scale_loss(loss).backward()
-        out[f"found_{step}"] = np.array(scaler.unscale_(_Opt()))
+        with comm.record_comm() if step == 0 else nullcontext() as stats:
+            _, loss = ddp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+            scaler.scale_loss(loss).backward()
+            out[f"found_{step}"] = np.array(scaler.unscale_(_Opt()))
+        if step == 0:
+            _save_rows(out, stats)
         scaler.update()
         for i, p in enumerate(params):
             out[f"local_{step}_{i}"] = _bits(local[id(p)])
@@ -127,14 +131,26 @@ def _fsdp_rank(rank: int, param_dtype: torch.dtype, out_dir: str, unit_batch: in
         for u, unit in enumerate(fsdp._units):
             out[f"full_{u}"] = _bits(unit._full)
     ids, tgt = tiny_gpt.batch(c, 8, seed=6)
-    _, loss = fsdp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
-    loss.backward()
+    with comm.record_comm() as stats:
+        _, loss = fsdp(ids.chunk(W)[rank].to(dev), tgt.chunk(W)[rank].to(dev))
+        loss.backward()
+    _save_rows(out, stats)
     for i, p in enumerate(params):
         out[f"local_{i}"] = _bits(local[id(p)])
     for u, unit in enumerate(fsdp._units):
         out[f"shard_grad_{u}"] = _bits(unit.flat_shard.grad)
     out["units"] = np.array(len(fsdp._units))
     np.savez(os.path.join(out_dir, f"fsdp_r{rank}.npz"), **out)
+
+
+def _save_rows(out: dict, stats: comm.CommStats) -> None:
+    rows = stats.as_rows()
+    out["comm_names"] = np.array([r[0] for r in rows])
+    out["comm_rows"] = np.array([r[1:] for r in rows], dtype=np.int64).reshape(len(rows), 3)
+
+
+def _recorded(res: dict) -> dict[str, tuple[int, int, int]]:
+    return {str(n): tuple(int(v) for v in row) for n, row in zip(res["comm_names"], res["comm_rows"], strict=True)}
 
 
 def _train(model, rank: int, steps: int = 4, lr: float = 1e-2):
@@ -227,6 +243,12 @@ def test_ddp_two_processes_bitwise(tmp_path, comm_stream):
             # the MAX exchange makes the decision unanimous: only rank 1 overflowed in step 1
             assert bool(res[rank][f"found_{step}"]) == want["found_inf"] == (step == 1)
     assert all(float(res[r]["scale_after"]) == SCALE / 2 for r in range(W))
+    # what step 0 recorded (comm.py:232-233): one all-reduce per bucket of the oracle's partition; the
+    # scaler's flag exchange goes straight to the backend, unrecorded, as in the reference (amp.py:216-217)
+    layout = o.build_buckets([k * 4 for k in numels], CAP_MB)
+    payloads = [sum(numels[i] * 4 for i in b) for b in layout]
+    want = {"all_reduce": (len(layout), sum(payloads), sum(int(2 * (W - 1) / W * b) for b in payloads))}
+    assert all(_recorded(res[r]) == want for r in range(W))
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16", "bf16-ub2"])
@@ -254,6 +276,17 @@ def test_fsdp_two_processes_bitwise(tmp_path, dtype):
             want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, o.F32)
             got = res[rank][f"shard_grad_{u}"]
             assert same_bits(got, want), f"unit {u} rank {rank}: " + first_mismatch(got, want)
+    # what the step recorded (comm.py:247-248, 263-264): every block unit gathered for its forward and
+    # its backward, the root unit (the last) once; one reduce-scatter of the padded fp32 buffer per unit
+    padded = []
+    for u in range(n_units):
+        total = sum(init0[int(i)].size for i in res[0][f"unit_{u}_params"])
+        padded.append(-(-total // W) * W)
+    gathers = [p for p in padded[:-1] for _ in range(2)] + [padded[-1]]
+    gb = 4 if pdt == o.F32 else 2
+    want = {"all_gather": (len(gathers), sum(p * gb for p in gathers), sum(int((W - 1) / W * p * gb) for p in gathers)),
+            "reduce_scatter": (n_units, sum(p * 4 for p in padded), sum(int((W - 1) / W * p * 4) for p in padded))}
+    assert all(_recorded(res[r]) == want for r in range(W))
 
 
 def _close(got: np.ndarray, want: np.ndarray, tol: float) -> float:
