@@ -808,6 +808,7 @@ class FullyShardedDataParallel(nn.Module):
         self._chain_index = {id(u): i for i, u in enumerate(self._chain)}
         self._held_reductions: list[_FSDPUnit] = []
         self._prefetched_for_backward: list[_FSDPUnit] = []
+        self._prefetched_for_forward: dict[int, _FSDPUnit] = {}
         self._end_queued = False
         for unit in self._units:
             unit.streams = self._streams
@@ -981,16 +982,20 @@ class FullyShardedDataParallel(nn.Module):
         expectation is registration order; where the model runs its units in another
         order, a backward batch leaves out every unit whose backward this step has
         already completed (gathering it again would keep pre-update weights past the
-        optimizer step), and a unit it brought along whose backward then never comes is
-        freed when the engine finishes the backward, so every unit is sharded after
-        backward, as in the reference."""
+        optimizer step), and a unit it brought along whose backward then never comes --
+        or, in forward, whose forward never comes -- is freed when the engine finishes the
+        backward, so every unit is sharded after backward, as in the reference."""
+        if forward:
+            self._prefetched_for_forward.pop(id(unit), None)  # it runs after all
         if not unit.is_unsharded:
             k = self.unit_batch
             i = self._chain_index.get(id(unit))
             if k == 1 or i is None:
                 unit.unshard()
             elif forward:
-                self._unshard_many([u for u in self._chain[i : i + k] if not u.is_unsharded])
+                batch = [u for u in self._chain[i : i + k] if not u.is_unsharded]
+                self._unshard_many(batch)
+                self._prefetched_for_forward.update((id(u), u) for u in batch if u is not unit)
             else:
                 ahead = [u for u in self._chain[max(0, i - k + 1) : i][::-1]
                          if not u.is_unsharded and not u._backward_done]
@@ -1040,6 +1045,8 @@ class FullyShardedDataParallel(nn.Module):
         self._end_queued = False
         self._reduce_held()
         prefetched, self._prefetched_for_backward = self._prefetched_for_backward, []
+        prefetched += self._prefetched_for_forward.values()
+        self._prefetched_for_forward = {}
         for unit in prefetched:
             unit.reshard()
         if self._streams is not None:

@@ -519,15 +519,15 @@ class _OrderBlock(torch.nn.Module):
 
 
 class _OutOfOrderNet(torch.nn.Module):
-    """Blocks registered 0..n-1 but run in ``order``: the unit chain a batched gather walks
-    (registration order) is not the order the units run in."""
+    """Blocks registered 0..n-1 but run in ``order`` (which may leave some out): the unit chain a
+    batched gather walks (registration order) is not the order the units run in."""
 
-    def __init__(self, order: list[int], seed: int = 17):
+    def __init__(self, order: list[int], seed: int = 17, n_blocks: int | None = None):
         super().__init__()
         g = torch.Generator().manual_seed(seed)
         self.order = list(order)
         self.inp = torch.nn.Linear(4, 8)
-        self.blocks = torch.nn.ModuleList([_OrderBlock(g) for _ in range(len(order))])
+        self.blocks = torch.nn.ModuleList([_OrderBlock(g) for _ in range(n_blocks or len(order))])
         self.head = torch.nn.Linear(8, 1)
         with torch.no_grad():
             for p in (*self.inp.parameters(), *self.head.parameters()):
@@ -549,10 +549,25 @@ def test_units_run_out_of_registration_order(order, unit_batch):
     weights).  Every unit is sharded after each backward (the reference's invariant,
     fsdp.py:199-213), and after 3 SGD steps this rank's shards equal its slice of the
     full-batch model's weights."""
+    _train_out_of_order(order, len(order), unit_batch)
+
+
+@pytest.mark.parametrize("order,n_blocks", [([0, 1, 3], 4), ([2, 0], 4), ([3, 1], 5)])
+@pytest.mark.parametrize("unit_batch", [2, 3])
+def test_units_skipped_in_forward(order, n_blocks, unit_batch):
+    """A batched forward gather brings the next units in registration order along; one the model
+    then skips never runs, so no hook reshards it: it is freed when the engine finishes the
+    backward, and every unit is sharded after each backward (the reference never gathers a
+    skipped unit).  The skipped units get no gradient and keep their weights; the SGD
+    trajectory still matches the full batch."""
+    _train_out_of_order(order, n_blocks, unit_batch)
+
+
+def _train_out_of_order(order, n_blocks, unit_batch):
     W, rank, steps, lr = 2, 1, 3, 0.2
     x = torch.randn(8, 4, generator=torch.Generator().manual_seed(23)).to(DEV)
-    ref = _OutOfOrderNet(order).to(DEV)
-    model = _OutOfOrderNet(order).to(DEV)
+    ref = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
+    model = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
     names_by_id = {id(p): n for n, p in model.named_parameters()}
     fsdp = FSDP(model, unit_types=(_OrderBlock,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
     opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
@@ -564,12 +579,13 @@ def test_units_run_out_of_registration_order(order, unit_batch):
             flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
             S, shards = unit.shard_numel, unit.peer_param_shards()
             shards[1 - rank].copy_(flat[(1 - rank) * S : (2 - rank) * S])
-        peer = _OutOfOrderNet(order).to(DEV)
+        peer = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
         with torch.no_grad():
             for n, p in peer.named_parameters():
                 p.copy_(cur[n])
         peer(x.chunk(W)[1 - rank]).backward()
-        replica = [{n: p.grad.detach().clone() for n, p in peer.named_parameters()}, {}]
+        replica = [{n: p.grad.detach().clone() if p.grad is not None else torch.zeros_like(p)
+                    for n, p in peer.named_parameters()}, {}]
         _stage(fsdp, names_by_id, replica if rank == 1 else replica[::-1], rank, W)
         fsdp(x.chunk(W)[rank]).backward()
         assert not any(u.is_unsharded for u in fsdp._units), "a unit is still gathered after backward"
