@@ -24,7 +24,10 @@ unchanged.  What changes is what sits under the collective hook:
 
 from __future__ import annotations
 
+import mmap
 import os
+import time
+import uuid
 from collections.abc import Iterator, Sequence
 from contextlib import contextmanager
 from dataclasses import dataclass, field
@@ -751,6 +754,98 @@ def _fused_reduce_dtype(wire: torch.Tensor, bucket: torch.Tensor | None, reduce_
     return reduce_dtype
 
 
+class _HostFence:
+    """A barrier of the processes of one host, in POSIX shared memory.
+
+    Each rank owns one 64-byte line: its epoch and two payload slots of three
+    int64, used in alternate epochs.  A rank entering barrier ``e`` writes its
+    payload into slot ``e % 2``, then ``e`` into its epoch, and spins until
+    every rank's epoch reaches ``e``; a rank can be at most one barrier ahead
+    of the slowest (it cannot pass the next one alone), so the other slot still
+    holds what the slowest rank reads.  Stores of aligned 8-byte words are
+    single instructions and x86 keeps stores in program order, so a peer that
+    sees the epoch also sees the payload written before it.  No kernel waits
+    on a host flag: only the host threads of the group spin.
+
+    Rank 0 creates the segment and unlinks its name once every rank has mapped
+    it, so nothing is left in /dev/shm whatever happens to the processes."""
+
+    LINE = 8  # int64 words per rank: epoch, payload slot 0 (3), payload slot 1 (3), pad
+    PAYLOAD = 3
+
+    def __init__(self, process_group, world: int, rank: int, timeout_s: float = 120.0):
+        self._world, self._rank, self._timeout = world, rank, timeout_s
+        size = world * self.LINE * 8
+        path, mapped = None, None
+        if rank == 0:
+            try:
+                path = os.path.join(self.SHM_DIR, f"mdx_fence_{uuid.uuid4().hex[:16]}")
+                mapped = self._map(path, size, create=True)
+            except OSError:
+                path, mapped = None, None
+        names: list = [None] * world
+        dist.all_gather_object(names, (path, os.uname().nodename), group=process_group)
+        usable = names[0][0] is not None and len({host for _, host in names}) == 1
+        if usable and mapped is None:
+            try:
+                mapped = self._map(names[0][0], size, create=False)
+            except OSError:
+                mapped = None
+        # every rank has mapped the segment, or the group falls back together
+        ok: list = [None] * world
+        dist.all_gather_object(ok, usable and mapped is not None, group=process_group)
+        if rank == 0 and path is not None:
+            os.unlink(path)  # the mappings stay; the name goes
+        if not all(ok):
+            if mapped is not None:
+                mapped.close()
+            raise RuntimeError("no shared host memory for the group's fences")
+        self._mem = mapped
+        self._lines = np.ndarray((world, self.LINE), dtype=np.int64, buffer=mapped)
+        self._epoch = 0
+
+    SHM_DIR = "/dev/shm"
+
+    @staticmethod
+    def _map(path: str, size: int, create: bool) -> mmap.mmap:
+        flags = os.O_RDWR | (os.O_CREAT | os.O_EXCL if create else 0)
+        fd = os.open(path, flags, 0o600)
+        try:
+            if create:
+                os.ftruncate(fd, size)  # zero-filled
+            return mmap.mmap(fd, size)
+        finally:
+            os.close(fd)
+
+    def wait(self, payload: Sequence[int] | None = None) -> np.ndarray | None:
+        """Meet every rank; with ``payload`` (up to three ints), return every rank's, rank order."""
+        self._epoch += 1
+        e, slot = self._epoch, 1 + (self._epoch % 2) * self.PAYLOAD
+        line = self._lines[self._rank]
+        if payload is not None:
+            line[slot : slot + len(payload)] = payload
+        line[0] = e
+        epochs = self._lines[:, 0]
+        spins, deadline = 0, None
+        while (epochs < e).any():
+            spins += 1
+            if spins > 2000:  # a peer is far behind: stop burning its core
+                os.sched_yield()
+                if deadline is None:
+                    deadline = time.monotonic() + self._timeout
+                elif time.monotonic() > deadline:
+                    late = [r for r in range(self._world) if epochs[r] < e]
+                    raise RuntimeError(f"IpcGroup: ranks {late} did not reach host barrier {e} "
+                                       f"within {self._timeout:.0f} s")
+        if payload is None:
+            return None
+        return self._lines[:, slot : slot + len(payload)].copy()
+
+    def close(self) -> None:
+        self._lines = None
+        self._mem.close()
+
+
 class _IpcArena:
     """One symmetric buffer of an :class:`IpcGroup`: this rank's row is a tensor of its own;
     the peers' rows are inside their allocations, mapped into this process over IPC."""
@@ -832,11 +927,16 @@ class IpcGroup(ResidentGroup):
         self.symmetric_targets = algorithm == "two_shot"
         self.plans_reductions = algorithm == "one_shot"
         self._released = False
-        # A peer's allocation mapped into this process, by (rank, handle bytes): the
-        # caching allocator may carve two small rows out of one allocation, whose
-        # exports then name the same memory; it is mapped once and unmapped once.
+        # A peer's allocation mapped into this process, by (rank, handle bytes): every row is
+        # an allocation of its own, so one mapping per peer row, unmapped once.
         self._mapped: dict[tuple[int, bytes], int] = {}
         super().__init__(dist.get_world_size(process_group), dist.get_rank(process_group), device)
+        # The fences between the steps of a collective: IPC maps memory between the processes of
+        # one host, so they meet in shared memory rather than over the process group's transport.
+        try:
+            self._fence: _HostFence | None = _HostFence(process_group, self._world, self._rank)
+        except (OSError, RuntimeError):
+            self._fence = None  # the process group's own barrier
 
     def __repr__(self) -> str:
         return (f"IpcGroup(world_size={self._world}, rank={self._rank}, device={self.device}, "
@@ -895,13 +995,16 @@ class IpcGroup(ResidentGroup):
     def release(self) -> None:
         """Unmap every peer row (collective: no rank still reads a row when it is released)."""
         torch.cuda.current_stream(self.device).synchronize()
-        dist.barrier(group=self.process_group)
+        self._barrier()
         for base in self._mapped.values():
             _native.ipc_close_base(base)
         self._mapped.clear()
         self._arenas.clear()
         # plans built over this group still hold the peers' (now unmapped) addresses
         self._released = True
+        if self._fence is not None:
+            self._fence.close()
+            self._fence = None
 
     # -- the one-shot protocol ----------------------------------------------
 
@@ -909,16 +1012,22 @@ class IpcGroup(ResidentGroup):
         if self._released:
             raise RuntimeError("IpcGroup: the peers' rows were released; no collective can run over them")
 
+    def _barrier(self) -> None:
+        if self._fence is not None:
+            self._fence.wait()
+        else:
+            dist.barrier(group=self.process_group)
+
     def rows_written(self) -> None:
         """Every rank's writes to its rows are complete (this one's: its stream is drained)."""
         self._check_open()
         torch.cuda.current_stream(self.device).synchronize()
-        dist.barrier(group=self.process_group)
+        self._barrier()
 
     def rows_read(self) -> None:
         """Every rank has finished reading its peers' rows."""
         torch.cuda.current_stream(self.device).synchronize()
-        dist.barrier(group=self.process_group)
+        self._barrier()
 
     def _one_shot(self, launch, async_op: bool):
         self.rows_written()
@@ -956,10 +1065,11 @@ class IpcGroup(ResidentGroup):
         return int(live["offset"].min()), int((live["offset"] + live["numel"]).max())
 
     def _runs_agreed(self, runs: np.ndarray) -> None:
-        """:meth:`rows_written` of a two-shot reduction.  Its barrier is a MAX over the runs'
-        signature (first element, end, a hash of every run's offset and length) and its
-        negation, which also checks that every rank reduces the same runs: each reduces its
-        share of them for all the others."""
+        """:meth:`rows_written` of a two-shot reduction.  Its barrier carries the runs'
+        signature (first element, end, a hash of every run's offset and length), and every
+        rank checks that all the others handed in the same -- each reduces its share of the
+        runs for all the others.  Over the process group's own barrier the same check is a
+        MAX of the signature and of its negation."""
         self._check_open()
         torch.cuda.current_stream(self.device).synchronize()
         live = runs[runs["numel"] > 0]
@@ -967,9 +1077,13 @@ class IpcGroup(ResidentGroup):
         # tuples of ints hash the same in every process (no per-process salt)
         sig = hash(tuple(zip(live["offset"].tolist(), live["numel"].tolist()))) & ((1 << 62) - 1)
         mine = [lo, hi, sig]
-        both = torch.tensor(mine + [-x for x in mine], dtype=torch.int64)
-        dist.all_reduce(both, op=dist.ReduceOp.MAX, group=self.process_group)
-        if [int(x) for x in both[:3]] != [-int(x) for x in both[3:]]:
+        if self._fence is not None:
+            agreed = bool((self._fence.wait(mine) == np.array(mine, dtype=np.int64)).all())
+        else:
+            both = torch.tensor(mine + [-x for x in mine], dtype=torch.int64)
+            dist.all_reduce(both, op=dist.ReduceOp.MAX, group=self.process_group)
+            agreed = [int(x) for x in both[:3]] == [-int(x) for x in both[3:]]
+        if not agreed:
             raise RuntimeError(f"IpcGroup two-shot: the ranks reduce different runs (this rank: elements "
                                f"[{lo}, {hi}) in {len(live)} runs)")
 
