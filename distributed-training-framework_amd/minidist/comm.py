@@ -760,7 +760,9 @@ class _HostFence:
     Each rank owns one 64-byte line: its epoch and two payload slots of three
     int64, used in alternate epochs.  A rank entering barrier ``e`` writes its
     payload into slot ``e % 2``, then ``e`` into its epoch, and spins until
-    every rank's epoch reaches ``e``; a rank can be at most one barrier ahead
+    every rank's epoch reaches ``e`` (yielding its core once the wait is long,
+    sleeping between checks after a millisecond, failing after ``timeout_s``);
+    a rank can be at most one barrier ahead
     of the slowest (it cannot pass the next one alone), so the other slot still
     holds what the slowest rank reads.  Stores of aligned 8-byte words are
     single instructions and x86 keeps stores in program order, so a peer that
@@ -826,17 +828,23 @@ class _HostFence:
             line[slot : slot + len(payload)] = payload
         line[0] = e
         epochs = self._lines[:, 0]
-        spins, deadline = 0, None
+        spins, since = 0, None
         while (epochs < e).any():
             spins += 1
-            if spins > 2000:  # a peer is far behind: stop burning its core
+            if spins <= 2000:  # the peers are a few µs away: keep checking
+                continue
+            # a peer is further behind: give the core away, and after a millisecond sleep between checks
+            now = time.monotonic()
+            if since is None:
+                since = now
+            elif now - since > self._timeout:
+                late = [r for r in range(self._world) if epochs[r] < e]
+                raise RuntimeError(f"IpcGroup: ranks {late} did not reach host barrier {e} "
+                                   f"within {self._timeout:.0f} s")
+            if now - since > 1e-3:
+                time.sleep(2e-5)
+            else:
                 os.sched_yield()
-                if deadline is None:
-                    deadline = time.monotonic() + self._timeout
-                elif time.monotonic() > deadline:
-                    late = [r for r in range(self._world) if epochs[r] < e]
-                    raise RuntimeError(f"IpcGroup: ranks {late} did not reach host barrier {e} "
-                                       f"within {self._timeout:.0f} s")
         if payload is None:
             return None
         return self._lines[:, slot : slot + len(payload)].copy()
