@@ -36,6 +36,24 @@ def test_kernel_classification():
     assert not P.is_collective(GEMM) and not P.is_collective(TORCH_COPY)
 
 
+def test_mangled_kernel_names_and_bookkeeping_kernels():
+    """A tracer may record a kernel's mangled name: the path's kernels are recognised in that form
+    too (namespace mdx, ``_ZN3mdx``), with the same kinds.  The flag clear and the allocation-free
+    launch's plan upload have kinds of their own."""
+    mangled = {
+        "_ZN3mdx11reduce_impl21allreduce_pack_kernelIffLi8EEEvNS_10PieceBatchENS_12ReduceParamsE": "all_reduce",
+        "_ZN3mdx11reduce_impl16share_kernel_fewIN3mdx4bf16EffLi8EEEvNS_8PieceFewENS_12ReduceParamsE":
+            "reduce_scatter",
+        "_ZN3mdx12_GLOBAL__N_115copy_kernel_oneIfNS_4bf16ELi0ELb0EEEvNS_7SpanOneENS_10CopyParamsE": "bucket_copy",
+        "_ZN3mdx12_GLOBAL__N_117clear_flag_kernelEPi": "flag_clear",
+        "_ZN3mdx12_GLOBAL__N_113upload_kernelENS0_11UploadChunkEPh": "plan_upload",
+    }
+    for name, kind in mangled.items():
+        assert P.is_collective(name) and P.classify(name) == kind, name
+    assert P.classify("void mdx::(anonymous namespace)::clear_flag_kernel(int*)") == "flag_clear"
+    assert not P.is_collective("_ZN2at6native29vectorized_elementwise_kernelILi4EEEviT_")
+
+
 def _grid_measure(intervals, lo=0, hi=80):
     cover = np.zeros(hi - lo, dtype=bool)
     for a, b in intervals:
