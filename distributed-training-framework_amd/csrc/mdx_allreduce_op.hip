@@ -16,10 +16,14 @@
 // dtype's quiet NaN.  A product of two bf16 or fp16 values is exact in fp32,
 // so each step rounds once, to T, as torch's CPU multiply does.
 //
-// These reductions carry flags and small tensors, not the gradient stream:
-// workgroups of kOpLanes lanes take kOpPerLane elements each, lane-strided
-// (every load instruction of a wave reads consecutive elements), with the
-// runs in the dispatch's kernel arguments.
+// Layout of the work: one-wave workgroups; a lane takes U 16-byte vectors (E
+// elements each) of every replica, all loaded (non-temporal) before the first
+// fold, U = op_unroll(WMAX) so that about 128 bytes are in flight per lane,
+// with WMAX >= W a compile-time bound and the ranks past W predicated off.
+// Vector accesses go through the library's 2-byte-aligned vector views, so a
+// run at any element offset moves in vectors; the last fewer-than-E elements
+// of a run are folded one per lane by its last workgroup.  The runs travel in
+// the dispatch's kernel arguments.
 #include <type_traits>
 
 #include "mdx_internal.h"
@@ -69,57 +73,92 @@ __device__ __forceinline__ T fold(T acc, T x) {
   }
 }
 
-template <typename T, int OP>
-__global__ void __launch_bounds__(kOpLanes) allreduce_op_kernel(OpRuns t, OpParams p) {
+template <typename T, int OP, int WMAX>
+__global__ void __launch_bounds__(kBlock) allreduce_op_kernel(OpRuns t, OpParams p) {
+  constexpr int E = 16 / int(sizeof(T));
+  constexpr int U = op_unroll(WMAX);
   const int blk = int(blockIdx.x);
   const int s = find_run_in(t.first_block, 0, t.count, blk);
   const int64_t c = blk - t.first_block[s];
+  const int64_t nblk = t.first_block[s + 1] - t.first_block[s];
   const int64_t off = t.offset[s];
   const int64_t n = t.numel[s];
+  const int64_t nvec = n / E;
   const int lane = int(threadIdx.x);
+  const int world = p.world;
+  const T* rows[WMAX];
+#pragma unroll
+  for (int r = 0; r < WMAX; ++r) rows[r] = r < world ? static_cast<const T*>(p.rep[r]) + off : nullptr;
   T* out = static_cast<T*>(p.out) + off;
-  T acc[kOpPerLane];
+
+  T x[U][WMAX][E];
 #pragma unroll
-  for (int k = 0; k < kOpPerLane; ++k) {
-    const int64_t i = c * (kOpLanes * kOpPerLane) + int64_t(k) * kOpLanes + lane;
-    if (i < n) acc[k] = static_cast<const T*>(p.rep[0])[off + i];
-  }
-  for (int r = 1; r < p.world; ++r) {
-    const T* row = static_cast<const T*>(p.rep[r]) + off;
+  for (int u = 0; u < U; ++u) {
+    const int64_t v = c * (kBlock * U) + int64_t(u) * kBlock + lane;
+    if (v < nvec) {
 #pragma unroll
-    for (int k = 0; k < kOpPerLane; ++k) {
-      const int64_t i = c * (kOpLanes * kOpPerLane) + int64_t(k) * kOpLanes + lane;
-      if (i < n) acc[k] = fold<T, OP>(acc[k], row[i]);
+      for (int r = 0; r < WMAX; ++r) {
+        if (r < world) vload<T, E, true>(x[u][r], rows[r] + v * E);
+      }
     }
   }
-  // Every row has been read before the first store: the in-place form (out = a row's base)
-  // only rewrites elements this lane alone reads.
+  // Every replica's vectors are loaded before the first store: the in-place form (out = a
+  // replica's base) only rewrites elements this lane alone reads.
 #pragma unroll
-  for (int k = 0; k < kOpPerLane; ++k) {
-    const int64_t i = c * (kOpLanes * kOpPerLane) + int64_t(k) * kOpLanes + lane;
-    if (i < n) out[i] = acc[k];
+  for (int u = 0; u < U; ++u) {
+    const int64_t v = c * (kBlock * U) + int64_t(u) * kBlock + lane;
+    if (v < nvec) {
+      T acc[E];
+#pragma unroll
+      for (int k = 0; k < E; ++k) acc[k] = x[u][0][k];
+#pragma unroll
+      for (int r = 1; r < WMAX; ++r) {
+        if (r < world) {
+#pragma unroll
+          for (int k = 0; k < E; ++k) acc[k] = fold<T, OP>(acc[k], x[u][r][k]);
+        }
+      }
+      vstore<T, E, true>(out + v * E, acc);
+    }
+  }
+  // The run's last fewer-than-E elements, one per lane of its last workgroup.
+  const int64_t i = nvec * E + lane;
+  if (c == nblk - 1 && i < n) {
+    T acc = rows[0][i];
+    for (int r = 1; r < world; ++r) acc = fold<T, OP>(acc, rows[r][i]);
+    out[i] = acc;
   }
 }
 
-template <typename T>
-hipError_t launch_t(int op, const OpRuns& t, int blocks, const OpParams& p, hipStream_t stream) {
-  if (op == MDX_OP_MAX) {
-    hipLaunchKernelGGL((allreduce_op_kernel<T, MDX_OP_MAX>), dim3(blocks), dim3(kOpLanes), 0, stream, t, p);
-  } else if (op == MDX_OP_MIN) {
-    hipLaunchKernelGGL((allreduce_op_kernel<T, MDX_OP_MIN>), dim3(blocks), dim3(kOpLanes), 0, stream, t, p);
+template <typename T, int OP>
+hipError_t launch_op(int wmax, const OpRuns& t, int blocks, const OpParams& p, hipStream_t stream) {
+  const dim3 grid(blocks), block(kBlock);
+  if (wmax == 2) {
+    hipLaunchKernelGGL((allreduce_op_kernel<T, OP, 2>), grid, block, 0, stream, t, p);
+  } else if (wmax == 4) {
+    hipLaunchKernelGGL((allreduce_op_kernel<T, OP, 4>), grid, block, 0, stream, t, p);
+  } else if (wmax == 8) {
+    hipLaunchKernelGGL((allreduce_op_kernel<T, OP, 8>), grid, block, 0, stream, t, p);
   } else {
-    hipLaunchKernelGGL((allreduce_op_kernel<T, MDX_OP_PRODUCT>), dim3(blocks), dim3(kOpLanes), 0, stream, t, p);
+    hipLaunchKernelGGL((allreduce_op_kernel<T, OP, 16>), grid, block, 0, stream, t, p);
   }
   return hipGetLastError();
 }
 
+template <typename T>
+hipError_t launch_t(int op, int wmax, const OpRuns& t, int blocks, const OpParams& p, hipStream_t stream) {
+  if (op == MDX_OP_MAX) return launch_op<T, MDX_OP_MAX>(wmax, t, blocks, p, stream);
+  if (op == MDX_OP_MIN) return launch_op<T, MDX_OP_MIN>(wmax, t, blocks, p, stream);
+  return launch_op<T, MDX_OP_PRODUCT>(wmax, t, blocks, p, stream);
+}
+
 }  // namespace
 
-hipError_t launch_allreduce_op(int dtype, int op, const OpRuns& t, int blocks, const OpParams& p,
+hipError_t launch_allreduce_op(int dtype, int op, int wmax, const OpRuns& t, int blocks, const OpParams& p,
                                hipStream_t stream) {
-  if (dtype == MDX_BF16) return launch_t<bf16>(op, t, blocks, p, stream);
-  if (dtype == MDX_F16) return launch_t<f16>(op, t, blocks, p, stream);
-  return launch_t<float>(op, t, blocks, p, stream);
+  if (dtype == MDX_BF16) return launch_t<bf16>(op, wmax, t, blocks, p, stream);
+  if (dtype == MDX_F16) return launch_t<f16>(op, wmax, t, blocks, p, stream);
+  return launch_t<float>(op, wmax, t, blocks, p, stream);
 }
 
 }  // namespace mdx

@@ -759,14 +759,15 @@ int mdx_allreduce_op(const void* const* replicas, int world, int dtype, int op, 
   p.out = out;
   p.world = world;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  constexpr int64_t kElemsPerBlock = int64_t(kOpLanes) * kOpPerLane;
+  const int wmax = op_wmax(world);
+  const int64_t elems_per_block = op_elems_per_block(es, wmax);
   OpRuns t;
   memset(&t, 0, sizeof(t));
   int blocks = 0;
   auto flush = [&]() -> int {
     if (t.count == 0) return MDX_OK;
     t.first_block[t.count] = blocks;
-    const int r = status(launch_allreduce_op(dtype, op, t, blocks, p, st));
+    const int r = status(launch_allreduce_op(dtype, op, wmax, t, blocks, p, st));
     memset(&t, 0, sizeof(t));
     blocks = 0;
     return r;
@@ -782,7 +783,7 @@ int mdx_allreduce_op(const void* const* replicas, int world, int dtype, int op, 
       t.offset[t.count] = offsets[k] + a;
       t.numel[t.count] = n;
       t.first_block[t.count] = blocks;
-      blocks += int((n + kElemsPerBlock - 1) / kElemsPerBlock);
+      blocks += int((n + elems_per_block - 1) / elems_per_block);
       ++t.count;
     }
   }

@@ -355,9 +355,12 @@ constexpr int share_unroll(int wmax, int frag_in_bytes) {
 }
 
 // Non-SUM all-reduce (mdx_allreduce_op): runs of the replica layout in the
-// kernel arguments, kOpLanes x kOpPerLane elements per workgroup.
-constexpr int kOpLanes = 256;
-constexpr int kOpPerLane = 8;
+// kernel arguments, one-wave workgroups.  A lane takes op_unroll(WMAX)
+// 16-byte vectors of every replica -- about 128 bytes of loads in flight, as
+// the W-way sums keep -- where WMAX is the compile-time bound on the world.
+constexpr int op_wmax(int world) { return world <= 2 ? 2 : (world <= 4 ? 4 : (world <= 8 ? 8 : 16)); }
+constexpr int op_unroll(int wmax) { return wmax >= 8 ? 1 : 8 / wmax; }
+constexpr int64_t op_elems_per_block(int esize, int wmax) { return int64_t(kBlock) * op_unroll(wmax) * (16 / esize); }
 
 struct OpRuns {
   int64_t offset[kRunsPerLaunch];
@@ -372,7 +375,7 @@ struct OpParams {
   int32_t world;
 };
 
-hipError_t launch_allreduce_op(int dtype, int op, const OpRuns& t, int blocks, const OpParams& p,
+hipError_t launch_allreduce_op(int dtype, int op, int wmax, const OpRuns& t, int blocks, const OpParams& p,
                                hipStream_t stream);
 
 // Host-side dispatch into the instantiating translation units.
