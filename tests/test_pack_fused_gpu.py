@@ -317,11 +317,13 @@ def test_ddp_step_leaves_packed_row_and_averaged_bucket(rng, dtype, reduce_dtype
 @pytest.mark.parametrize("dtype,reduce_dtype", [(torch.float32, None), (torch.bfloat16, torch.float32)])
 @pytest.mark.parametrize("n_params,cap", [(5, 0.001), (70, 25.0)])
 @pytest.mark.parametrize("inf", [False, True])
-def test_ddp_without_bucket_average(rng, dtype, reduce_dtype, n_params, cap, inf):
+@pytest.mark.parametrize("launch", ["eager", "comm_stream", "graphs"])
+def test_ddp_without_bucket_average(rng, dtype, reduce_dtype, n_params, cap, inf, launch):
     """``keep_bucket_average=False``: the same step as the default -- gradients, found-inf and this
     rank's packed rows bit for bit, and against the oracle -- while every bucket keeps the sentinel
     it held before the step.  Small runs go through kernel-argument tables (one bucket per launch),
-    70 gradients in one bucket through a device plan; fp32 and widening bf16 -> fp32 buckets."""
+    70 gradients in one bucket through a device plan; fp32 and widening bf16 -> fp32 buckets; eager
+    launches, a dedicated communication stream, and graph replay."""
     from minidist import DDP, DistributedGradScaler, ResidentGroup
     from test_ddp_gpu import Flat, odt, stage_peers, synthetic_grads, dev_from, host_bits
 
@@ -337,7 +339,8 @@ def test_ddp_without_bucket_average(rng, dtype, reduce_dtype, n_params, cap, inf
         model = Flat(shapes, dtype)
         scaler = DistributedGradScaler(init_scale=S)
         ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, reduce_dtype=reduce_dtype,
-                  grad_scaler=scaler, keep_bucket_average=keep)
+                  grad_scaler=scaler, keep_bucket_average=keep, comm_stream=launch == "comm_stream",
+                  capture_graphs=launch == "graphs")
         stage_peers(ddp, grads, dts, rank, W)
         for b in ddp._buckets:
             b.buffer.fill_(-3.25)
