@@ -156,3 +156,35 @@ def test_comm_rejects_ops_a_resident_group_does_not_reduce():
     t = group.zeros(4, torch.float32)
     with pytest.raises(NotImplementedError, match="SUM, PRODUCT, MIN and MAX"):
         comm.all_reduce(t, op=dist.ReduceOp.AVG, group=group)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_allreduce_op_fuzz(seed):
+    """Seeded random cases: W in [1, 16], dtype, op, 1-60 runs of 0-20000 elements at any element
+    offset (gaps keep a sentinel), in place on a random replica or into a separate buffer."""
+    g = np.random.default_rng(5000 + seed)
+    W = int(g.integers(1, 17))
+    dt = DTYPES[int(g.integers(0, 3))]
+    op = list(OPS)[int(g.integers(0, 3))]
+    runs, off = [], int(g.integers(0, 9))
+    for _ in range(int(g.integers(1, 61))):
+        n = int(g.integers(0, 20001)) if g.random() < 0.8 else int(g.integers(0, 9))
+        runs.append((off, n))
+        off += n + int(g.integers(0, 9))
+    extent = off + 3
+    reps_host = _replicas(g, W, extent, dt, scale=1.5 if op == "product" else 1.0)
+    reps = [to_dev(h) for h in reps_host]
+    in_place = bool(g.integers(0, 2))
+    k = int(g.integers(0, W))
+    out = reps[k] if in_place else empty_dev(extent, dt)
+    print(f"op fuzz seed {seed}: W={W} {dt} {op} runs={len(runs)} in_place={in_place}", flush=True)
+    nat.allreduce_op([r.data_ptr() for r in reps], code(dt), OPS[op], [a for a, _ in runs], [n for _, n in runs],
+                     out.data_ptr(), stream())
+    got = to_host(out)
+    want = reps_host[k].copy() if in_place else np.full(extent, SENTINEL[dt], dtype=got.dtype)
+    for a, n in runs:
+        want[a : a + n] = o.allreduce_op([h[a : a + n] for h in reps_host], dt, op)
+    assert same_bits(got, want), first_mismatch(got, want)
+    for r in range(W):
+        if not (in_place and r == k):
+            assert same_bits(to_host(reps[r]), reps_host[r]), f"replica {r} was written"
