@@ -43,6 +43,33 @@ def test_library_exports_every_declared_symbol():
     assert lib.mdx_abi_version() == nat.ABI_VERSION
 
 
+_C_TO_CTYPES = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}
+
+
+def _ctype_of(decl: str):
+    """The ctypes type a C parameter (or return) declaration passes as: any pointer is an address."""
+    decl = " ".join(decl.replace("*", " * ").split())
+    if "*" in decl:
+        return ctypes.c_char_p if decl.startswith("const char *") and decl.count("*") == 1 else ctypes.c_void_p
+    base = decl.split()[0] if decl.split()[0] != "const" else decl.split()[1]
+    return _C_TO_CTYPES[base]
+
+
+def test_ctypes_signatures_follow_the_header_prototypes():
+    """Every argument the Python binding passes has the C type, position and count of the prototype
+    in include/mdx.h (a float passed where an int is declared, or a missing argument, would be read
+    as garbage by the library without any error)."""
+    protos = re.findall(r"^MDX_API\s+(int|const char\*)\s+(mdx_\w+)\(([^)]*)\);", HEADER.read_text(), flags=re.M)
+    assert {name for _, name, _ in protos} == set(nat.SIGNATURES)
+    for ret, name, params in protos:
+        params = " ".join(params.split())
+        args = [] if params in ("", "void") else [_ctype_of(p.rsplit(" ", 1)[0] if not p.endswith("*") else p)
+                                                   for p in (q.strip() for q in params.split(","))]
+        want_ret, want_args = nat.SIGNATURES[name]
+        assert _ctype_of(ret) is want_ret, f"{name}: returns {ret}"
+        assert list(want_args) == args, f"{name}: header {params!r}"
+
+
 def test_exported_symbols_are_only_the_abi():
     import subprocess
 
