@@ -68,6 +68,11 @@ def test_ctypes_signatures_follow_the_header_prototypes():
         want_ret, want_args = nat.SIGNATURES[name]
         assert _ctype_of(ret) is want_ret, f"{name}: returns {ret}"
         assert list(want_args) == args, f"{name}: header {params!r}"
+    # the reference-side bindings shown in INTEGRATION.md declare the same argument lists
+    shown = re.findall(r"_lib\.(mdx_\w+)\.argtypes = (\[[^\]]*\])", (ROOT / "INTEGRATION.md").read_text())
+    assert len(shown) >= 5
+    for name, listed in shown:
+        assert eval(listed, {"ctypes": ctypes}) == list(nat.SIGNATURES[name][1]), f"INTEGRATION.md: {name}"
 
 
 def test_exported_symbols_are_only_the_abi():
