@@ -669,12 +669,13 @@ def _attach_ipc_rows(units: list[_FSDPUnit], group, dtype: torch.dtype) -> list[
     segments: list[list[tuple[_FSDPUnit, int, int]]] = [[]]
     g_total = s_total = 0
     for u in units:
+        # a unit starts at an aligned offset; the buffer ends with the last unit's rows
         g_len = -(-u.padded_numel // _ARENA_ALIGN_ELEMS) * _ARENA_ALIGN_ELEMS
         s_len = -(-u.shard_numel // _ARENA_ALIGN_ELEMS) * _ARENA_ALIGN_ELEMS
-        if g_len * es > limit:
+        if u.padded_numel * es > limit:
             raise ValueError(f"FSDP over an IpcGroup: unit {u.name!r} needs {u.padded_numel * es} bytes of "
                              f"gradient rows, more than the group's segment_bytes ({limit})")
-        if segments[-1] and (g_total + g_len) * es > limit:
+        if segments[-1] and (g_total + u.padded_numel) * es > limit:
             segments.append([])
             g_total = s_total = 0
         segments[-1].append((u, g_total, s_total))

@@ -492,6 +492,53 @@ def test_ddp_segments_bound_each_allocation():
             _segments(buckets, align, esize, max(numels) * esize - 1)
 
 
+def test_fsdp_ipc_segments_bound_each_allocation():
+    """FSDP's units over an IpcGroup: in order, each at an aligned offset of its segment's two buffers,
+    no buffer past ``segment_bytes``, a new segment only when the next unit would not fit; a unit
+    exactly ``segment_bytes`` long fits alone; one larger is refused with the size it needs."""
+    from types import SimpleNamespace
+
+    from minidist.fsdp import _ARENA_ALIGN_ELEMS, _attach_ipc_rows
+
+    class _Rows:  # IpcGroup.zeros / row_addresses, on the CPU
+        def __init__(self, limit):
+            self.segment_bytes, self.sizes = limit, []
+
+        def zeros(self, numel, dtype):
+            self.sizes.append(numel * torch.empty((), dtype=dtype).element_size())
+            return torch.zeros(numel, dtype=dtype)
+
+        def row_addresses(self, row):
+            return [row.data_ptr(), row.data_ptr() + (1 << 40)]
+
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        W, dtype = int(rng.integers(1, 9)), [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        es = 4 if dtype == torch.float32 else 2
+        units = []
+        for k in range(int(rng.integers(1, 12))):
+            shard = int(rng.integers(0, 3000))
+            units.append(SimpleNamespace(name=f"u{k}", padded_numel=shard * W, shard_numel=shard))
+        need = max(u.padded_numel for u in units) * es
+        limit = need if trial % 5 == 0 else int(rng.integers(max(need, 1), 3 * need + 2))
+        group = _Rows(limit)
+        rows = _attach_ipc_rows(units, group, dtype)
+        assert len(group.sizes) == 2 * len(rows) and max(group.sizes) <= limit
+        segs = [[u for u in units if u.segment == s] for s in range(len(rows))]
+        assert [u for seg in segs for u in seg] == units
+        for s, seg in enumerate(segs):
+            assert seg[0].arena_offset == 0 and all(u.arena_offset % _ARENA_ALIGN_ELEMS == 0 for u in seg)
+            assert all(u._ipc.grads.numel() == u.padded_numel and u._ipc.shard.numel() == u.shard_numel for u in seg)
+            assert all(u._ipc.grad_ptrs[1] - u._ipc.grad_ptrs[0] == 1 << 40 for u in seg)
+            if s + 1 < len(segs):  # the next segment's first unit did not fit in this one
+                end = seg[-1].arena_offset + -(-seg[-1].padded_numel // _ARENA_ALIGN_ELEMS) * _ARENA_ALIGN_ELEMS
+                assert (end + segs[s + 1][0].padded_numel) * es > limit
+        if need:
+            with pytest.raises(ValueError, match=f"needs {need} bytes of gradient rows, more than the group's "
+                                                 f"segment_bytes \\({need - 1}\\)"):
+                _attach_ipc_rows(units, _Rows(need - 1), dtype)
+
+
 def test_ipc_group_checks_its_algorithm():
     with pytest.raises(ValueError, match="algorithm"):
         comm.IpcGroup(None, "cpu", algorithm="ring")

@@ -1,4 +1,7 @@
-"""Seeded random DDP pipelines over IPC-mapped rows: W processes on the one GPU (comm.IpcGroup).
+"""Seeded random DDP pipelines and FSDP steps over IPC-mapped rows: W processes on the one GPU
+(comm.IpcGroup).
+
+DDP:
 
 Each case draws W in [2, 4], one- or two-shot, the gradient dtype (fp32, bf16
 or fp16, the 16-bit ones optionally widened into fp32 buckets), 10-30
@@ -13,6 +16,16 @@ rank-ordered pipeline (``oracle.gradpath.ddp_pipeline``) over all ranks'
 gradients, and the found-inf decision against the oracle's.  The reference
 hands each bucket to ``dist.all_reduce`` (minidist/comm.py:223-234,
 ddp.py:243-274).
+
+FSDP: each case draws W in [2, 4], 1-5 units of random width (frozen biases,
+empty parameters) plus the root, the gather dtype, ``unit_batch``,
+``reshard_after_forward``, ``keep_low_precision_shard``, one or several
+symmetric buffers, and accumulation under ``no_sync`` with the final flush.
+Every rank runs its own backward on its own input; every unit's gathered
+parameters against the oracle's cast of the initial weights, and every rank's
+shard gradient against ``oracle.gradpath.fsdp_reduce_scatter_share`` over all
+ranks' captured full-size gradients (the reference's fsdp.py:172-241 over
+comm.all_gather_into_tensor / reduce_scatter_tensor).
 """
 
 from __future__ import annotations
@@ -28,8 +41,9 @@ import torch.multiprocessing as mp
 from torch import nn
 
 from conftest import first_mismatch, same_bits
-from minidist import DDP, DistributedGradScaler, IpcGroup
+from minidist import DDP, FSDP, DistributedGradScaler, IpcGroup, MixedPrecisionPolicy
 from oracle import gradpath as o
+from test_fuzz_gpu import _FuzzBlock, _FuzzNet
 
 pytestmark = pytest.mark.gpu
 SPECIALS = np.array([np.inf, -np.inf, np.nan, 1e-45, -1e-40, 0.0, -0.0], dtype=np.float32)
@@ -174,3 +188,102 @@ def test_random_ipc_pipeline_matches_oracle(tmp_path, seed):
         if c["use_scaler"]:
             scaler.update(want["found_inf"])
             assert all(float(res[r][f"scale_after_{step}"]) == scaler.scale for r in range(W)), case
+
+
+def _fsdp_case(seed: int) -> dict:
+    rng = np.random.default_rng(43000 + seed)
+    W = int(rng.integers(2, 5))
+    h = int(rng.integers(3, 41))
+    blocks = [(bool(rng.random() < 0.3), bool(rng.random() < 0.3)) for _ in range(int(rng.integers(1, 6)))]
+    param_dtype = DTYPES[int(rng.integers(0, 3))]
+    # every unit's full-size rows within the segment: blocks h*h + h (+3), the root the head's h + 1
+    largest = max([h * h + h + (0 if empty else 3) for _, empty in blocks] + [h + 1])
+    padded = -(-largest // W) * W
+    segment_bytes = [1 << 30, max(256, (padded * 4 + 255) // 256 * 256)][int(rng.integers(0, 2))]
+    return dict(W=W, h=h, blocks=blocks, param_dtype=param_dtype, unit_batch=int(rng.integers(1, 4)),
+                reshard=bool(rng.random() < 0.7), keep_low=bool(rng.random() < 0.3),
+                accumulate=bool(rng.random() < 0.4), segment_bytes=segment_bytes)
+
+
+def _fsdp_model(seed: int, c: dict, dev) -> nn.Module:
+    blocks = [_FuzzBlock(c["h"], 1000 * seed + k, frozen, empty) for k, (frozen, empty) in enumerate(c["blocks"])]
+    return _FuzzNet(blocks, c["h"]).to(dev)
+
+
+def _fsdp_worker(rank: int, world: int, store: str, out_dir: str, seed: int) -> None:
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        c = _fsdp_case(seed)
+        group = IpcGroup(dist.group.WORLD, dev, segment_bytes=c["segment_bytes"])
+        model = _fsdp_model(seed, c, dev)
+        init = {id(p): p.detach().float().reshape(-1).cpu().numpy().copy() for p in model.parameters()}
+        captured: dict[int, torch.Tensor] = {}
+        for p in model.parameters():
+            if p.requires_grad:
+                p.register_post_accumulate_grad_hook(lambda q: captured.__setitem__(id(q), q.grad.detach().clone()))
+        policy = MixedPrecisionPolicy(param_dtype=c["param_dtype"], reduce_dtype=torch.float32,
+                                      keep_low_precision_shard=c["keep_low"])
+        fsdp = FSDP(model, unit_types=(_FuzzBlock,), process_group=group, mixed_precision=policy,
+                    unit_batch=c["unit_batch"], reshard_after_forward=c["reshard"])
+        out = {"units": np.array(len(fsdp._units)), "segments": np.array(len({u.segment for u in fsdp._units}))}
+        with fsdp.summon_full_params():
+            for u, unit in enumerate(fsdp._units):
+                out[f"full_{u}"] = _host_bits(unit._full)
+        x = torch.randn(6, c["h"], generator=torch.Generator().manual_seed(100 * seed + rank)).to(dev)
+        if c["accumulate"]:
+            with fsdp.no_sync():
+                for half in x.chunk(2):
+                    (fsdp(half) / 2).backward()
+        else:
+            fsdp(x).backward()
+        fsdp.finish_gradient_sync()
+        torch.cuda.synchronize()
+        for u, unit in enumerate(fsdp._units):
+            out[f"numels_{u}"] = np.array(unit.numels, dtype=np.int64)
+            out[f"init_{u}"] = (np.concatenate([init[id(p)] for p in unit.params]) if unit.params
+                                else np.zeros(0, np.float32))
+            for k, p in enumerate(unit.params):
+                if id(p) in captured:
+                    out[f"local_{u}_{k}"] = _host_bits(captured[id(p)])
+            out[f"shard_grad_{u}"] = _host_bits(unit.flat_shard.grad)
+            out[f"sharded_{u}"] = np.array(not unit.is_unsharded and all(p.grad is None for p in unit.params))
+        group.release()
+        np.savez(os.path.join(out_dir, f"fsdp_fuzz_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_ipc_fsdp_matches_oracle(tmp_path, seed):
+    c = _fsdp_case(seed)
+    W = c["W"]
+    pdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(c["param_dtype"], o.F32)
+    case = (f"ipc fsdp fuzz seed {seed}: W={W} h={c['h']} blocks={len(c['blocks'])} {c['param_dtype']} "
+            f"unit_batch={c['unit_batch']} reshard={c['reshard']} keep_low={c['keep_low']} "
+            f"accumulate={c['accumulate']} segment={c['segment_bytes']}")
+    print(case, flush=True)
+    mp.spawn(_fsdp_worker, args=(W, str(tmp_path / "store"), str(tmp_path), seed), nprocs=W, join=True)
+    res = []
+    for r in range(W):
+        with np.load(tmp_path / f"fsdp_fuzz_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    n_units = int(res[0]["units"])
+    assert n_units == len(c["blocks"]) + 1, case
+    print(f"  {n_units} units in {int(res[0]['segments'])} pair(s) of symmetric buffers", flush=True)
+    for u in range(n_units):
+        numels = [int(n) for n in res[0][f"numels_{u}"]]
+        _, _, P = o.fsdp_layout(numels, W)
+        flat = np.zeros(P, np.float32)
+        flat[: sum(numels)] = res[0][f"init_{u}"]
+        gathered = o.fsdp_gather_cast(flat, pdt)
+        grads = [[res[r][f"local_{u}_{k}"] if f"local_{u}_{k}" in res[r] else o.zeros(n, pdt)
+                  for k, n in enumerate(numels)] for r in range(W)]
+        for rank in range(W):
+            assert bool(res[rank][f"sharded_{u}"]), f"{case}: unit {u} rank {rank} still gathered after backward"
+            assert same_bits(res[rank][f"full_{u}"], gathered), f"{case}: unit {u} rank {rank} all-gather"
+            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, pdt if c["keep_low"] else o.F32)
+            got = res[rank][f"shard_grad_{u}"]
+            assert same_bits(got, want), f"{case}: unit {u} rank {rank} shard grad: " + first_mismatch(got, want)
