@@ -139,6 +139,95 @@ def _pipeline_case(seed: int, rng, empty_rate: float = 0.0) -> None:
         assert found == want["found_inf"], case
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_pipeline_launch_modes_over_steps(seed):
+    """Seeded random pipelines run for four steps in one launch mode -- eager, on DDP's
+    communication stream, or replayed from captured HIP graphs -- with or without the bucket
+    average kept, and each step hands over its gradients one of three ways: new tensors (at odd
+    offsets of larger buffers), the same tensors overwritten in place (a graph then replays), or
+    new tensors with some parameters left without a gradient.  An overflow backs the scale off
+    for the next step, as the reference's scaler does.  Every step's gradients, buckets and
+    found-inf decision against the oracle."""
+    rng = np.random.default_rng(23000 + seed)
+    dtype = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    widening = dtype != torch.float32 and bool(rng.random() < 0.5)
+    gdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(dtype, o.F32)
+    W = int(rng.integers(2, 17))
+    rank = int(rng.integers(0, W))
+    n_params = int(rng.integers(10, 31))
+    shapes = [(0,) if rng.random() < 0.1 else (int(rng.integers(1, 3000)),) for _ in range(n_params)]
+    numels = [int(np.prod(s)) for s in shapes]
+    total_mb = sum(numels) * (4 if dtype == torch.float32 else 2) / 2**20
+    cap = float(rng.choice([1e-6, total_mb / 5, total_mb / 2, 1e6]))
+    mode = ["eager", "comm_stream", "graphs"][int(rng.integers(0, 3))]
+    keep = bool(rng.random() < 0.5)
+    use_scaler = bool(rng.random() < 0.7)
+    scale = 2.0 ** int(rng.integers(0, 14 if dtype != torch.float16 else 10)) if use_scaler else 1.0
+    case = (f"seed {seed}: {dtype} widening={widening} W={W} rank={rank} cap={cap:.3g} {mode} "
+            f"keep_bucket_average={keep} scale={scale:g}")
+    print(case, flush=True)
+
+    model = Flat(shapes, dtype)
+    scaler = DistributedGradScaler(init_scale=scale) if use_scaler else None
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, grad_scaler=scaler,
+              reduce_dtype=torch.float32 if widening else None, comm_stream=mode == "comm_stream",
+              capture_graphs=mode == "graphs", keep_bucket_average=keep)
+    params = list(model.parameters())
+    index = {id(p): i for i, p in enumerate(params)}
+
+    class _Opt:
+        param_groups = [{"params": params}]
+
+    state = o.ScalerState(scale=scale)
+    for step in range(4):
+        how = "new" if step == 0 else ["new", "in_place", "missing"][int(rng.integers(0, 3))]
+        grads = []
+        for r in range(W):
+            row = []
+            for n in numels:
+                g = (rng.standard_normal(n) * 1e-3 * scale).astype(np.float32)
+                if n and rng.random() < 0.03:
+                    g[int(rng.integers(0, n))] = SPECIALS[int(rng.integers(0, len(SPECIALS)))]
+                row.append(o.from_f32(g, gdt))
+            grads.append(row)
+        if how == "missing":
+            for i in rng.integers(0, n_params, int(rng.integers(1, 4))):
+                grads[rank][int(i)] = None
+        for b, bucket in enumerate(ddp._buckets):
+            idxs = [index[id(p)] for p in bucket.params]
+            rows = ddp.bucket_replicas(b)
+            wire_dtype, prescaled = ddp.bucket_wire_format(b)
+            wdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(wire_dtype, o.F32)
+            for r in range(W):
+                if r != rank:
+                    packed = o.pack([grads[r][i] for i in idxs], [gdt] * len(idxs), [numels[i] for i in idxs],
+                                    wdt, 1.0 / W if prescaled else 1.0)
+                    rows[r].copy_(dev_from(packed))
+        for p, g in zip(params, grads[rank], strict=True):
+            if g is None:
+                p.grad = None
+            elif how == "in_place" and p.grad is not None:
+                p.grad.copy_(dev_from(g).view(p.shape))
+            else:
+                p.grad = dev_view(g, p.shape, int(rng.integers(0, 9)))
+        ddp.finish_gradient_sync()
+        found = scaler.unscale_(_Opt()) if scaler is not None else None
+        want = o.ddp_pipeline(grads, [gdt] * n_params, numels, cap, rank, 1.0 / state.scale if use_scaler else None,
+                              bucket_dtype=o.F32 if widening else None)
+        where = f"{case} step {step} ({how})"
+        for i, p in enumerate(params):
+            got = host_bits(p.grad)
+            assert same_bits(got, want["grads"][i]), f"{where} param {i}: {first_mismatch(got, want['grads'][i])}"
+        if keep:
+            for b, bucket in enumerate(ddp._buckets):
+                assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"{where} bucket {b}"
+        if scaler is not None:
+            assert found == want["found_inf"], where
+            scaler.update()
+            state.update(want["found_inf"])
+            assert scaler.scale == state.scale, where
+
+
 class _FuzzBlock(nn.Module):
     """A random FSDP unit: a square Linear (its bias frozen in some), and an extra parameter that
     is empty in some."""
