@@ -44,6 +44,10 @@ whose replicas fit in host memory):
           trainer's --fsdp-param-dtype fp16; fp16 gradients)
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 10] [--no-cpu-baseline] [--workload cfg1]
+
+Three probes print their own JSON line instead: ``--calibrate-copy`` (the known-size copy that
+scales the PMC traffic counters), ``--dispatch-floor`` (cfg3 issued one unit at a time) and
+``--op-rates`` (the MAX / MIN / PRODUCT all-reduce beside the SUM kernel).
 """
 
 from __future__ import annotations
@@ -292,6 +296,49 @@ def dispatch_floor() -> int:
         "cfg3_step_bar_ms": round(n_units * bar_unit_us * 1e-3, 4),
         "sweep": sweep,
     }), flush=True)
+    return 0
+
+
+def op_rates() -> int:
+    """The non-SUM all-reduce (mdx_allreduce_op: MAX, MIN, PRODUCT) beside the SUM kernel
+    (mdx_allreduce_sum) on the same fp32 rows: W = 8 over 2^26 elements and W = 4 over 2^27, one
+    run each, (W+1)*4 bytes per element moved.  HIP events around each dispatch on the stream it
+    is launched on, median of 20 after 3 untimed."""
+    import torch
+
+    from minidist import _native
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    s_ptr = stream.cuda_stream
+    out = {"probe": "mdx_allreduce_op (MAX, MIN, PRODUCT) beside mdx_allreduce_sum, fp32, one run", "cases": []}
+    for W, N in ((8, 1 << 26), (4, 1 << 27)):
+        rows = torch.randn(W, N, device=dev)
+        res = torch.empty(N, device=dev)
+        ptrs = [rows[r].data_ptr() for r in range(W)]
+        launches = {
+            "sum": lambda: _native.allreduce_sum(ptrs, _native.MDX_F32, [0], [N], res.data_ptr(), s_ptr),
+            **{name: (lambda op=op: _native.allreduce_op(ptrs, _native.MDX_F32, op, [0], [N], res.data_ptr(), s_ptr))
+               for name, op in (("max", _native.MDX_OP_MAX), ("min", _native.MDX_OP_MIN),
+                                ("product", _native.MDX_OP_PRODUCT))},
+        }
+        for name, launch in launches.items():
+            for _ in range(3):
+                launch()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+            for e0, e1 in ev:
+                e0.record(stream)
+                launch()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us = sorted(e0.elapsed_time(e1) for e0, e1 in ev)[10] * 1e3
+            out["cases"].append({"W": W, "numel": N, "op": name, "us": round(us, 1),
+                                 "gbs": round((W + 1) * 4 * N / (us * 1e-6) / 1e9, 1)})
+            print(f"[bench] op rates: {out['cases'][-1]}", file=sys.stderr, flush=True)
+        del rows, res
+        torch.cuda.empty_cache()
+    print(json.dumps(out), flush=True)
     return 0
 
 
@@ -1055,11 +1102,17 @@ def main() -> int:
         help="only measure the per-unit floor of cfg3 issued in the reference's order (two stream-ordered "
              "dispatches per unit; see dispatch_floor)",
     )
+    ap.add_argument(
+        "--op-rates", action="store_true",
+        help="only time the non-SUM all-reduce kernel (MAX, MIN, PRODUCT) beside the SUM kernel (see op_rates)",
+    )
     args = ap.parse_args()
     if args.calibrate_copy:
         return calibrate_copy()
     if args.dispatch_floor:
         return dispatch_floor()
+    if args.op_rates:
+        return op_rates()
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU: this build emulates the W={W_CFG1} data-parallel replicas on a single "
