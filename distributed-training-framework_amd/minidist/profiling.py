@@ -89,7 +89,10 @@ def is_collective(name: str) -> bool:
 
 
 def classify(name: str) -> str | None:
-    """The collective kind of an event or kernel name (None when none applies)."""
+    """The collective kind of an event or kernel name; None for a name that is not a collective's
+    (torch's own ``direct_copy_kernel_cuda`` is no bucket copy) or matches no kind."""
+    if not is_collective(name):
+        return None
     low = name.lower()
     for kind, needles in _KINDS:
         if any(n in low for n in needles):

@@ -10,7 +10,9 @@ the gfx950 path's own kernel names as rocprofv3 prints them.
 from __future__ import annotations
 
 import csv
+import gzip
 import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -34,6 +36,7 @@ def test_kernel_classification():
     assert P.classify("ncclDevKernel_ReduceScatter_Sum_f32") == "reduce_scatter"
     assert P.classify("nccl:all_gather") == "all_gather"
     assert not P.is_collective(GEMM) and not P.is_collective(TORCH_COPY)
+    assert P.classify(TORCH_COPY) is None and P.classify(GEMM) is None
 
 
 def test_mangled_kernel_names_and_bookkeeping_kernels():
@@ -158,6 +161,41 @@ def test_rocprof_kernel_trace(tmp_path):
     assert r.per_kind_s == pytest.approx({"bucket_copy": 200e-9, "all_reduce": 1000e-9})
     late = P.analyze_kernel_trace(path, since_ns=2000)
     assert late.compute_s == 0.0 and late.exposed_comm_s == pytest.approx(600e-9)
+
+
+def test_real_rocprof_trace_of_an_overlapped_step(tmp_path):
+    """One step of the cfg1 path inside a real forward + backward on an MI355X, DDP's bucket runs on
+    their own stream, as rocprofv3 recorded it (``tests/golden/rocprof_cfg1_overlap_step.csv.gz``,
+    cut from the raw trace by ``tests/golden/make_rocprof_fixture.py``): the names rocprofv3 gave
+    this path's kernels are its collectives and no other kernel is (torch's own copy kernels
+    included); the report's busy, overlapped and exposed times equal a nanosecond grid over the
+    same rows."""
+    path = tmp_path / "run_kernel_trace.csv"
+    path.write_bytes(gzip.decompress((Path(__file__).parent / "golden" / "rocprof_cfg1_overlap_step.csv.gz").read_bytes()))
+    with open(path, newline="") as fh:
+        rows = list(csv.DictReader(fh))
+    r = P.analyze_kernel_trace(path)
+    ours = [row for row in rows if "mdx::" in row["Kernel_Name"]]
+    gemms = [row for row in rows if row["Kernel_Name"].startswith("Cijk_")]
+    assert len(rows) > 500 and ours and gemms
+    assert r.num_comm_events == len(ours) and r.num_compute_events == len(rows) - len(ours)
+    assert {P.classify(row["Kernel_Name"]) for row in ours} == {"all_reduce"}
+    assert any("copy_kernel" in row["Kernel_Name"] for row in rows if row not in ours)  # torch's, not a bucket copy
+    assert {row["Stream_Id"] for row in ours}.isdisjoint({row["Stream_Id"] for row in gemms})  # DDP's own stream
+
+    end = max(int(row["End_Timestamp"]) for row in rows)
+    comm, compute = np.zeros(end, dtype=bool), np.zeros(end, dtype=bool)
+    for row in rows:
+        cover = comm if "mdx::" in row["Kernel_Name"] else compute
+        cover[int(row["Start_Timestamp"]) : int(row["End_Timestamp"])] = True
+    ns = 1e-9
+    assert r.comm_s == pytest.approx(comm.sum() * ns, abs=1e-12)
+    assert r.compute_s == pytest.approx(compute.sum() * ns, abs=1e-12)
+    assert r.overlapped_s == pytest.approx((comm & compute).sum() * ns, abs=1e-12)
+    assert r.exposed_comm_s == pytest.approx((comm & ~compute).sum() * ns, abs=1e-12)
+    assert r.per_kind_s == pytest.approx({"all_reduce": comm.sum() * ns}, abs=1e-12)
+    assert r.wall_s == pytest.approx(end * ns, abs=1e-12)
+    assert 0 < r.overlapped_s < r.comm_s  # the stream ran part of the path under backward's kernels
 
 
 def test_package_exports_the_reference_names():
