@@ -563,13 +563,33 @@ def test_units_skipped_in_forward(order, n_blocks, unit_batch):
     _train_out_of_order(order, n_blocks, unit_batch)
 
 
-def _train_out_of_order(order, n_blocks, unit_batch):
-    W, rank, steps, lr = 2, 1, 3, 0.2
-    x = torch.randn(8, 4, generator=torch.Generator().manual_seed(23)).to(DEV)
-    ref = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
-    model = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
+@pytest.mark.parametrize("seed", range(12))
+def test_random_unit_orders_track_full_batch(seed):
+    """Seeded random cases of the two tests above: 2-6 registered blocks run as a random
+    permutation of a random subset, W in [2, 4], any rank, ``unit_batch`` 1-4, side streams or
+    not, ``reshard_after_forward`` or not; 3 SGD steps, every unit sharded after each backward
+    and the final shards on this rank's slice of the full-batch model's weights."""
+    rng = np.random.default_rng(31000 + seed)
+    n_blocks = int(rng.integers(2, 7))
+    order = [int(i) for i in rng.permutation(n_blocks)[: int(rng.integers(1, n_blocks + 1))]]
+    W = int(rng.integers(2, 5))
+    rank = int(rng.integers(0, W))
+    unit_batch = int(rng.integers(1, 5))
+    comm_streams, reshard = bool(rng.random() < 0.3), bool(rng.random() < 0.7)
+    print(f"seed {seed}: {n_blocks} blocks run as {order}, W={W} rank={rank} unit_batch={unit_batch} "
+          f"comm_streams={comm_streams} reshard_after_forward={reshard}", flush=True)
+    _train_out_of_order(order, n_blocks, unit_batch, W=W, rank=rank, comm_streams=comm_streams, reshard=reshard,
+                        seed=100 + seed)
+
+
+def _train_out_of_order(order, n_blocks, unit_batch, W=2, rank=1, comm_streams=False, reshard=True, seed=17):
+    steps, lr = 3, 0.2
+    x = torch.randn(12, 4, generator=torch.Generator().manual_seed(23)).to(DEV)  # W equal chunks for W = 2, 3, 4
+    ref = _OutOfOrderNet(order, seed=seed, n_blocks=n_blocks).to(DEV)
+    model = _OutOfOrderNet(order, seed=seed, n_blocks=n_blocks).to(DEV)
     names_by_id = {id(p): n for n, p in model.named_parameters()}
-    fsdp = FSDP(model, unit_types=(_OrderBlock,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch)
+    fsdp = FSDP(model, unit_types=(_OrderBlock,), process_group=ResidentGroup(W, rank, DEV), unit_batch=unit_batch,
+                comm_streams=comm_streams, reshard_after_forward=reshard)
     opt = torch.optim.SGD(fsdp.parameters(), lr=lr)
     opt_ref = torch.optim.SGD(ref.parameters(), lr=lr)
     for _ in range(steps):
@@ -578,15 +598,21 @@ def _train_out_of_order(order, n_blocks, unit_batch):
             flat = torch.cat([cur[names_by_id[id(p)]].reshape(-1) for p in unit.params])
             flat = torch.cat([flat, flat.new_zeros(unit.padded_numel - unit.total_numel)])
             S, shards = unit.shard_numel, unit.peer_param_shards()
-            shards[1 - rank].copy_(flat[(1 - rank) * S : (2 - rank) * S])
-        peer = _OutOfOrderNet(order, n_blocks=n_blocks).to(DEV)
-        with torch.no_grad():
-            for n, p in peer.named_parameters():
-                p.copy_(cur[n])
-        peer(x.chunk(W)[1 - rank]).backward()
-        replica = [{n: p.grad.detach().clone() if p.grad is not None else torch.zeros_like(p)
-                    for n, p in peer.named_parameters()}, {}]
-        _stage(fsdp, names_by_id, replica if rank == 1 else replica[::-1], rank, W)
+            for r in range(W):
+                if r != rank:
+                    shards[r].copy_(flat[r * S : (r + 1) * S])
+        replica = [{} for _ in range(W)]
+        for r in range(W):  # the peers' backward on their own chunks, from the same weights
+            if r == rank:
+                continue
+            peer = _OutOfOrderNet(order, seed=seed, n_blocks=n_blocks).to(DEV)
+            with torch.no_grad():
+                for n, p in peer.named_parameters():
+                    p.copy_(cur[n])
+            peer(x.chunk(W)[r]).backward()
+            replica[r] = {n: p.grad.detach().clone() if p.grad is not None else torch.zeros_like(p)
+                          for n, p in peer.named_parameters()}
+        _stage(fsdp, names_by_id, replica, rank, W)
         fsdp(x.chunk(W)[rank]).backward()
         assert not any(u.is_unsharded for u in fsdp._units), "a unit is still gathered after backward"
         opt.step()
