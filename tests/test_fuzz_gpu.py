@@ -228,6 +228,127 @@ def test_random_pipeline_launch_modes_over_steps(seed):
             assert scaler.scale == state.scale, where
 
 
+class _HookNet(nn.Module):
+    """Linear layers of random widths, used by forward in a random order; optionally one layer
+    used twice (its weight and bias are each one parameter fed from two places), one frozen
+    layer, and one parameter that forward never touches (its gradient stays None)."""
+
+    def __init__(self, rng, dtype):
+        super().__init__()
+        n = int(rng.integers(2, 7))
+        self.h = int(rng.integers(4, 33))
+        self.layers = nn.ModuleList([nn.Linear(self.h, self.h) for _ in range(n)])
+        self.unused = nn.Parameter(torch.zeros(int(rng.integers(1, 50))))
+        self.order = [int(i) for i in rng.permutation(n)]
+        if rng.random() < 0.4:
+            self.order.append(self.order[0])  # one layer twice
+        self.frozen = int(rng.integers(0, n)) if rng.random() < 0.3 else None
+        g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+        with torch.no_grad():
+            for p in self.parameters():
+                p.copy_(torch.randn(p.shape, generator=g) * 0.3)
+        if self.frozen is not None:
+            self.layers[self.frozen].requires_grad_(False)
+        self.to(device=DEV, dtype=dtype)
+
+    def forward(self, x):
+        for i in self.order:
+            x = torch.tanh(self.layers[i](x))
+        return x.float().square().mean()
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_backward_pipelines(seed):
+    """Seeded random models through a real backward, DDP's bucket runs launched from the autograd
+    hooks as buckets fill (or all at the end without ``overlap_with_backward``), eagerly, on
+    ``comm_stream`` or from captured graphs, over two or three steps with ``zero_grad`` to None,
+    to zero, or not at all (backward then accumulates onto the previous step's averages).  Every
+    step's gradients -- unused parameter included -- and found-inf decision against the oracle
+    over this rank's captured local gradients and the staged peers'."""
+    rng = np.random.default_rng(27000 + seed)
+    dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+    widening = dtype == torch.bfloat16 and bool(rng.random() < 0.5)
+    gdt = o.BF16 if dtype == torch.bfloat16 else o.F32
+    model = _HookNet(rng, dtype)
+    W = int(rng.integers(2, 9))
+    rank = int(rng.integers(0, W))
+    params = [p for p in model.parameters() if p.requires_grad]
+    numels = [p.numel() for p in params]
+    total_mb = sum(numels) * (4 if dtype == torch.float32 else 2) / 2**20
+    cap = float(rng.choice([1e-6, total_mb / 4, total_mb / 2, 1e6]))
+    overlap = bool(rng.random() < 0.75)
+    mode = ["eager", "comm_stream", "graphs"][int(rng.integers(0, 3))]
+    use_scaler = bool(rng.random() < 0.6)
+    scale = 2.0 ** int(rng.integers(0, 12)) if use_scaler else 1.0
+    zero = ["none", "zero", "keep"][int(rng.integers(0, 3))]
+    steps = int(rng.integers(2, 4))
+    case = (f"seed {seed}: {dtype} widening={widening} W={W} rank={rank} layers={len(model.layers)} "
+            f"order={model.order} frozen={model.frozen} cap={cap:.3g} overlap={overlap} {mode} "
+            f"scale={scale:g} zero_grad={zero} steps={steps}")
+    print(case, flush=True)
+
+    captured: dict[int, torch.Tensor] = {}
+    for p in params:  # registered before DDP's hooks, so they see the local gradient
+        p.register_post_accumulate_grad_hook(lambda q: captured.__setitem__(id(q), q.grad.detach().clone()))
+    scaler = DistributedGradScaler(init_scale=scale) if use_scaler else None
+    ddp = DDP(model, process_group=ResidentGroup(W, rank, DEV), bucket_cap_mb=cap, overlap_with_backward=overlap,
+              grad_scaler=scaler, reduce_dtype=torch.float32 if widening else None,
+              comm_stream=mode == "comm_stream", capture_graphs=mode == "graphs")
+    index = {id(p): i for i, p in enumerate(params)}
+
+    class _Opt:
+        param_groups = [{"params": params}]
+
+    state = o.ScalerState(scale=scale)
+    for step in range(steps):
+        peers = []
+        for _ in range(W):
+            row = []
+            for n in numels:
+                g = (rng.standard_normal(n) * 1e-2 * state.scale).astype(np.float32)
+                if rng.random() < 0.02:
+                    g[int(rng.integers(0, n))] = SPECIALS[int(rng.integers(0, 3))]  # +-inf or NaN
+                row.append(o.from_f32(g, gdt))
+            peers.append(row)
+        for b, bucket in enumerate(ddp._buckets):
+            idxs = [index[id(p)] for p in bucket.params]
+            rows = ddp.bucket_replicas(b)
+            wire_dtype, prescaled = ddp.bucket_wire_format(b)
+            wdt = {torch.bfloat16: o.BF16}.get(wire_dtype, o.F32)
+            for r in range(W):
+                if r != rank:
+                    packed = o.pack([peers[r][i] for i in idxs], [gdt] * len(idxs), [numels[i] for i in idxs], wdt,
+                                    1.0 / W if prescaled else 1.0)
+                    rows[r].copy_(dev_from(packed))
+        captured.clear()
+        # what a parameter backward does not reach contributes: its gradient as it stands (None, the
+        # zeros zero_grad left, or the previous step's average)
+        before = [None if p.grad is None else host_bits(p.grad) for p in params]
+        x = torch.randn(5, model.h, generator=torch.Generator().manual_seed(1000 * seed + step)).to(DEV, dtype)
+        loss = ddp(x) * state.scale
+        loss.backward()
+        found = scaler.unscale_(_Opt()) if scaler is not None else None
+        own = [host_bits(captured[id(p)]) if id(p) in captured else before[i] for i, p in enumerate(params)]
+        assert id(model.unused) not in captured
+        grads = [own if r == rank else peers[r] for r in range(W)]
+        want = o.ddp_pipeline(grads, [gdt] * len(params), numels, cap, rank, 1.0 / state.scale if use_scaler else None,
+                              bucket_dtype=o.F32 if widening else None)
+        where = f"{case} step {step}"
+        for i, p in enumerate(params):
+            got = host_bits(p.grad)
+            assert same_bits(got, want["grads"][i]), f"{where} param {i}: {first_mismatch(got, want['grads'][i])}"
+        if scaler is not None:
+            assert found == want["found_inf"], where
+            scaler.update()
+            state.update(want["found_inf"])
+        if zero == "none":
+            for p in params:
+                p.grad = None
+        elif zero == "zero":
+            for p in params:
+                p.grad.zero_()
+
+
 class _FuzzBlock(nn.Module):
     """A random FSDP unit: a square Linear (its bias frozen in some), and an extra parameter that
     is empty in some."""
