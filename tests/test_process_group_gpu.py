@@ -321,3 +321,100 @@ def test_fsdp_matches_ddp_two_processes(tmp_path):
         if tag == "fsdp_keep":
             assert all(bool(res[r]["fsdp_keep_blocks_gathered"]) for r in range(W))
 
+
+
+def _random_ddp_case(seed: int) -> dict:
+    rng = np.random.default_rng(37000 + seed)
+    dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+    return dict(dtype=dtype, model_seed=int(rng.integers(0, 1 << 30)), cap=float(rng.choice([1e-6, 1e-3, 4e-3, 1e6])),
+                overlap=bool(rng.random() < 0.75), comm_stream=bool(rng.random() < 0.4),
+                use_scaler=bool(rng.random() < 0.7), scale=2.0 ** int(rng.integers(0, 12)),
+                zero=["none", "zero", "keep"][int(rng.integers(0, 3))], steps=int(rng.integers(2, 4)),
+                inject=[bool(rng.random() < 0.3) for _ in range(4)])
+
+
+def _random_ddp_worker(rank: int, seed: int, store: str, out_dir: str) -> None:
+    """One rank of a random DDP case over the default gloo group (see test_random_ddp_two_processes)."""
+    from test_fuzz_gpu import _HookNet
+
+    torch.cuda.set_device(0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=W,
+                            timeout=timedelta(seconds=60))
+    try:
+        c = _random_ddp_case(seed)
+        dev = torch.device("cuda", 0)
+        model = _HookNet(np.random.default_rng(c["model_seed"]), c["dtype"])  # one architecture on every rank
+        params = [p for p in model.parameters() if p.requires_grad]
+        local: dict[int, torch.Tensor] = {}
+        for p in params:
+            p.register_post_accumulate_grad_hook(lambda q: local.__setitem__(id(q), q.grad.detach().clone()))
+        scaler = DistributedGradScaler(init_scale=c["scale"]) if c["use_scaler"] else None
+        ddp = DDP(model, bucket_cap_mb=c["cap"], overlap_with_backward=c["overlap"], grad_scaler=scaler,
+                  reduce_dtype=torch.float32 if c["dtype"] != torch.float32 else None, comm_stream=c["comm_stream"])
+
+        class _Opt:
+            param_groups = [{"params": params}]
+
+        out = {"h": np.array(model.h), "buckets": np.array(len(ddp._buckets))}
+        for step in range(c["steps"]):
+            local.clear()
+            before = [None if p.grad is None else _bits(p.grad) for p in params]
+            x = torch.randn(5, model.h, generator=torch.Generator().manual_seed(100 * step + rank)).to(dev, c["dtype"])
+            loss = ddp(x) * (scaler.scale if scaler is not None else 1.0)
+            if c["inject"][step] and rank == 1:
+                loss = loss * float("inf")  # this rank's backward overflows
+            loss.backward()
+            if scaler is not None:
+                out[f"found_{step}"] = np.array(scaler.unscale_(_Opt()))
+                out[f"scale_{step}"] = np.array(scaler.scale)
+                scaler.update()
+            torch.cuda.synchronize()
+            for i, p in enumerate(params):
+                own = _bits(local[id(p)]) if id(p) in local else before[i]
+                out[f"local_{step}_{i}"] = own if own is not None else np.zeros(0, np.float32)
+                out[f"has_{step}_{i}"] = np.array(own is not None)
+                out[f"final_{step}_{i}"] = _bits(p.grad)
+            if c["zero"] == "none":
+                for p in params:
+                    p.grad = None
+            elif c["zero"] == "zero":
+                for p in params:
+                    p.grad.zero_()
+        np.savez(os.path.join(out_dir, f"rand_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_ddp_two_processes(tmp_path, seed):
+    """Seeded random DDP cases over a real two-process gloo group: random layer widths run in a random
+    order (a layer used twice, a frozen layer, a parameter forward never touches), fp32 or bf16
+    gradients into fp32 buckets, bucket caps from one bucket per parameter to one, launched from the
+    hooks or at the end, on ``comm_stream`` or not, the fused scaler with an overflow on one rank in
+    some steps, ``zero_grad`` to None, to zero or not at all.  Each rank's gradients and found-inf
+    decision every step against the oracle over both ranks' local gradients (W = 2: the backend's
+    a + b is order-free, so bit for bit)."""
+    c = _random_ddp_case(seed)
+    print(f"seed {seed}: {c}", flush=True)
+    mp.spawn(_random_ddp_worker, args=(seed, str(tmp_path / "store"), str(tmp_path)), nprocs=W, join=True)
+    res = []
+    for r in range(W):
+        with np.load(tmp_path / f"rand_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    n = sum(1 for k in res[0] if k.startswith("final_0_"))
+    gdt = o.BF16 if c["dtype"] == torch.bfloat16 else o.F32
+    for step in range(c["steps"]):
+        grads = [[res[r][f"local_{step}_{i}"] if bool(res[r][f"has_{step}_{i}"]) else None for i in range(n)]
+                 for r in range(W)]
+        numels = [res[0][f"final_{step}_{i}"].size for i in range(n)]
+        for rank in range(W):
+            inv = 1.0 / float(res[rank][f"scale_{step}"]) if c["use_scaler"] else None
+            want = o.ddp_pipeline(grads, [gdt] * n, numels, c["cap"], rank, inv,
+                                  bucket_dtype=o.F32 if gdt == o.BF16 else None)
+            where = f"seed {seed} step {step} rank {rank}"
+            if c["use_scaler"]:
+                assert bool(res[rank][f"found_{step}"]) == want["found_inf"], where
+                assert want["found_inf"] or not c["inject"][step], where  # rank 1's overflow reaches both
+            for i in range(n):
+                got = res[rank][f"final_{step}_{i}"]
+                assert same_bits(got, want["grads"][i]), f"{where} param {i}: " + first_mismatch(got, want["grads"][i])
