@@ -418,3 +418,94 @@ def test_random_ddp_two_processes(tmp_path, seed):
             for i in range(n):
                 got = res[rank][f"final_{step}_{i}"]
                 assert same_bits(got, want["grads"][i]), f"{where} param {i}: " + first_mismatch(got, want["grads"][i])
+
+
+def _random_fsdp_case(seed: int) -> dict:
+    rng = np.random.default_rng(39000 + seed)
+    h = int(rng.integers(3, 41))
+    blocks = [(bool(rng.random() < 0.3), bool(rng.random() < 0.3)) for _ in range(int(rng.integers(1, 6)))]
+    return dict(h=h, blocks=blocks, param_dtype=[torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))],
+                unit_batch=int(rng.integers(1, 4)), reshard=bool(rng.random() < 0.7), keep_low=bool(rng.random() < 0.3),
+                accumulate=bool(rng.random() < 0.4), comm_streams=bool(rng.random() < 0.3))
+
+
+def _random_fsdp_worker(rank: int, seed: int, store: str, out_dir: str) -> None:
+    """One rank of a random FSDP case over the default gloo group (see test_random_fsdp_two_processes)."""
+    from test_fuzz_gpu import _FuzzBlock, _FuzzNet
+
+    torch.cuda.set_device(0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=W,
+                            timeout=timedelta(seconds=60))
+    try:
+        c = _random_fsdp_case(seed)
+        dev = torch.device("cuda", 0)
+        blocks = [_FuzzBlock(c["h"], 1000 * seed + k, frozen, empty) for k, (frozen, empty) in enumerate(c["blocks"])]
+        model = _FuzzNet(blocks, c["h"]).to(dev)
+        init = {id(p): p.detach().float().reshape(-1).cpu().numpy().copy() for p in model.parameters()}
+        local: dict[int, torch.Tensor] = {}
+        for p in model.parameters():
+            if p.requires_grad:
+                p.register_post_accumulate_grad_hook(lambda q: local.__setitem__(id(q), q.grad.detach().clone()))
+        policy = MixedPrecisionPolicy(param_dtype=c["param_dtype"], reduce_dtype=torch.float32,
+                                      keep_low_precision_shard=c["keep_low"])
+        fsdp = FSDP(model, unit_types=(_FuzzBlock,), mixed_precision=policy, unit_batch=c["unit_batch"],
+                    reshard_after_forward=c["reshard"], comm_streams=c["comm_streams"])
+        out = {"units": np.array(len(fsdp._units))}
+        with fsdp.summon_full_params():
+            for u, unit in enumerate(fsdp._units):
+                out[f"full_{u}"] = _bits(unit._full)
+        x = torch.randn(6, c["h"], generator=torch.Generator().manual_seed(100 * seed + rank)).to(dev)
+        if c["accumulate"]:
+            with fsdp.no_sync():
+                for half in x.chunk(2):
+                    (fsdp(half) / 2).backward()
+        else:
+            fsdp(x).backward()
+        fsdp.finish_gradient_sync()
+        torch.cuda.synchronize()
+        for u, unit in enumerate(fsdp._units):
+            out[f"numels_{u}"] = np.array(unit.numels, dtype=np.int64)
+            out[f"init_{u}"] = (np.concatenate([init[id(p)] for p in unit.params]) if unit.params
+                                else np.zeros(0, np.float32))
+            for k, p in enumerate(unit.params):
+                if id(p) in local:
+                    out[f"local_{u}_{k}"] = _bits(local[id(p)])
+            out[f"shard_grad_{u}"] = _bits(unit.flat_shard.grad)
+            out[f"sharded_{u}"] = np.array(not unit.is_unsharded and all(p.grad is None for p in unit.params))
+        np.savez(os.path.join(out_dir, f"frand_r{rank}.npz"), **out)
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_fsdp_two_processes(tmp_path, seed):
+    """Seeded random FSDP cases over a real two-process gloo group: 1-5 units of random width (frozen
+    biases, empty parameters) and the root, the gather dtype, ``unit_batch``, ``reshard_after_forward``,
+    ``keep_low_precision_shard``, side streams, accumulation under ``no_sync`` and the flush.  Every
+    unit's gathered parameters against the oracle's cast of rank 0's weights, every rank's shard
+    gradient against the oracle over both ranks' captured gradients (W = 2: order-free), every unit
+    sharded after backward."""
+    c = _random_fsdp_case(seed)
+    print(f"seed {seed}: {c}", flush=True)
+    mp.spawn(_random_fsdp_worker, args=(seed, str(tmp_path / "store"), str(tmp_path)), nprocs=W, join=True)
+    res = []
+    for r in range(W):
+        with np.load(tmp_path / f"frand_r{r}.npz", allow_pickle=False) as d:
+            res.append({k: d[k] for k in d.files})
+    pdt = {torch.bfloat16: o.BF16, torch.float16: o.F16}.get(c["param_dtype"], o.F32)
+    assert int(res[0]["units"]) == len(c["blocks"]) + 1
+    for u in range(int(res[0]["units"])):
+        numels = [int(n) for n in res[0][f"numels_{u}"]]
+        _, _, P = o.fsdp_layout(numels, W)
+        flat = np.zeros(P, np.float32)
+        flat[: sum(numels)] = res[0][f"init_{u}"]
+        gathered = o.fsdp_gather_cast(flat, pdt)
+        grads = [[res[r][f"local_{u}_{k}"] if f"local_{u}_{k}" in res[r] else o.zeros(n, pdt)
+                  for k, n in enumerate(numels)] for r in range(W)]
+        for rank in range(W):
+            where = f"seed {seed} unit {u} rank {rank}"
+            assert bool(res[rank][f"sharded_{u}"]), f"{where}: still gathered after backward"
+            assert same_bits(res[rank][f"full_{u}"], gathered), f"{where}: all-gather"
+            want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, pdt if c["keep_low"] else o.F32)
+            got = res[rank][f"shard_grad_{u}"]
+            assert same_bits(got, want), f"{where}: shard grad: " + first_mismatch(got, want)
