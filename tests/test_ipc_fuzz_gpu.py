@@ -287,3 +287,93 @@ def test_random_ipc_fsdp_matches_oracle(tmp_path, seed):
             want = o.fsdp_reduce_scatter_share(grads, pdt, numels, rank, o.F32, pdt if c["keep_low"] else o.F32)
             got = res[rank][f"shard_grad_{u}"]
             assert same_bits(got, want), f"{case}: unit {u} rank {rank} shard grad: " + first_mismatch(got, want)
+
+
+REDUCE_OPS = {"sum": dist.ReduceOp.SUM, "max": dist.ReduceOp.MAX, "min": dist.ReduceOp.MIN,
+              "product": dist.ReduceOp.PRODUCT}
+ODT = {torch.float32: o.F32, torch.bfloat16: o.BF16, torch.float16: o.F16}
+
+
+def _collectives_case(seed: int) -> dict:
+    """Symmetric buffers, every rank's starting rows and a sequence of in-place collectives on views."""
+    rng = np.random.default_rng(47000 + seed)
+    W = int(rng.integers(2, 5))
+    bufs = [(int(rng.integers(1, 5000)), DTYPES[int(rng.integers(0, 3))]) for _ in range(int(rng.integers(1, 4)))]
+    rows = []  # [rank][buffer] in the oracle's representation
+    for _ in range(W):
+        per = []
+        for n, dt in bufs:
+            v = (rng.standard_normal(n) * (0.01 if dt == torch.float16 else 1.0)).astype(np.float32)
+            v[rng.random(n) < 0.05] = 0.0
+            v[rng.random(n) < 0.05] = -0.0
+            per.append(o.from_f32(v, ODT[dt]))
+        rows.append(per)
+    ops = []
+    for _ in range(int(rng.integers(3, 9))):
+        b = int(rng.integers(0, len(bufs)))
+        n = bufs[b][0]
+        if rng.random() < 0.3 and n >= 4:  # several views of one buffer in one coalesced SUM
+            cuts = sorted(int(x) for x in rng.choice(np.arange(1, n), size=min(n - 1, int(rng.integers(2, 5))),
+                                                      replace=False))
+            spans = [(a, c) for a, c in zip([0, *cuts], [*cuts, n], strict=True)][:: int(rng.integers(1, 3))]
+            ops.append(("coalesced", b, spans, "sum", bool(rng.random() < 0.5)))
+        else:
+            a = int(rng.integers(0, n))
+            c = int(rng.integers(a + 1, n + 1))
+            ops.append(("single", b, [(a, c)], list(REDUCE_OPS)[int(rng.integers(0, 4))], bool(rng.random() < 0.5)))
+    return dict(W=W, algorithm=["one_shot", "two_shot"][seed % 2], bufs=bufs, rows=rows, ops=ops)
+
+
+def _collectives_worker(rank: int, world: int, store: str, out_dir: str, seed: int) -> None:
+    from minidist import comm
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dist.init_process_group("gloo", init_method=f"file://{store}", rank=rank, world_size=world,
+                            timeout=timedelta(seconds=60))
+    try:
+        c = _collectives_case(seed)
+        group = IpcGroup(dist.group.WORLD, dev, algorithm=c["algorithm"])
+        rows = [group.zeros(n, dt) for n, dt in c["bufs"]]
+        for row, host in zip(rows, c["rows"][rank], strict=True):
+            row.copy_(_to_dev(host, row.shape, dev))
+        for kind, b, spans, op, async_op in c["ops"]:
+            views = [rows[b][a:e] for a, e in spans]
+            if kind == "coalesced":
+                work = comm.all_reduce_coalesced(views, group=group, async_op=async_op)
+            else:
+                work = comm.all_reduce(views[0], op=REDUCE_OPS[op], group=group, async_op=async_op)
+            if async_op and work is not None:
+                work.wait()
+        torch.cuda.synchronize()
+        np.savez(os.path.join(out_dir, f"coll_r{rank}.npz"), **{f"buf_{b}": _host_bits(r) for b, r in enumerate(rows)})
+        group.release()
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_ipc_in_place_collectives(tmp_path, seed):
+    """Seeded random sequences of in-place ``comm.all_reduce`` (SUM, MAX, MIN, PRODUCT) and
+    ``comm.all_reduce_coalesced`` (several views of one buffer) on views of 1-3 symmetric fp32 / bf16
+    / fp16 buffers of an IpcGroup with no reduce target, one- or two-shot, synchronous or async:
+    every rank's rows after the sequence against the oracle replaying it (each view replaced, on
+    every rank, by the rank-ordered fold of all ranks' values; everything else kept)."""
+    c = _collectives_case(seed)
+    W = c["W"]
+    print(f"ipc collectives seed {seed}: W={W} {c['algorithm']} buffers={[(n, str(d)) for n, d in c['bufs']]} "
+          f"ops={[(k, b, len(s), op) for k, b, s, op, _ in c['ops']]}", flush=True)
+    mp.spawn(_collectives_worker, args=(W, str(tmp_path / "store"), str(tmp_path), seed), nprocs=W, join=True)
+    want = [[np.array(x, copy=True) for x in per] for per in c["rows"]]
+    for kind, b, spans, op, _ in c["ops"]:
+        dt = ODT[c["bufs"][b][1]]
+        for a, e in spans:
+            parts = [want[r][b][a:e] for r in range(W)]
+            red = o.allreduce_sum(parts, dt) if op == "sum" else o.allreduce_op(parts, dt, op)
+            for r in range(W):
+                want[r][b][a:e] = red
+    for r in range(W):
+        with np.load(tmp_path / f"coll_r{r}.npz", allow_pickle=False) as d:
+            for b in range(len(c["bufs"])):
+                got = d[f"buf_{b}"]
+                assert same_bits(got, want[r][b]), f"seed {seed} rank {r} buffer {b}: " + first_mismatch(got, want[r][b])
