@@ -459,17 +459,25 @@ def bench_ddp(name: str, args) -> dict:
     opt = _Opt()
 
     # Dominant kernel timing: HIP events around the fused W-way reduction
-    # dispatch, recorded on the stream it is launched on.
+    # dispatch, recorded on the stream it is launched on (the caller's: these
+    # workloads use no communication stream).  The stream object and the event
+    # pairs are made before the timed region, so each dispatch adds only its two
+    # event records to the host's work.
     red_events: list = []
-    timing = {"on": False}
+    timing: dict = {"on": False, "stream": None, "pool": []}
     hook_name = "pack_all_reduce_unpack_planned" if fused_pack else "all_reduce_unpack_planned"
     orig = getattr(ResidentGroup, hook_name)
+
+    def event_pair():
+        if timing["pool"]:
+            return timing["pool"].pop()
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def timed_all_reduce(self, *a, **k):
         if not timing["on"]:
             return orig(self, *a, **k)
-        s = torch.cuda.current_stream(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s = timing["stream"]
+        e0, e1 = event_pair()
         e0.record(s)
         work = orig(self, *a, **k)
         e1.record(s)
@@ -495,8 +503,8 @@ def bench_ddp(name: str, args) -> dict:
         """--staged: the W-way sum dispatch, with HIP events like the fused reduction's."""
         if not timing["on"]:
             return staged_sum()
-        s = torch.cuda.current_stream(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s = timing["stream"]
+        e0, e1 = event_pair()
         e0.record(s)
         staged_sum()
         e1.record(s)
@@ -536,6 +544,9 @@ def bench_ddp(name: str, args) -> dict:
     # own stream (two event records per step cost ~0.8% of a cfg1 step).  Every
     # step ends in the scaler's flag read (a host synchronisation), so the host
     # clock between step ends is each step's own time.
+    timing["stream"] = torch.cuda.current_stream(dev)
+    timing["pool"] = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(steps + (min(steps, 50) if args.graphs else 0))]
     with gc_paused():
         timing["on"] = not args.graphs
         t0 = time.perf_counter()

@@ -162,6 +162,24 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+# (device index, raw handle) -> the Stream object torch.cuda.current_stream returned for it
+_stream_objects: dict[tuple[int, int], torch.cuda.Stream] = {}
+
+
+def current_stream(device: torch.device) -> torch.cuda.Stream:
+    """``torch.cuda.current_stream(device)``, found by the stream's raw handle (one C call) among
+    the Stream objects built before: a handle names one stream, and building the object costs
+    ~2 us of host time on the path between a launch and the step's flag read."""
+    if _current_raw_stream is None:
+        return torch.cuda.current_stream(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, _current_raw_stream(index))
+    stream = _stream_objects.get(key)
+    if stream is None:
+        stream = _stream_objects[key] = torch.cuda.current_stream(device)
+    return stream
+
+
 def spans_array(rows: list[tuple[int, int, int]]) -> np.ndarray:
     return np.array(rows, dtype=SPAN_DTYPE)
 

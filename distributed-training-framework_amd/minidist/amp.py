@@ -101,7 +101,7 @@ class _HostFlag:
     def settle(self) -> None:
         """Wait until the kernels that may set the flag (on the current stream, or on streams
         it joined) are done, so that the host load sees their stores."""
-        torch.cuda.current_stream(self.device).synchronize()
+        _native.current_stream(self.device).synchronize()
 
 
 class DistributedGradScaler:
@@ -285,8 +285,10 @@ class DistributedGradScaler:
         groups: dict[torch.dtype, list[tuple[int, int, int]]] = {}
         for group in optimizer.param_groups:
             for p in group["params"]:
+                if id(p) in prescaled:  # unscaled by a producer (a set lookup is cheaper than .grad)
+                    continue
                 g = p.grad
-                if g is None or id(p) in prescaled:
+                if g is None:
                     continue
                 _native.require_device_tensor(g, "gradient")
                 if not g.is_contiguous():

@@ -165,9 +165,16 @@ def shutdown_distributed() -> None:
         dist.destroy_process_group()
 
 
+_cuda_devices: dict[int, torch.device] = {}
+
+
 def current_device() -> torch.device:
-    if torch.cuda.is_available():
-        return torch.device("cuda", torch.cuda.current_device())
+    if torch.cuda.is_initialized() or torch.cuda.is_available():
+        index = torch.cuda.current_device()
+        device = _cuda_devices.get(index)
+        if device is None:
+            device = _cuda_devices[index] = torch.device("cuda", index)
+        return device
     return torch.device("cpu")
 
 
@@ -232,7 +239,7 @@ class StreamWork:
         return self._event
 
     def wait(self, timeout=None) -> bool:  # noqa: ARG002 - mirrors dist.Work.wait
-        current = torch.cuda.current_stream(self._stream.device)
+        current = _native.current_stream(self._stream.device)
         if current != self._stream:
             current.wait_event(self._marker())
         return True
@@ -445,7 +452,7 @@ class ResidentGroup:
         if not tensors:
             return None
         device = tensors[0].device
-        stream = torch.cuda.current_stream(device)
+        stream = _native.current_stream(device)
         groups: dict[int, tuple[_Arena, list[int], list[int]]] = {}
         for t in tensors:
             _native.require_device_tensor(t, "all_reduce input")
@@ -474,7 +481,7 @@ class ResidentGroup:
             return self.all_reduce_sum(tensors, async_op)
         if not tensors:
             return None
-        stream = torch.cuda.current_stream(tensors[0].device)
+        stream = _native.current_stream(tensors[0].device)
         groups: dict[int, tuple[_Arena, list[int], list[int]]] = {}
         for t in tensors:
             _native.require_device_tensor(t, "all_reduce input")
@@ -515,7 +522,7 @@ class ResidentGroup:
         esize = arena.esize
         bases = [b + off * esize for b in arena.row_ptrs]
         out = self._bucket_out(buffer, bucket)
-        stream = torch.cuda.current_stream(buffer.device)
+        stream = _native.current_stream(buffer.device)
         _native.allreduce_unpack(
             bases, _native.dtype_code(arena.dtype), runs, out, _native.dtype_code(grad_dtype),
             _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
@@ -547,7 +554,7 @@ class ResidentGroup:
         if bucket.numel() < wire.numel():
             raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
         bases = [b + off * arena.esize for b in arena.row_ptrs]
-        stream = torch.cuda.current_stream(wire.device)
+        stream = _native.current_stream(wire.device)
         _native.allreduce_unpack_wide(
             bases, _native.dtype_code(arena.dtype), runs, bucket.data_ptr(), _native.dtype_code(bucket.dtype),
             _native.dtype_code(grad_dtype), _native.f32(prescale), _native.f32(inv_scale),
@@ -607,7 +614,7 @@ class ResidentGroup:
             plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
             _native.stream_of(device),
         )
-        return StreamWork(torch.cuda.current_stream(device)) if async_op else None
+        return StreamWork(_native.current_stream(device)) if async_op else None
 
     def pack_all_reduce_unpack(
         self,
@@ -644,7 +651,7 @@ class ResidentGroup:
             _native.require_device_tensor(bucket, "all_reduce output")
             if bucket.numel() < wire.numel():
                 raise ValueError("all_reduce: the bucket is shorter than the contribution rows")
-        stream = torch.cuda.current_stream(wire.device)
+        stream = _native.current_stream(wire.device)
         _native.pack_allreduce_unpack(
             bases, self._rank, _native.dtype_code(arena.dtype), runs,
             None if bucket is None else bucket.data_ptr(), _native.dtype_code(reduce_dtype), _native.f32(scale),
@@ -681,8 +688,8 @@ class ResidentGroup:
             plan, _native.f32(inv_scale), found_inf.data_ptr() if found_inf is not None else None,
             clear_flag.data_ptr() if clear_flag is not None else None, _native.stream_of(device),
         )
-        # the Work's stream object is built after the launch, off the path to the GPU
-        return StreamWork(torch.cuda.current_stream(device)) if async_op else None
+        # the Work's stream object is found after the launch, off the path to the GPU
+        return StreamWork(_native.current_stream(device)) if async_op else None
 
     def reduce_scatter_op(self, output: torch.Tensor, input_: torch.Tensor, op: int, async_op: bool = False):
         """:meth:`reduce_scatter_sum` with the reduction ``op`` (``_native.MDX_OP_*``): this rank's
@@ -698,7 +705,7 @@ class ResidentGroup:
             raise TypeError("reduce_scatter: output and input dtypes differ")
         _native.require_dense(output, "reduce_scatter output")
         lo = self._rank * S * input_.element_size()
-        stream = torch.cuda.current_stream(input_.device)
+        stream = _native.current_stream(input_.device)
         _native.allreduce_op([r + lo for r in rows], _native.dtype_code(input_.dtype), op, [0], [S],
                              output.data_ptr(), stream.cuda_stream)
         return StreamWork(stream) if async_op else None
@@ -717,7 +724,7 @@ class ResidentGroup:
         peers = [r + lo for r in rows]
         own = _native.pieces_array([(peers[self._rank], 0, S)])
         code = _native.dtype_code(input_.dtype)
-        stream = torch.cuda.current_stream(input_.device)
+        stream = _native.current_stream(input_.device)
         _native.reduce_scatter_share(
             own, peers, self._rank, code, code, False, output.data_ptr(), code, False, 1.0, None,
             stream.cuda_stream,
@@ -735,7 +742,7 @@ class ResidentGroup:
         es, base = input_.element_size(), output.data_ptr()
         spans = self._gather_order([(rows[r], base + r * S * es, S) for r in range(self._world)], es)
         code = _native.dtype_code(input_.dtype)
-        stream = torch.cuda.current_stream(input_.device)
+        stream = _native.current_stream(input_.device)
         _native.pack(_native.spans_array(spans), code, code, 1.0, False, stream.cuda_stream)
         return StreamWork(stream) if async_op else None
 
