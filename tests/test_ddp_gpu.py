@@ -854,3 +854,20 @@ def test_mixed_dtype_buckets_bitwise(rng, W, rank, cap, offset):
         assert bucket.buffer.dtype == bucket.params[0].dtype
         assert same_bits(host_bits(bucket.buffer), want["reduced"][b]), f"bucket {b}"
     assert found == want["found_inf"]
+
+
+def test_current_stream_lookup_follows_torch():
+    """The launch path finds the current stream by its raw handle (minidist._native.current_stream):
+    it is the stream torch.cuda.current_stream names, inside and outside stream contexts, for
+    streams made and dropped in turn, and for a device given without an index."""
+    from minidist import _native
+
+    assert _native.current_stream(DEV) == torch.cuda.current_stream(DEV)
+    for _ in range(4):
+        s = torch.cuda.Stream(device=DEV)
+        with torch.cuda.stream(s):
+            got = _native.current_stream(DEV)
+            assert got == s and got.cuda_stream == s.cuda_stream
+            assert _native.current_stream(torch.device("cuda")) == s
+        del s
+        assert _native.current_stream(DEV) == torch.cuda.current_stream(DEV)
