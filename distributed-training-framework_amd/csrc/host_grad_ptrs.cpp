@@ -28,10 +28,17 @@ PyObject* grad_ptrs(PyObject*, PyObject* params) {
       PyErr_SetString(PyExc_TypeError, "grad_ptrs: every element must be a tensor");
       return nullptr;
     }
-    const at::Tensor& g = THPVariable_Unpack(p).grad();
-    const unsigned long long addr = g.defined() ? static_cast<unsigned long long>(
-                                                      reinterpret_cast<uintptr_t>(g.data_ptr()))
-                                                : 0ull;
+    unsigned long long addr = 0;
+    try {
+      // torch's own error (a gradient without storage, e.g. a sparse one) goes back to Python as a
+      // RuntimeError: an exception must not leave this C function
+      const at::Tensor& g = THPVariable_Unpack(p).grad();
+      if (g.defined()) addr = static_cast<unsigned long long>(reinterpret_cast<uintptr_t>(g.data_ptr()));
+    } catch (const std::exception& e) {
+      Py_DECREF(out);
+      PyErr_SetString(PyExc_RuntimeError, e.what());
+      return nullptr;
+    }
     PyObject* v = PyLong_FromUnsignedLongLong(addr);
     if (v == nullptr) {
       Py_DECREF(out);

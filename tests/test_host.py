@@ -859,6 +859,11 @@ def test_host_grad_ptrs_helper_matches_python():
         _hostptrs.grad_ptrs([ps[0], 3])
     with pytest.raises(TypeError):
         _hostptrs.grad_ptrs(tuple(ps))
+    # torch's own error for a gradient without storage comes back as a Python error, as it does from
+    # p.grad.data_ptr(), instead of ending the process
+    ps[2].grad = torch.zeros(3).to_sparse()
+    with pytest.raises(RuntimeError, match="storage"):
+        _hostptrs.grad_ptrs(ps)
 
 
 def test_new_entry_points_check_arguments_before_any_launch():
